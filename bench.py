@@ -1,0 +1,283 @@
+"""Benchmark: fused SE12 decode + GEMV at batch 1 on one MI355X.
+
+Workload (one "step"): every linear of a 26-layer Gemma-2-2B at batch 1 -
+per layer q 2048x2304, k 1024x2304, v 1024x2304, o 2304x2048, gate 9216x2304,
+up 9216x2304, down 2304x9216 - i.e. 182 fused SE12 GEMVs over 3.04 GB of SE12
+streams (2.03 G weights), far beyond the 256 MB Infinity Cache, so every step
+streams from HBM. Weights are BF16 N(0, 0.02) drawn on the device (torch
+generator seeded per layer and projection) and SE12-encoded on the GPU;
+activations are BF16 N(0, 1) seeded per layer. The step is captured once in a
+HIP graph and replayed; the timed region is bracketed by synchronizations and
+HIP events on the replay stream.
+
+Printed JSON (one line on stdout): value = BF16-equivalent weight GB/s of the
+whole step (2 bytes x weights / step time, the reference's convention,
+lws/bench/micro.py:162-165), the per-shape microseconds, the same step through
+hipBLASLt BF16 (torch.nn.functional.linear) and through the raw-BF16 twin
+kernel, a roofline line for the fused GEMV kernel and the oracle's numpy
+decode + matmul timed on the host as the CPU baseline.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+METRIC = "BF16-equiv weight GB/s + us per fused SE12 GEMV at batch 1; decode tok/s"
+HBM_PEAK_GBPS = 8000.0
+LAYERS = 26
+HIDDEN, INTER, QDIM, KVDIM = 2304, 9216, 2048, 1024
+# (name, rows N, cols K, input vector)
+PROJECTIONS = (
+    ("q", QDIM, HIDDEN, "h"),
+    ("k", KVDIM, HIDDEN, "h"),
+    ("v", KVDIM, HIDDEN, "h"),
+    ("o", HIDDEN, QDIM, "a"),
+    ("gate", INTER, HIDDEN, "h"),
+    ("up", INTER, HIDDEN, "h"),
+    ("down", HIDDEN, INTER, "m"),
+)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--layers", type=int, default=LAYERS, help="layers in the stack (26 = Gemma-2-2B)")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-per-shape", action="store_true")
+    p.add_argument("--only-fused", action="store_true", help="skip the BF16 and raw-twin comparisons (profiling)")
+    return p.parse_args(argv)
+
+
+def build_stack(layers: int, device):
+    from se12_amd.hip import Se12MatVecKernel, encode_on_device
+
+    gen = torch.Generator(device=device)
+    stack = []
+    for layer in range(layers):
+        xs = {}
+        for key, dim in (("h", HIDDEN), ("a", QDIM), ("m", INTER)):
+            gen.manual_seed(1_000_000 + layer * 10 + len(xs))
+            xs[key] = torch.randn((1, dim), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+        entries = []
+        for pi, (name, n, k, xin) in enumerate(PROJECTIONS):
+            gen.manual_seed(layer * 100 + pi)
+            w = (torch.randn((n, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+            enc = encode_on_device(w)
+            kern = Se12MatVecKernel(enc, max_batch=1)
+            y = torch.empty((1, n), dtype=torch.float32, device=device)
+            entries.append({"name": name, "n": n, "k": k, "w": w, "enc": enc, "kern": kern, "x": xs[xin], "y": y})
+        stack.append(entries)
+        if layer == 0 or (layer + 1) % 13 == 0:
+            log(f"[bench] layer {layer + 1}/{layers} encoded")
+    return stack
+
+
+def capture(fn):
+    """Captures fn() (a sequence of launches on the current stream) in a graph."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, steps: int, warmup: int, flush=None) -> float:
+    """Mean ms per replay over `steps` replays, events on the replay stream."""
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    if flush is None:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            g.replay()
+        end.record()
+        end.synchronize()
+        return start.elapsed_time(end) / steps
+    total = 0.0
+    for _ in range(steps):
+        flush()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        end.record()
+        end.synchronize()
+        total += start.elapsed_time(end)
+    return total / steps
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    """The oracle's numpy decode + float32 matmul of one 2304x9216 GEMV (the
+    Gemma-2-2B down_proj shape, N(0, 0.02) seed 0) on the host, BLAS limited
+    to one thread; median over repeated runs within the time budget."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import se12_codec as o
+
+    n, k = 2304, 9216
+    bits = o.normal_bf16(n, k, seed=0, std=0.02)
+    enc = o.encode(bits.reshape(-1), n, k)
+    x = o.bf16_bits_to_f32(o.normal_bf16(1, k, seed=1, std=1.0))
+    times = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + budget_s
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
+            t0 = time.perf_counter()
+            o.gemv_reference(enc, x)
+            times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {
+        "value": round(2.0 * n * k / med / 1e9, 4),
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"one 2304x9216 GEMV at batch 1 (numpy decode + float32 matmul, 1 thread), median of {len(times)} runs, {med * 1e3:.1f} ms each",
+    }
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the SE12 path has no multi-GPU mode", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP GPU", file=sys.stderr)
+        return 2
+    from se12_amd import _native
+    from se12_amd.hip import HipGpuProbe, RawBf16MatVecKernel
+
+    _native.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    props = HipGpuProbe(0).properties()
+    log(f"[bench] device {props.name} {props.arch} CUs={props.compute_units}")
+    t0 = time.perf_counter()
+    stack = build_stack(args.layers, dev)
+    torch.cuda.synchronize()
+    log(f"[bench] stack built in {time.perf_counter() - t0:.1f}s")
+
+    flat = [e for layer in stack for e in layer]
+    weights = sum(e["n"] * e["k"] for e in flat)
+    se12_bytes = sum(e["enc"].byte_size() for e in flat)
+    act_bytes = sum(e["k"] * 2 + e["n"] * 4 for e in flat)
+    bf16_bytes = 2 * weights
+
+    def fused_step():
+        for e in flat:
+            e["kern"].multiply(e["x"], out=e["y"])
+
+    g_fused = capture(fused_step)
+    ms = time_graph(g_fused, args.steps, args.warmup)
+    value = bf16_bytes / (ms * 1e-3) / 1e9
+    log(f"[bench] fused step {ms:.3f} ms -> {value:.1f} GB/s BF16-equivalent")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"gemma-2-2b linear stack: {args.layers} layers x 7 projections, batch 1",
+            "gemvs_per_step": len(flat),
+            "weights_per_step": weights,
+            "se12_bytes_per_step": se12_bytes,
+            "bf16_bytes_per_step": bf16_bytes,
+            "batch": 1,
+        },
+    }
+
+    achieved = (se12_bytes + act_bytes) / (ms * 1e-3) / 1e9
+    result["roofline"] = {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBPS, 4),
+        "traffic": None,
+        "kernel": "se12::gemv_kernel<1,bf16,se12>",
+        "avg_launch_us": round(ms * 1e3 / len(flat), 3),
+        "algorithmic_bytes_per_launch": round((se12_bytes + act_bytes) / len(flat)),
+    }
+
+    if not args.only_fused:
+        def bf16_step():
+            for e in flat:
+                torch.nn.functional.linear(e["x"], e["w"])
+
+        g_bf16 = capture(bf16_step)
+        ms_bf16 = time_graph(g_bf16, args.steps, args.warmup)
+        raw = [RawBf16MatVecKernel(e["w"], max_batch=1) for e in flat]
+
+        def raw_step():
+            for e, r in zip(flat, raw):
+                r.multiply(e["x"], out=e["y"])
+
+        g_raw = capture(raw_step)
+        ms_raw = time_graph(g_raw, args.steps, args.warmup)
+        result["bf16_hipblaslt"] = {"ms_per_step": round(ms_bf16, 4), "gbps": round(bf16_bytes / (ms_bf16 * 1e-3) / 1e9, 1),
+                                   "speedup_of_se12": round(ms_bf16 / ms, 4)}
+        result["raw_bf16_twin"] = {"ms_per_step": round(ms_raw, 4), "gbps": round(bf16_bytes / (ms_raw * 1e-3) / 1e9, 1),
+                                  "speedup_of_se12": round(ms_raw / ms, 4)}
+        log(f"[bench] hipBLASLt bf16 {ms_bf16:.3f} ms, raw twin {ms_raw:.3f} ms")
+        del g_raw, raw
+
+    if not args.no_per_shape:
+        flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB > 2 x (L2 + MALL)
+
+        def flush():
+            flush_buf.fill_(1.0)
+
+        per_shape = {}
+        for pi, (name, n, k, _) in enumerate(PROJECTIONS):
+            col = [layer[pi] for layer in stack]
+            g = capture(lambda col=col: [e["kern"].multiply(e["x"], out=e["y"]) for e in col])
+            ms_s = time_graph(g, 10, 3, flush=flush)
+            us = ms_s * 1e3 / len(col)
+            per_shape[name] = {"shape": [n, k], "us": round(us, 3), "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
+                               "se12_gbps": round(col[0]["enc"].byte_size() / (us * 1e-6) / 1e9, 1)}
+            if not args.only_fused:
+                gb = capture(lambda col=col: [torch.nn.functional.linear(e["x"], e["w"]) for e in col])
+                us_b = time_graph(gb, 10, 3, flush=flush) * 1e3 / len(col)
+                per_shape[name]["bf16_hipblaslt_us"] = round(us_b, 3)
+            log(f"[bench] {name} {n}x{k}: {per_shape[name]}")
+        result["per_shape"] = per_shape
+        del flush_buf
+
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

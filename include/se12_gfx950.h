@@ -1,0 +1,184 @@
+/*
+ * se12_gfx950.h - C ABI of the MI355X (gfx950) SE12 decode + GEMV library.
+ *
+ * SE12 stores a BF16 matrix [rows, cols] as 16x256 tiles (tile-major,
+ * tile t = tile_row * tile_cols + tile_col, in-tile index = local_row*256 +
+ * local_col), each tile as 4096 sign|mantissa bytes (`sm`), 2048 bytes of
+ * 4-bit exponent codes (`ec`, even index in the low nibble), 16 escape slots
+ * (`esc`), plus one bitmap bit per tile (MSB first) marking tiles kept raw in
+ * `fallback_raw`, and a 15-entry exponent codebook. The layout is the one the
+ * reference encoder writes (lws/domain/se12/codec.py:111-141) and its packer
+ * stores (lws/adapters/safetensors/packed_store.py:70-107).
+ *
+ * Conventions: every pointer named *_dev is device memory owned by the caller
+ * (e.g. a torch tensor); streams are hipStream_t passed as void*; every entry
+ * point returns 0 on success or a negative SE12_E* code, and se12_last_error()
+ * gives the message of the calling thread's last failure. No entry point that
+ * launches work synchronizes the stream unless its comment says so.
+ */
+#ifndef SE12_GFX950_H
+#define SE12_GFX950_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SE12_TILE_ROWS 16
+#define SE12_TILE_COLS 256
+#define SE12_TILE_SIZE 4096
+#define SE12_ESCAPE_BUDGET 16
+#define SE12_CODEBOOK_SIZE 15
+#define SE12_ESCAPE_CODE 15
+#define SE12_MAX_BATCH 32
+
+/* status codes */
+#define SE12_OK 0
+#define SE12_E_INVALID (-1)   /* bad argument (null pointer, shape, size) */
+#define SE12_E_HIP (-2)       /* a HIP runtime call failed */
+#define SE12_E_CAPACITY (-3)  /* an output or workspace is too small */
+#define SE12_E_DEVICE (-4)    /* wrong or unsupported device */
+
+/* activation element types */
+#define SE12_X_BF16 0
+#define SE12_X_F32 1
+
+/* weight formats a handle can be bound to */
+#define SE12_FORMAT_SE12 0
+#define SE12_FORMAT_RAW_BF16 1
+
+/* The five SE12 streams and the codebook, as device pointers. */
+typedef struct se12_streams {
+    const uint8_t* sm_dev;              /* [tiles * 4096] */
+    const uint8_t* ec_dev;              /* [tiles * 2048] */
+    const uint8_t* esc_dev;             /* [tiles * 16] */
+    const uint8_t* codebook_dev;        /* [15] */
+    const uint8_t* fallback_bitmap_dev; /* [ceil(tiles / 8)] */
+    const int16_t* fallback_raw_dev;    /* [fallback_tiles * 4096], may be NULL when empty */
+    int64_t fallback_raw_elems;         /* element count of fallback_raw (checked at bind) */
+} se12_streams;
+
+/* Writable streams for the encoder. */
+typedef struct se12_streams_out {
+    uint8_t* sm_dev;
+    uint8_t* ec_dev;
+    uint8_t* esc_dev;
+    uint8_t* fallback_bitmap_dev;
+    int16_t* fallback_raw_dev;          /* capacity: fallback_raw_tiles tiles */
+    int64_t fallback_raw_tiles;
+} se12_streams_out;
+
+/* Launch shape of the GEMV: `threads_per_block` = 64 * waves per workgroup
+ * (64..1024), `blocks` = tile_rows * k_splits, k_splits dividing the K tiles
+ * into equal contiguous ranges. Mirrors the reference LaunchConfiguration
+ * (lws/domain/launch/heuristic.py:40-43) re-derived for wave64. */
+typedef struct se12_launch {
+    int32_t threads_per_block;
+    int32_t blocks;
+} se12_launch;
+
+typedef struct se12_device_info {
+    char name[256];
+    char arch[64];              /* e.g. "gfx950:sramecc+:xnack-" */
+    int32_t compute_units;
+    int32_t wavefront_size;
+    int64_t l2_bytes;
+    int64_t lds_bytes_per_cu;
+    int64_t lds_bytes_per_block;
+    int64_t total_memory_bytes;
+    int32_t clock_khz;
+    int32_t memory_clock_khz;
+    int32_t memory_bus_width_bits;
+    int32_t max_threads_per_block;
+} se12_device_info;
+
+typedef struct se12_handle se12_handle;
+
+/* Thread-local message of the last failed call ("" if none). */
+const char* se12_last_error(void);
+
+/* Library build string (arch, compiler). Host only, never touches the GPU. */
+const char* se12_version(void);
+
+/* Device facts from hipDeviceProp_t. Replaces CudaGpuProbe.properties
+ * (lws/adapters/cuda/gpu_probe.py:59-80). */
+int se12_device_info_get(int32_t device, se12_device_info* out);
+
+/* Binds a weight matrix already resident on the current device: validates the
+ * streams' sizes, builds the per-tile fallback-rank sidecar (the reference's
+ * host-side fallback_offsets, lws/adapters/cuda/gemv.py:47-53) on the GPU and
+ * allocates the split-K workspace for batches up to `max_batch`.
+ * Synchronizes `stream`. Replaces Se12MatVecKernel.__init__ and
+ * _upload_se12_streams (lws/adapters/cuda/gemv.py:183-194,229-264); the
+ * caller keeps ownership of the streams, which must outlive the handle. */
+int se12_bind(const se12_streams* streams, int64_t rows, int64_t cols, int32_t max_batch,
+              void* stream, se12_handle** out);
+
+/* Binds a row-major BF16 matrix [rows, cols] for the same-skeleton raw twin.
+ * Replaces RawBf16MatVecKernel.__init__ (lws/adapters/cuda/gemv.py:146-155). */
+int se12_bind_raw_bf16(const uint16_t* w_dev, int64_t rows, int64_t cols, int32_t max_batch,
+                       void* stream, se12_handle** out);
+
+/* Frees the handle's sidecar and workspace (synchronizes its device). */
+int se12_release(se12_handle* h);
+
+/* Shape facts of a bound handle (host only). */
+int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_t* tiles,
+                      int64_t* fallback_tiles, int32_t* format);
+
+/* The default launch for `batch` (the heuristic of
+ * lws/domain/launch/heuristic.py:46-87 re-derived for 256 CUs of wave64). */
+int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out);
+
+/* y[b, n] = sum_k W[n, k] * x[b, k] for b < batch (1..32), FP32 accumulate.
+ * x: [batch, cols] row-major, BF16 or FP32 (`x_dtype`); y: FP32 [batch, rows].
+ * `launch` NULL selects the default. No allocation and no synchronization,
+ * so it can be captured in a HIP graph. Calls on one handle must be ordered
+ * on one stream (they share the handle's split-K workspace).
+ * Replaces the lws_gemv_se12 / lws_gemv_raw_bf16 launches of
+ * MatVecKernel.multiply (lws/adapters/cuda/gemv.py:157-172,196-226;
+ * kernels: lws/adapters/cuda/kernels/gemv_se12.cu:50-64,
+ * gemv_raw_bf16.cu:18-25). */
+int se12_gemv(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch, float* y_dev,
+              const se12_launch* launch, void* stream);
+
+/* Decodes the whole matrix to row-major BF16 bits [rows, cols] (cropped).
+ * Replaces the lws_se12_decode launch plus the device untile/crop of
+ * CudaSe12WeightDecoder (lws/adapters/cuda/se12_decoder.py:58-76,147-185;
+ * kernel lws/adapters/cuda/kernels/se12_decode.cu:12-22). */
+int se12_decode(se12_handle* h, uint16_t* out_dev, void* stream);
+
+/* Decodes `nrows` rows given by device int64 indices, in that order, to
+ * [nrows, cols] BF16 bits; only the tiles covering those rows are read. An
+ * index outside [0, rows) yields a row of zeros. Replaces
+ * WeightDecoder.decode_rows (lws/application/ports/gpu/weight_decoder.py:30-33,
+ * lws/adapters/cuda/se12_decoder.py:64-70). */
+int se12_decode_rows(se12_handle* h, const int64_t* rows_dev, int64_t nrows, uint16_t* out_dev,
+                     void* stream);
+
+/* Host-only: the 15-entry codebook from a 256-bin exponent histogram of the
+ * real weights: descending count, equal counts to the larger exponent value,
+ * zero-count values last (lws/domain/se12/codebook.py:41-59). */
+int se12_codebook_from_histogram(const uint64_t counts[256], uint8_t codebook_out[15]);
+
+/* Encoder pass 1 on the GPU: exponent histogram of w [rows, cols] (row-major
+ * BF16 bits, row stride `ld` elements), codebook, and the number of tiles that
+ * exceed the escape budget. Synchronizes `stream`. Together with se12_encode
+ * this replaces encode_tensor (lws/domain/se12/codec.py:111-141) for the
+ * packer (lws/application/codec/pack_model.py:113-120). */
+int se12_encode_prepare(const uint16_t* w_dev, int64_t rows, int64_t cols, int64_t ld,
+                        uint8_t codebook_out[15], int64_t* fallback_tiles_out, void* stream);
+
+/* Encoder pass 2: writes every stream for `codebook` (from pass 1). Fails with
+ * SE12_E_CAPACITY when out->fallback_raw_tiles is smaller than needed.
+ * Synchronizes `stream`. */
+int se12_encode(const uint16_t* w_dev, int64_t rows, int64_t cols, int64_t ld,
+                const uint8_t codebook[15], const se12_streams_out* out, int64_t* fallback_tiles_out,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SE12_GFX950_H */

@@ -1,0 +1,498 @@
+// C ABI of libse12_gfx950.so: handle management, argument validation, the
+// default launch heuristic and the encoder orchestration. Kernels live in
+// se12_gemv.hip, se12_decode.hip and se12_encode.hip.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "se12_gfx950.h"
+#include "se12_internal.hpp"
+
+using namespace se12;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+#define SE12_HIP(call)                                                                        \
+    do {                                                                                      \
+        hipError_t e_ = (call);                                                               \
+        if (e_ != hipSuccess) return fail(SE12_E_HIP, "%s: %s", #call, hipGetErrorString(e_)); \
+    } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Restores the caller's current device on scope exit.
+struct DeviceScope {
+    int prev = -1;
+    bool changed = false;
+    hipError_t enter(int dev) {
+        hipError_t e = hipGetDevice(&prev);
+        if (e != hipSuccess) return e;
+        if (prev != dev) {
+            changed = true;
+            return hipSetDevice(dev);
+        }
+        return hipSuccess;
+    }
+    ~DeviceScope() {
+        if (changed) (void)hipSetDevice(prev);
+    }
+};
+
+constexpr int32_t kMaxSplits = 64;
+constexpr size_t kLdsBudget = 64 * 1024;  // per block, leaves room for 2+ blocks per CU
+
+}  // namespace
+
+struct se12_handle {
+    int32_t format;
+    int32_t device;
+    int64_t N, K, Np, T;
+    int32_t TR, TC;
+    se12_streams s;
+    const uint16_t* wraw;
+    int32_t* fb_rank;
+    int64_t n_fallback;
+    float* partial;
+    int32_t* counters;
+    int32_t max_batch;
+    int32_t s_cap;
+    int32_t cu_count;
+    int64_t lds_per_block;
+    int32_t codebook0;  // first codebook entry: the exponent every padding weight decodes to
+};
+
+extern "C" {
+
+const char* se12_last_error(void) { return g_last_error.c_str(); }
+
+const char* se12_version(void) {
+    return "se12_gfx950 1 (gfx950, wave64, dot2-bf16 fused decode+GEMV, " __VERSION__ ")";
+}
+
+int se12_device_info_get(int32_t device, se12_device_info* out) {
+    if (!out) return fail(SE12_E_INVALID, "se12_device_info_get: out is NULL");
+    hipDeviceProp_t p;
+    SE12_HIP(hipGetDeviceProperties(&p, device));
+    std::memset(out, 0, sizeof *out);
+    std::snprintf(out->name, sizeof out->name, "%s", p.name);
+    std::snprintf(out->arch, sizeof out->arch, "%s", p.gcnArchName);
+    out->compute_units = p.multiProcessorCount;
+    out->wavefront_size = p.warpSize;
+    out->l2_bytes = p.l2CacheSize;
+    out->lds_bytes_per_cu = (int64_t)p.maxSharedMemoryPerMultiProcessor;
+    out->lds_bytes_per_block = (int64_t)p.sharedMemPerBlock;
+    out->total_memory_bytes = (int64_t)p.totalGlobalMem;
+    out->clock_khz = p.clockRate;
+    out->memory_clock_khz = p.memoryClockRate;
+    out->memory_bus_width_bits = p.memoryBusWidth;
+    out->max_threads_per_block = p.maxThreadsPerBlock;
+    return SE12_OK;
+}
+
+static int bind_common(se12_handle* h, int64_t rows, int64_t cols, int32_t max_batch) {
+    h->N = rows;
+    h->K = cols;
+    h->TR = (int32_t)ceil_div(rows, SE12_TILE_ROWS);
+    h->TC = (int32_t)ceil_div(cols, SE12_TILE_COLS);
+    h->Np = (int64_t)h->TR * SE12_TILE_ROWS;
+    h->T = (int64_t)h->TR * h->TC;
+    h->max_batch = max_batch;
+    h->s_cap = std::min<int32_t>(h->TC, kMaxSplits);
+    SE12_HIP(hipGetDevice(&h->device));
+    hipDeviceProp_t p;
+    SE12_HIP(hipGetDeviceProperties(&p, h->device));
+    h->cu_count = p.multiProcessorCount;
+    h->lds_per_block = (int64_t)p.sharedMemPerBlock;
+    const int32_t b_launch = std::min<int32_t>(max_batch, kGemvMaxBatchPerLaunch);
+    if (h->s_cap > 1) {
+        const size_t pe = (size_t)h->s_cap * b_launch * h->Np;
+        SE12_HIP(hipMalloc(&h->partial, pe * sizeof(float)));
+        SE12_HIP(hipMalloc(&h->counters, (size_t)h->TR * sizeof(int32_t)));
+        SE12_HIP(hipMemset(h->counters, 0, (size_t)h->TR * sizeof(int32_t)));
+    }
+    return SE12_OK;
+}
+
+static void free_handle(se12_handle* h) {
+    if (!h) return;
+    if (h->fb_rank) (void)hipFree(h->fb_rank);
+    if (h->partial) (void)hipFree(h->partial);
+    if (h->counters) (void)hipFree(h->counters);
+    delete h;
+}
+
+static int check_shape(int64_t rows, int64_t cols, int32_t max_batch) {
+    if (rows <= 0 || cols <= 0) return fail(SE12_E_INVALID, "shape must be positive, got [%lld, %lld]", (long long)rows, (long long)cols);
+    if (ceil_div(rows, SE12_TILE_ROWS) > INT32_MAX / 2 || ceil_div(cols, SE12_TILE_COLS) > INT32_MAX / 2)
+        return fail(SE12_E_INVALID, "shape too large");
+    if (max_batch < 1 || max_batch > SE12_MAX_BATCH)
+        return fail(SE12_E_INVALID, "max_batch must be in [1, %d], got %d", SE12_MAX_BATCH, max_batch);
+    return SE12_OK;
+}
+
+int se12_bind(const se12_streams* s, int64_t rows, int64_t cols, int32_t max_batch, void* stream,
+              se12_handle** out) {
+    if (!s || !out) return fail(SE12_E_INVALID, "se12_bind: NULL argument");
+    *out = nullptr;
+    if (int rc = check_shape(rows, cols, max_batch)) return rc;
+    if (!s->sm_dev || !s->ec_dev || !s->esc_dev || !s->codebook_dev || !s->fallback_bitmap_dev)
+        return fail(SE12_E_INVALID, "se12_bind: a required stream pointer is NULL");
+    if (!aligned16(s->sm_dev) || !aligned16(s->ec_dev) || !aligned16(s->esc_dev) ||
+        (s->fallback_raw_dev && !aligned16(s->fallback_raw_dev)))
+        return fail(SE12_E_INVALID, "se12_bind: sm/ec/esc/fallback_raw must be 16-byte aligned");
+    if (s->fallback_raw_elems < 0 || s->fallback_raw_elems % SE12_TILE_SIZE != 0)
+        return fail(SE12_E_INVALID, "se12_bind: fallback_raw has %lld elements, not a whole number of tiles",
+                    (long long)s->fallback_raw_elems);
+    if (s->fallback_raw_elems > 0 && !s->fallback_raw_dev)
+        return fail(SE12_E_INVALID, "se12_bind: fallback_raw is NULL but has elements");
+    se12_handle* h = new se12_handle();
+    std::memset(h, 0, sizeof *h);
+    h->format = SE12_FORMAT_SE12;
+    h->s = *s;
+    if (int rc = bind_common(h, rows, cols, max_batch)) {
+        free_handle(h);
+        return rc;
+    }
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int64_t* total_dev = nullptr;
+    hipError_t e = hipMalloc(&h->fb_rank, (size_t)h->T * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&total_dev, sizeof(int64_t));
+    if (e == hipSuccess) e = launch_fallback_rank_from_bitmap(s->fallback_bitmap_dev, h->T, h->fb_rank, total_dev, st);
+    int64_t total = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&total, total_dev, sizeof total, hipMemcpyDeviceToHost, st);
+    uint8_t cb0 = 0;
+    if (e == hipSuccess) e = hipMemcpyAsync(&cb0, s->codebook_dev, 1, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    h->codebook0 = cb0;
+    if (total_dev) (void)hipFree(total_dev);
+    if (e != hipSuccess) {
+        free_handle(h);
+        return fail(SE12_E_HIP, "se12_bind: %s", hipGetErrorString(e));
+    }
+    if (total * SE12_TILE_SIZE != s->fallback_raw_elems) {
+        free_handle(h);
+        return fail(SE12_E_INVALID, "se12_bind: bitmap marks %lld fallback tiles but fallback_raw holds %lld elements",
+                    (long long)total, (long long)s->fallback_raw_elems);
+    }
+    h->n_fallback = total;
+    *out = h;
+    return SE12_OK;
+}
+
+int se12_bind_raw_bf16(const uint16_t* w, int64_t rows, int64_t cols, int32_t max_batch, void* stream,
+                       se12_handle** out) {
+    (void)stream;
+    if (!w || !out) return fail(SE12_E_INVALID, "se12_bind_raw_bf16: NULL argument");
+    *out = nullptr;
+    if (int rc = check_shape(rows, cols, max_batch)) return rc;
+    se12_handle* h = new se12_handle();
+    std::memset(h, 0, sizeof *h);
+    h->format = SE12_FORMAT_RAW_BF16;
+    h->wraw = w;
+    if (int rc = bind_common(h, rows, cols, max_batch)) {
+        free_handle(h);
+        return rc;
+    }
+    *out = h;
+    return SE12_OK;
+}
+
+int se12_release(se12_handle* h) {
+    if (!h) return SE12_OK;
+    DeviceScope ds;
+    if (ds.enter(h->device) == hipSuccess) (void)hipDeviceSynchronize();
+    free_handle(h);
+    return SE12_OK;
+}
+
+int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_t* tiles, int64_t* fallback_tiles,
+                      int32_t* format) {
+    if (!h) return fail(SE12_E_INVALID, "se12_handle_shape: NULL handle");
+    if (rows) *rows = h->N;
+    if (cols) *cols = h->K;
+    if (tiles) *tiles = h->T;
+    if (fallback_tiles) *fallback_tiles = h->n_fallback;
+    if (format) *format = h->format;
+    return SE12_OK;
+}
+
+// The default launch, re-derived for MI355X: 4 waves per block (fewer when
+// a tile row has fewer K tiles), and enough K splits that the grid holds
+// about 8 waves per CU, each wave keeping >= 1 tile; more splits when the
+// block's slice of x would not fit the LDS budget.
+static void default_launch(const se12_handle* h, int32_t batch, bool xf32, int32_t* waves_out, int32_t* splits_out) {
+    const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
+    const int32_t waves = std::max<int32_t>(1, std::min<int32_t>(4, h->TC));
+    const int64_t target_waves = (int64_t)h->cu_count * 8;
+    int64_t splits = ceil_div(target_waves, (int64_t)h->TR * waves);
+    splits = std::min<int64_t>(splits, std::max<int64_t>(1, h->TC / waves));
+    splits = std::max<int64_t>(splits, 1);
+    while (splits < h->s_cap &&
+           gemv_lds_bytes(waves, bl, (int)ceil_div(h->TC, splits) * SE12_TILE_COLS, xf32) > kLdsBudget)
+        ++splits;
+    splits = std::min<int64_t>(splits, h->s_cap);
+    *waves_out = waves;
+    *splits_out = (int32_t)splits;
+}
+
+int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
+    if (!h || !out) return fail(SE12_E_INVALID, "se12_default_launch: NULL argument");
+    if (batch < 1 || batch > SE12_MAX_BATCH) return fail(SE12_E_INVALID, "batch must be in [1, %d]", SE12_MAX_BATCH);
+    int32_t waves, splits;
+    default_launch(h, batch, false, &waves, &splits);
+    out->threads_per_block = waves * 64;
+    out->blocks = h->TR * splits;
+    return SE12_OK;
+}
+
+int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, const se12_launch* launch,
+              void* stream) {
+    if (!h) return fail(SE12_E_INVALID, "se12_gemv: NULL handle");
+    if (!x || !y) return fail(SE12_E_INVALID, "se12_gemv: NULL x or y");
+    if (x_dtype != SE12_X_BF16 && x_dtype != SE12_X_F32) return fail(SE12_E_INVALID, "se12_gemv: unknown x_dtype %d", x_dtype);
+    if (batch < 1 || batch > h->max_batch)
+        return fail(SE12_E_INVALID, "se12_gemv: batch %d outside [1, %d] (the handle's max_batch)", batch, h->max_batch);
+    const bool xf32 = x_dtype == SE12_X_F32;
+    int32_t waves, splits;
+    if (launch) {
+        if (launch->threads_per_block < 64 || launch->threads_per_block > kGemvMaxThreads ||
+            launch->threads_per_block % 64 != 0)
+            return fail(SE12_E_INVALID, "se12_gemv: threads_per_block %d must be a multiple of 64 in [64, %d]",
+                        launch->threads_per_block, kGemvMaxThreads);
+        if (launch->blocks <= 0 || launch->blocks % h->TR != 0)
+            return fail(SE12_E_INVALID, "se12_gemv: blocks %d must be a positive multiple of the %d tile rows",
+                        launch->blocks, h->TR);
+        waves = launch->threads_per_block / 64;
+        splits = launch->blocks / h->TR;
+        if (splits > h->s_cap)
+            return fail(SE12_E_CAPACITY, "se12_gemv: %d K splits exceed the handle's limit %d", splits, h->s_cap);
+    } else {
+        default_launch(h, batch, xf32, &waves, &splits);
+    }
+    DeviceScope ds;
+    SE12_HIP(ds.enter(h->device));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t xstride = ceil_div(h->TC, splits) * SE12_TILE_COLS;
+    const size_t esize = xf32 ? 4 : 2;
+    for (int32_t b0 = 0; b0 < batch; b0 += kGemvMaxBatchPerLaunch) {
+        const int32_t bl = std::min<int32_t>(kGemvMaxBatchPerLaunch, batch - b0);
+        const size_t lds = gemv_lds_bytes(waves, bl, (int)xstride, xf32);
+        if ((int64_t)lds > h->lds_per_block)
+            return fail(SE12_E_CAPACITY, "se12_gemv: launch needs %zu bytes of LDS, the device allows %lld", lds,
+                        (long long)h->lds_per_block);
+        GemvArgs a{};
+        a.sm = h->s.sm_dev;
+        a.ec = h->s.ec_dev;
+        a.esc = h->s.esc_dev;
+        a.codebook = h->s.codebook_dev;
+        a.fb_rank = h->fb_rank;
+        a.fb_raw = h->s.fallback_raw_dev;
+        a.wraw = h->wraw;
+        a.mask_tail = (h->K % SE12_TILE_COLS != 0 && h->codebook0 == 255) ? 1 : 0;
+        a.x = static_cast<const char*>(x) + (size_t)b0 * h->K * esize;
+        a.y = y + (size_t)b0 * h->N;
+        a.partial = h->partial;
+        a.counters = h->counters;
+        a.N = h->N;
+        a.K = h->K;
+        a.Np = h->Np;
+        a.TR = h->TR;
+        a.TC = h->TC;
+        a.S = splits;
+        a.xstride = (int32_t)xstride;
+        a.x_vec_ok = (aligned16(a.x) && (xf32 ? h->K % 4 == 0 : h->K % 8 == 0)) ? 1 : 0;
+        a.w_vec_ok = (h->wraw && aligned16(h->wraw) && h->K % 8 == 0) ? 1 : 0;
+        hipError_t e = launch_gemv(a, bl, xf32, h->format == SE12_FORMAT_RAW_BF16, waves * 64, h->TR * splits, lds, st);
+        if (e != hipSuccess) return fail(SE12_E_HIP, "se12_gemv launch: %s", hipGetErrorString(e));
+    }
+    return SE12_OK;
+}
+
+static DecodeArgs decode_args(const se12_handle* h, uint16_t* out) {
+    DecodeArgs a{};
+    a.sm = h->s.sm_dev;
+    a.ec = h->s.ec_dev;
+    a.esc = h->s.esc_dev;
+    a.codebook = h->s.codebook_dev;
+    a.bitmap = h->s.fallback_bitmap_dev;
+    a.fb_rank = h->fb_rank;
+    a.fb_raw = h->s.fallback_raw_dev;
+    a.out = out;
+    a.N = h->N;
+    a.K = h->K;
+    a.T = h->T;
+    a.TR = h->TR;
+    a.TC = h->TC;
+    a.out_vec_ok = (aligned16(out) && h->K % 8 == 0) ? 1 : 0;
+    return a;
+}
+
+int se12_decode(se12_handle* h, uint16_t* out, void* stream) {
+    if (!h || !out) return fail(SE12_E_INVALID, "se12_decode: NULL argument");
+    if (h->format != SE12_FORMAT_SE12) return fail(SE12_E_INVALID, "se12_decode: handle is not SE12");
+    DeviceScope ds;
+    SE12_HIP(ds.enter(h->device));
+    DecodeArgs a = decode_args(h, out);
+    a.items = h->T;
+    hipError_t e = launch_decode(a, false, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SE12_E_HIP, "se12_decode launch: %s", hipGetErrorString(e));
+    return SE12_OK;
+}
+
+int se12_decode_rows(se12_handle* h, const int64_t* rows, int64_t nrows, uint16_t* out, void* stream) {
+    if (!h) return fail(SE12_E_INVALID, "se12_decode_rows: NULL handle");
+    if (h->format != SE12_FORMAT_SE12) return fail(SE12_E_INVALID, "se12_decode_rows: handle is not SE12");
+    if (nrows < 0) return fail(SE12_E_INVALID, "se12_decode_rows: negative row count");
+    if (nrows == 0) return SE12_OK;
+    if (!rows || !out) return fail(SE12_E_INVALID, "se12_decode_rows: NULL rows or out");
+    DeviceScope ds;
+    SE12_HIP(ds.enter(h->device));
+    DecodeArgs a = decode_args(h, out);
+    a.rows = rows;
+    a.nrows = nrows;
+    a.items = nrows * h->TC;
+    hipError_t e = launch_decode(a, true, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(SE12_E_HIP, "se12_decode_rows launch: %s", hipGetErrorString(e));
+    return SE12_OK;
+}
+
+int se12_codebook_from_histogram(const uint64_t counts[256], uint8_t codebook_out[15]) {
+    if (!counts || !codebook_out) return fail(SE12_E_INVALID, "se12_codebook_from_histogram: NULL argument");
+    int order[256];
+    for (int i = 0; i < 256; ++i) order[i] = i;
+    std::stable_sort(order, order + 256, [&](int a, int b) {
+        if (counts[a] != counts[b]) return counts[a] > counts[b];
+        return a > b;
+    });
+    for (int i = 0; i < SE12_CODEBOOK_SIZE; ++i) codebook_out[i] = (uint8_t)order[i];
+    return SE12_OK;
+}
+
+static int encode_args(EncodeArgs& a, const uint16_t* w, int64_t rows, int64_t cols, int64_t ld) {
+    if (!w) return fail(SE12_E_INVALID, "encode: NULL weights");
+    if (rows <= 0 || cols <= 0 || ld < cols) return fail(SE12_E_INVALID, "encode: bad shape [%lld, %lld] ld %lld",
+                                                         (long long)rows, (long long)cols, (long long)ld);
+    a = EncodeArgs{};
+    a.w = w;
+    a.N = rows;
+    a.K = cols;
+    a.ld = ld;
+    a.TR = (int32_t)ceil_div(rows, SE12_TILE_ROWS);
+    a.TC = (int32_t)ceil_div(cols, SE12_TILE_COLS);
+    a.T = (int64_t)a.TR * a.TC;
+    a.w_vec_ok = (aligned16(w) && ld % 8 == 0) ? 1 : 0;
+    return SE12_OK;
+}
+
+static void pack_codebook(EncodeArgs& a, const uint8_t cb[15]) {
+    uint8_t b[16] = {0};
+    std::memcpy(b, cb, 15);
+    std::memcpy(a.codebook, b, 16);
+}
+
+int se12_encode_prepare(const uint16_t* w, int64_t rows, int64_t cols, int64_t ld, uint8_t codebook_out[15],
+                        int64_t* fallback_tiles_out, void* stream) {
+    if (!codebook_out || !fallback_tiles_out) return fail(SE12_E_INVALID, "se12_encode_prepare: NULL output");
+    EncodeArgs a;
+    if (int rc = encode_args(a, w, rows, cols, ld)) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    uint64_t* hist = nullptr;
+    int32_t* counts = nullptr;
+    SE12_HIP(hipMalloc(&hist, 256 * sizeof(uint64_t)));
+    hipError_t e = hipMalloc(&counts, (size_t)a.T * sizeof(int32_t));
+    uint64_t hh[256];
+    std::vector<int32_t> ch((size_t)a.T);
+    if (e == hipSuccess) e = hipMemsetAsync(hist, 0, 256 * sizeof(uint64_t), st);
+    a.histogram = hist;
+    a.tile_escapes = counts;
+    if (e == hipSuccess) e = launch_encode_histogram(a, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(hh, hist, sizeof hh, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) {
+        se12_codebook_from_histogram(hh, codebook_out);
+        pack_codebook(a, codebook_out);
+        e = launch_encode_count(a, st);
+    }
+    if (e == hipSuccess) e = hipMemcpyAsync(ch.data(), counts, (size_t)a.T * sizeof(int32_t), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(hist);
+    if (counts) (void)hipFree(counts);
+    if (e != hipSuccess) return fail(SE12_E_HIP, "se12_encode_prepare: %s", hipGetErrorString(e));
+    int64_t nfb = 0;
+    for (int32_t c : ch) nfb += c > SE12_ESCAPE_BUDGET ? 1 : 0;
+    *fallback_tiles_out = nfb;
+    return SE12_OK;
+}
+
+int se12_encode(const uint16_t* w, int64_t rows, int64_t cols, int64_t ld, const uint8_t codebook[15],
+                const se12_streams_out* out, int64_t* fallback_tiles_out, void* stream) {
+    if (!codebook || !out) return fail(SE12_E_INVALID, "se12_encode: NULL argument");
+    EncodeArgs a;
+    if (int rc = encode_args(a, w, rows, cols, ld)) return rc;
+    if (!out->sm_dev || !out->ec_dev || !out->esc_dev || !out->fallback_bitmap_dev)
+        return fail(SE12_E_INVALID, "se12_encode: a required output stream is NULL");
+    if (!aligned16(out->sm_dev) || !aligned16(out->ec_dev) ||
+        (out->fallback_raw_dev && !aligned16(out->fallback_raw_dev)))
+        return fail(SE12_E_INVALID, "se12_encode: sm/ec/fallback_raw outputs must be 16-byte aligned");
+    if (out->fallback_raw_tiles < 0) return fail(SE12_E_INVALID, "se12_encode: negative fallback capacity");
+    if (out->fallback_raw_tiles > 0 && !out->fallback_raw_dev)
+        return fail(SE12_E_INVALID, "se12_encode: fallback_raw is NULL but has capacity");
+    pack_codebook(a, codebook);
+    a.sm = out->sm_dev;
+    a.ec = out->ec_dev;
+    a.esc = out->esc_dev;
+    a.bitmap = out->fallback_bitmap_dev;
+    a.raw = out->fallback_raw_dev;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    int32_t* counts = nullptr;
+    int32_t* rank = nullptr;
+    int64_t* totals = nullptr;
+    int64_t total = 0;
+    hipError_t e = hipMalloc(&counts, (size_t)a.T * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&rank, (size_t)a.T * sizeof(int32_t));
+    if (e == hipSuccess) e = hipMalloc(&totals, sizeof(int64_t));
+    a.tile_escapes = counts;
+    a.fb_rank = rank;
+    a.totals = totals;
+    if (e == hipSuccess) e = launch_encode_count(a, st);
+    if (e == hipSuccess) e = launch_encode_scan(a, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(&total, totals, sizeof total, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    int rc = SE12_OK;
+    if (e != hipSuccess) {
+        rc = fail(SE12_E_HIP, "se12_encode: %s", hipGetErrorString(e));
+    } else if (total > out->fallback_raw_tiles) {
+        rc = fail(SE12_E_CAPACITY, "se12_encode: %lld fallback tiles, fallback_raw holds %lld", (long long)total,
+                  (long long)out->fallback_raw_tiles);
+    } else {
+        e = launch_encode_write(a, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) rc = fail(SE12_E_HIP, "se12_encode write: %s", hipGetErrorString(e));
+    }
+    if (fallback_tiles_out) *fallback_tiles_out = total;
+    if (counts) (void)hipFree(counts);
+    if (rank) (void)hipFree(rank);
+    if (totals) (void)hipFree(totals);
+    return rc;
+}
+
+}  // extern "C"

@@ -1,0 +1,155 @@
+// Decode-only kernels: SE12 streams -> row-major BF16 bits, bit-exact with the
+// reference decoder (lws/domain/se12/codec.py:144-186). One wave decodes one
+// 16x256 tile with the same per-lane routine as the fused GEMV and writes its
+// rows straight to the cropped [rows, cols] output, replacing the reference's
+// one-thread-per-tile kernel plus device untile/crop
+// (lws/adapters/cuda/kernels/se12_decode.cu:12-43,
+// lws/adapters/cuda/se12_decoder.py:147-185).
+//
+// Also here: the per-tile fallback rank (rank of a fallback tile among all
+// fallback tiles, cumsum(bitmap bits) - 1 as in lws/adapters/cuda/gemv.py:47-53,
+// and -1 for a tile that is not a fallback tile), computed once at bind time
+// by a single-block scan; the kernels read it instead of the bitmap.
+#include "se12_device.hpp"
+#include "se12_internal.hpp"
+
+namespace se12 {
+
+constexpr int kDecodeWaves = 4;
+
+__device__ __forceinline__ void store16(uint16_t* out_row, int64_t col, int64_t K, bool vec_ok, const uint32_t w[8]) {
+    if (vec_ok && col + 16 <= K) {
+        reinterpret_cast<uint4*>(out_row + col)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        reinterpret_cast<uint4*>(out_row + col)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (col + i < K) out_row[col + i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+    }
+}
+
+// Decodes tile `tile` for this lane; calls sink(j, w) for each chunk j.
+template <typename Sink>
+__device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t* lut, int64_t tile, uint32_t lane,
+                                            Sink&& sink) {
+    TileLoads t;
+    load_tile(t, a.sm, a.ec, a.esc, a.fb_rank, tile, lane);
+    if (t.fallback_rank >= 0) {
+        const int16_t* raw = a.fb_raw + (int64_t)t.fallback_rank * kTile;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t w[8];
+            load_raw_chunk(raw, j, lane, w);
+            sink(j, w);
+        }
+    } else {
+        uint32_t run = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            uint32_t w[8];
+            decode_chunk(lut, t.sm[j], t.ec[j], t.esc, run, lane, w);
+            sink(j, w);
+        }
+    }
+}
+
+template <bool ROWS>
+__global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeArgs a) {
+    __shared__ uint32_t lut[256];
+    const int tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    build_pair_lut(lut, a.codebook, tid, blockDim.x);
+    lds_barrier();
+
+    const int64_t item = (int64_t)blockIdx.x * kDecodeWaves + w;
+    if (item >= a.items) return;
+    const bool vec_ok = a.out_vec_ok != 0;
+    if constexpr (!ROWS) {
+        const int64_t tile = item;
+        const int tr = (int)(tile / a.TC);
+        const int kt = (int)(tile - (int64_t)tr * a.TC);
+        const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
+        decode_tile(a, lut, tile, lane, [&](int j, const uint32_t* wv) {
+            const int64_t row = (int64_t)tr * kTileRows + 4 * j + (lane >> 4);
+            if (row < a.N) store16(a.out + row * a.K, col, a.K, vec_ok, wv);
+        });
+    } else {
+        const int64_t ri = item / a.TC;
+        const int kt = (int)(item - ri * a.TC);
+        const int64_t row = a.rows[ri];
+        const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
+        uint16_t* out_row = a.out + ri * a.K;
+        if (row < 0 || row >= a.N) {
+            const uint32_t zero[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            if ((lane >> 4) == 0) store16(out_row, col, a.K, vec_ok, zero);
+            return;
+        }
+        const int lr = (int)(row & (kTileRows - 1));
+        const int64_t tile = (row / kTileRows) * a.TC + kt;
+        decode_tile(a, lut, tile, lane, [&](int j, const uint32_t* wv) {
+            if (4 * j + (int)(lane >> 4) == lr) store16(out_row, col, a.K, vec_ok, wv);
+        });
+    }
+}
+
+hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream) {
+    if (a.items <= 0) return hipSuccess;
+    const int64_t blocks = (a.items + kDecodeWaves - 1) / kDecodeWaves;
+    if (rows)
+        hipLaunchKernelGGL(decode_kernel<true>, dim3((uint32_t)blocks), dim3(kDecodeWaves * kWave), 0, stream, a);
+    else
+        hipLaunchKernelGGL(decode_kernel<false>, dim3((uint32_t)blocks), dim3(kDecodeWaves * kWave), 0, stream, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// fallback ranks from the bitmap (bind time, one block)
+// ---------------------------------------------------------------------------
+
+constexpr int kScanThreads = 1024;
+
+// exclusive scan of one value per thread over the block (1024 threads)
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* tmp, int64_t* total) {
+    const int tid = threadIdx.x;
+    tmp[tid] = v;
+    __syncthreads();
+    for (int d = 1; d < kScanThreads; d <<= 1) {
+        int64_t u = tid >= d ? tmp[tid - d] : 0;
+        __syncthreads();
+        tmp[tid] += u;
+        __syncthreads();
+    }
+    const int64_t incl = tmp[tid];
+    *total = tmp[kScanThreads - 1];
+    __syncthreads();
+    return incl - v;
+}
+
+__global__ __launch_bounds__(kScanThreads) void fallback_rank_kernel(const uint8_t* bitmap, int64_t T,
+                                                                     int32_t* rank, int64_t* total_out) {
+    __shared__ int64_t tmp[kScanThreads];
+    const int tid = threadIdx.x;
+    int64_t chunk = (T + kScanThreads - 1) / kScanThreads;
+    chunk = (chunk + 7) & ~int64_t(7);
+    const int64_t t0 = (int64_t)tid * chunk;
+    const int64_t t1 = t0 + chunk < T ? t0 + chunk : T;
+    int64_t count = 0;
+    for (int64_t t = t0; t < t1; ++t) count += (bitmap[t >> 3] >> (7 - (t & 7))) & 1;
+    int64_t total;
+    int64_t base = block_exclusive_scan(count, tmp, &total);
+    for (int64_t t = t0; t < t1; ++t) {
+        const int bit = (bitmap[t >> 3] >> (7 - (t & 7))) & 1;
+        rank[t] = bit ? (int32_t)base : -1;
+        base += bit;
+    }
+    if (tid == 0) *total_out = total;
+}
+
+hipError_t launch_fallback_rank_from_bitmap(const uint8_t* bitmap, int64_t T, int32_t* rank, int64_t* total,
+                                            hipStream_t stream) {
+    hipLaunchKernelGGL(fallback_rank_kernel, dim3(1), dim3(kScanThreads), 0, stream, bitmap, T, rank, total);
+    return hipGetLastError();
+}
+
+}  // namespace se12

@@ -1,0 +1,384 @@
+"""HIP adapters behind the reference's GPU ports, over libse12_gfx950.so.
+
+  Se12MatVecKernel / RawBf16MatVecKernel  -> MatVecKernel
+      (lws/application/ports/gpu/matvec_kernel.py:18-23,
+       lws/adapters/cuda/gemv.py:143-226)
+  HipSe12WeightDecoder                    -> WeightDecoder
+      (lws/application/ports/gpu/weight_decoder.py:26-33,
+       lws/adapters/cuda/se12_decoder.py:45-76)
+  HipGpuProbe                             -> GpuProbe
+      (lws/application/ports/gpu/gpu_probe.py:17-27)
+  HipBenchmarkTimer                       -> BenchmarkTimer
+      (lws/application/ports/gpu/benchmark_timer.py:13-21)
+  encode_on_device                        -> the packer's encode_tensor step
+      (lws/domain/se12/codec.py:111-141), run on the GPU
+
+Torch is used only to own device memory and to name the stream; every kernel
+is launched by the library on the caller's current HIP stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import dataclasses
+import statistics as _st
+from typing import Any, Callable
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .format import (
+    CODEBOOK_SIZE,
+    ESCAPE_BUDGET,
+    TILE_SIZE,
+    Bf16Weights,
+    Se12DeviceTensor,
+    bitmap_bytes,
+    tile_grid,
+)
+from .launch import BlockCount, LaunchConfiguration, ThreadsPerBlock
+
+
+def _device_of(t: torch.Tensor) -> torch.device:
+    if not t.is_cuda:
+        raise ValueError("expected a tensor on a HIP device")
+    return t.device
+
+
+def _as_device_tensor(tensor: Any, device=None) -> Se12DeviceTensor:
+    if isinstance(tensor, Se12DeviceTensor):
+        return tensor
+    return Se12DeviceTensor.from_host(tensor, device=device)
+
+
+class _Handle:
+    """Owns one se12_handle*; released when garbage-collected."""
+
+    def __init__(self, raw: ctypes.c_void_p, keepalive: tuple) -> None:
+        self.raw = raw
+        self._keepalive = keepalive  # the tensors the handle points into
+
+    def release(self) -> None:
+        if self.raw:
+            nat.lib().se12_release(self.raw)
+            self.raw = ctypes.c_void_p(None)
+
+    def __del__(self) -> None:
+        try:
+            self.release()
+        except Exception:
+            pass
+
+    def default_launch(self, batch: int) -> LaunchConfiguration:
+        out = nat.Launch()
+        nat.check(nat.lib().se12_default_launch(self.raw, batch, ctypes.byref(out)))
+        return LaunchConfiguration(ThreadsPerBlock(out.threads_per_block), BlockCount(out.blocks))
+
+
+def bind_se12(dt: Se12DeviceTensor, max_batch: int = nat.MAX_BATCH) -> _Handle:
+    s = nat.Streams(
+        sm_dev=dt.sm.data_ptr(),
+        ec_dev=dt.ec.data_ptr(),
+        esc_dev=dt.esc.data_ptr(),
+        codebook_dev=dt.codebook.data_ptr(),
+        fallback_bitmap_dev=dt.fallback_bitmap.data_ptr(),
+        fallback_raw_dev=dt.fallback_raw.data_ptr() if dt.fallback_raw.numel() else None,
+        fallback_raw_elems=int(dt.fallback_raw.numel()),
+    )
+    h = ctypes.c_void_p()
+    with torch.cuda.device(dt.sm.device):
+        nat.check(nat.lib().se12_bind(ctypes.byref(s), dt.rows, dt.cols, max_batch, nat.stream_ptr(), ctypes.byref(h)))
+    return _Handle(h, (dt,))
+
+
+def bind_raw_bf16(w: torch.Tensor, max_batch: int = nat.MAX_BATCH) -> _Handle:
+    if w.dtype != torch.bfloat16 or w.dim() != 2:
+        raise ValueError("raw twin needs a 2-D bfloat16 weight matrix")
+    w = w.contiguous()
+    h = ctypes.c_void_p()
+    with torch.cuda.device(w.device):
+        nat.check(nat.lib().se12_bind_raw_bf16(nat.ptr(w), w.shape[0], w.shape[1], max_batch, nat.stream_ptr(), ctypes.byref(h)))
+    return _Handle(h, (w,))
+
+
+def _launch_struct(launch: LaunchConfiguration | None):
+    if launch is None:
+        return None
+    return ctypes.byref(nat.Launch(launch.threads_per_block.value, launch.blocks.value))
+
+
+class _GemvBase:
+    rows: int
+    cols: int
+    handle: _Handle
+    device: torch.device
+
+    def multiply(self, activations: torch.Tensor, launch: LaunchConfiguration | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+        """y = x . W^T in FP32 for x [B, K] (BF16 or FP32) on the device;
+        `launch=None` uses the default configuration (matvec_kernel.py:19-22)."""
+        x = activations
+        if x.dim() == 1:
+            x = x.unsqueeze(0)
+        if x.dim() != 2 or x.shape[1] != self.cols:
+            raise ValueError(f"activations must be [B, {self.cols}], got {tuple(activations.shape)}")
+        if x.device != self.device:
+            raise ValueError(f"activations on {x.device}, weights on {self.device}")
+        if x.dtype == torch.bfloat16:
+            xd = nat.X_BF16
+        elif x.dtype == torch.float32:
+            xd = nat.X_F32
+        else:
+            raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
+        x = x.contiguous()
+        b = x.shape[0]
+        if out is None:
+            out = torch.empty((b, self.rows), dtype=torch.float32, device=self.device)
+        elif out.shape != (b, self.rows) or out.dtype != torch.float32 or not out.is_contiguous():
+            raise ValueError("out must be a contiguous float32 [B, rows] tensor")
+        nat.check(nat.lib().se12_gemv(self.handle.raw, nat.ptr(x), xd, b, nat.ptr(out), _launch_struct(launch), nat.stream_ptr()))
+        return out
+
+    def default_launch(self, batch: int) -> LaunchConfiguration:
+        return self.handle.default_launch(batch)
+
+
+class Se12MatVecKernel(_GemvBase):
+    """Fused SE12 decode + GEMV bound to one SE12 matrix (gemv.py:180-226).
+
+    `tensor` is a host `Se12Tensor` (reference layout, uploaded once) or an
+    `Se12DeviceTensor` already in HBM."""
+
+    def __init__(self, tensor: Any, max_batch: int = nat.MAX_BATCH, device=None) -> None:
+        self.tensor = _as_device_tensor(tensor, device)
+        self.rows, self.cols = self.tensor.rows, self.tensor.cols
+        self.device = self.tensor.sm.device
+        self.handle = bind_se12(self.tensor, max_batch)
+
+
+class RawBf16MatVecKernel(_GemvBase):
+    """The same-skeleton raw-BF16 twin bound to a [N, K] BF16 matrix (gemv.py:143-172)."""
+
+    def __init__(self, weights: torch.Tensor, max_batch: int = nat.MAX_BATCH) -> None:
+        self.weights = weights.contiguous()
+        self.rows, self.cols = self.weights.shape
+        self.device = _device_of(self.weights)
+        self.handle = bind_raw_bf16(self.weights, max_batch)
+
+
+@dataclasses.dataclass(frozen=True)
+class RowIndices:
+    """Row indices in request order (weight_decoder.py:18-23)."""
+
+    values: tuple[int, ...]
+
+
+class HipSe12WeightDecoder:
+    """WeightDecoder on the GPU (se12_decoder.py:45-76). Bindings are cached per
+    device tensor so repeated decodes reuse the bind-time sidecar."""
+
+    def __init__(self) -> None:
+        self._last: tuple[Any, Se12DeviceTensor, _Handle] | None = None
+
+    def _handle(self, tensor: Any) -> tuple[Se12DeviceTensor, _Handle]:
+        if self._last is not None and self._last[0] is tensor:
+            return self._last[1], self._last[2]
+        dt = _as_device_tensor(tensor)
+        h = bind_se12(dt, max_batch=1)
+        self._last = (tensor, dt, h)
+        return dt, h
+
+    def decode_to_device(self, tensor: Any) -> torch.Tensor:
+        """Decoded weights as a device BF16 [rows, cols] tensor (se12_decoder.py:58-62)."""
+        dt, h = self._handle(tensor)
+        out = torch.empty((dt.rows, dt.cols), dtype=torch.bfloat16, device=dt.sm.device)
+        nat.check(nat.lib().se12_decode(h.raw, nat.ptr(out), nat.stream_ptr()))
+        return out
+
+    def decode(self, tensor: Any) -> Bf16Weights:
+        """Host copy of the decoded bit pattern (se12_decoder.py:54-56)."""
+        out = self.decode_to_device(tensor)
+        return Bf16Weights(bit_pattern=out.view(torch.int16).cpu().numpy().reshape(-1))
+
+    def decode_rows_to_device(self, tensor: Any, rows: torch.Tensor) -> torch.Tensor:
+        """Rows given by a device int64 index tensor, in order; only their tiles are read."""
+        dt, h = self._handle(tensor)
+        idx = rows.to(device=dt.sm.device, dtype=torch.int64).contiguous()
+        out = torch.empty((idx.numel(), dt.cols), dtype=torch.bfloat16, device=dt.sm.device)
+        nat.check(nat.lib().se12_decode_rows(h.raw, nat.ptr(idx), idx.numel(), nat.ptr(out), nat.stream_ptr()))
+        return out
+
+    def decode_rows(self, tensor: Any, rows: RowIndices) -> Bf16Weights:
+        """The decoded rows, in request order (weight_decoder.py:30-33)."""
+        dt, _ = self._handle(tensor)
+        values = tuple(int(r) for r in rows.values)
+        bad = [r for r in values if not 0 <= r < dt.rows]
+        if bad:
+            raise IndexError(f"row indices {bad[:4]} outside [0, {dt.rows})")
+        idx = torch.tensor(values, dtype=torch.int64, device=dt.sm.device)
+        out = self.decode_rows_to_device(tensor, idx)
+        return Bf16Weights(bit_pattern=out.view(torch.int16).cpu().numpy().reshape(-1))
+
+
+def encode_on_device(weights: torch.Tensor) -> Se12DeviceTensor:
+    """SE12-encodes a [rows, cols] BF16 device tensor on the GPU; the streams are
+    byte-identical to the reference encoder's (codec.py:111-141)."""
+    if weights.dtype != torch.bfloat16 or weights.dim() != 2:
+        raise ValueError("encode_on_device needs a 2-D bfloat16 tensor")
+    w = weights.contiguous()
+    dev = _device_of(w)
+    rows, cols = w.shape
+    tr, tc = tile_grid(rows, cols)
+    t = tr * tc
+    cb = (ctypes.c_uint8 * CODEBOOK_SIZE)()
+    nfb = ctypes.c_int64()
+    lib = nat.lib()
+    with torch.cuda.device(dev):
+        st = nat.stream_ptr()
+        nat.check(lib.se12_encode_prepare(nat.ptr(w), rows, cols, cols, cb, ctypes.byref(nfb), st))
+        sm = torch.empty(t * TILE_SIZE, dtype=torch.uint8, device=dev)
+        ec = torch.empty(t * TILE_SIZE // 2, dtype=torch.uint8, device=dev)
+        esc = torch.empty(t * ESCAPE_BUDGET, dtype=torch.uint8, device=dev)
+        bitmap = torch.empty(bitmap_bytes(t), dtype=torch.uint8, device=dev)
+        raw = torch.empty(nfb.value * TILE_SIZE, dtype=torch.int16, device=dev)
+        out = nat.StreamsOut(
+            sm_dev=sm.data_ptr(), ec_dev=ec.data_ptr(), esc_dev=esc.data_ptr(), fallback_bitmap_dev=bitmap.data_ptr(),
+            fallback_raw_dev=raw.data_ptr() if raw.numel() else None, fallback_raw_tiles=nfb.value,
+        )
+        got = ctypes.c_int64()
+        nat.check(lib.se12_encode(nat.ptr(w), rows, cols, cols, cb, ctypes.byref(out), ctypes.byref(got), st))
+    codebook = tuple(int(c) for c in cb)
+    return Se12DeviceTensor(
+        sm=sm, ec=ec, esc=esc, codebook=torch.tensor(codebook, dtype=torch.uint8, device=dev),
+        fallback_bitmap=bitmap, fallback_raw=raw, rows=int(rows), cols=int(cols), codebook_host=codebook,
+    )
+
+
+def codebook_from_histogram(counts) -> tuple[int, ...]:
+    """Host call into the library's codebook rule (codebook.py:41-59)."""
+    arr = (ctypes.c_uint64 * 256)(*[int(c) for c in counts])
+    out = (ctypes.c_uint8 * CODEBOOK_SIZE)()
+    nat.check(nat.lib().se12_codebook_from_histogram(arr, out))
+    return tuple(int(c) for c in out)
+
+
+# ---------------------------------------------------------------------------
+# device facts and timing
+# ---------------------------------------------------------------------------
+
+
+@dataclasses.dataclass(frozen=True)
+class DeviceProperties:
+    """hipDeviceProp_t facts the roofline and the launch heuristic use."""
+
+    name: str
+    arch: str
+    compute_units: int
+    wavefront_size: int
+    l2_bytes: int
+    lds_bytes_per_cu: int
+    lds_bytes_per_block: int
+    total_memory_bytes: int
+    clock_khz: int
+    memory_clock_khz: int
+    memory_bus_width_bits: int
+
+    @property
+    def slug(self) -> str:
+        """GPU slug for per-GPU files, e.g. 'amd-instinct-mi355x-gfx950'."""
+        base = "".join(ch.lower() if ch.isalnum() else "-" for ch in self.name).strip("-")
+        while "--" in base:
+            base = base.replace("--", "-")
+        return f"{base}-{self.arch.split(':')[0]}"
+
+
+class HipGpuProbe:
+    """GpuProbe over hipGetDeviceProperties (gpu_probe.py:59-80)."""
+
+    def __init__(self, device: int | None = None) -> None:
+        self.device = torch.cuda.current_device() if device is None else device
+
+    def properties(self) -> DeviceProperties:
+        info = nat.DeviceInfo()
+        nat.check(nat.lib().se12_device_info_get(self.device, ctypes.byref(info)))
+        return DeviceProperties(
+            name=info.name.decode(), arch=info.arch.decode(), compute_units=info.compute_units,
+            wavefront_size=info.wavefront_size, l2_bytes=info.l2_bytes, lds_bytes_per_cu=info.lds_bytes_per_cu,
+            lds_bytes_per_block=info.lds_bytes_per_block, total_memory_bytes=info.total_memory_bytes,
+            clock_khz=info.clock_khz, memory_clock_khz=info.memory_clock_khz,
+            memory_bus_width_bits=info.memory_bus_width_bits,
+        )
+
+    def software_versions(self) -> dict:
+        return {"torch": torch.__version__, "hip": getattr(torch.version, "hip", None), "se12": nat.version()}
+
+    def smoke_test(self) -> bool:
+        """Does a kernel run on this device at all (gpu_probe.py:152-166)."""
+        try:
+            a = torch.ones(16, device=f"cuda:{self.device}")
+            return bool((a + a).sum().item() == 32.0)
+        except Exception:
+            return False
+
+
+# MI355X's last-level Infinity Cache (MALL) is not reported by hipDeviceProp;
+# the flush covers it explicitly.
+INFINITY_CACHE_BYTES = 256 * 1024 * 1024
+
+
+@dataclasses.dataclass(frozen=True)
+class LatencyStats:
+    median_us: float
+    p10_us: float
+    p90_us: float
+    samples: tuple[float, ...]
+
+
+def latency_stats(samples_us) -> LatencyStats:
+    arr = np.asarray(samples_us, dtype=np.float64)
+    return LatencyStats(float(np.median(arr)), float(np.percentile(arr, 10)), float(np.percentile(arr, 90)), tuple(arr.tolist()))
+
+
+class HipBenchmarkTimer:
+    """Event timing after a cache flush of at least 2 x (L2 + Infinity Cache)
+    (benchmark_timer.py:20-66; the reference flushes 2 x L2 only)."""
+
+    def __init__(self, device: int | None = None, l2_bytes: int | None = None) -> None:
+        self.device = torch.cuda.current_device() if device is None else device
+        if l2_bytes is None:
+            l2_bytes = HipGpuProbe(self.device).properties().l2_bytes
+        flush = 2 * (int(l2_bytes) + INFINITY_CACHE_BYTES)
+        self.flush_buffer = torch.empty(flush // 4, dtype=torch.float32, device=f"cuda:{self.device}")
+
+    def flush(self) -> None:
+        self.flush_buffer.fill_(1.0)
+
+    def time_operation(self, operation: Callable[[], Any], warmup: int = 25, timed: int = 100, flush: bool = True) -> LatencyStats:
+        for _ in range(warmup):
+            operation()
+        torch.cuda.synchronize(self.device)
+        out = []
+        for _ in range(timed):
+            if flush:
+                self.flush()
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record()
+            operation()
+            e.record()
+            e.synchronize()
+            out.append(s.elapsed_time(e) * 1000.0)
+        return latency_stats(out)
+
+    def measure_peak_copy_bandwidth(self, nbytes: int = 1 << 30) -> float:
+        """GB/s of a device-to-device copy of `nbytes` (read + write counted),
+        the measured peak the 80%-of-HBM target is checked against."""
+        n = nbytes // 4
+        src = torch.empty(n, dtype=torch.float32, device=f"cuda:{self.device}")
+        dst = torch.empty_like(src)
+        st = self.time_operation(lambda: dst.copy_(src), warmup=5, timed=20, flush=False)
+        return 2 * n * 4 / (st.median_us * 1e-6) / 1e9
+
+
+def median(values) -> float:
+    return float(_st.median(values))

@@ -1,0 +1,114 @@
+"""Launch configurations for the SE12 GEMV on MI355X, and the tuner's rules.
+
+Mirrors lws/domain/launch/heuristic.py:24-51 (LaunchConfiguration =
+threads_per_block + blocks) and lws/domain/launch/search_space.py:14-75
+(candidate set, best configuration, order-matched configuration), re-derived
+for this kernel's grid: a block is 1..4 wave64s working on one 16-row tile
+row, and `blocks` = tile_rows x k_splits, where the K tiles of a tile row are
+cut into `k_splits` contiguous ranges (the last block of a tile row to finish
+adds the splits in order). The default configuration itself is computed by
+the library (se12_default_launch) from the device's CU count.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+WAVE_SIZE = 64
+THREADS_PER_BLOCK_CANDIDATES = (64, 128, 192, 256)
+MAX_K_SPLITS = 64
+
+
+@dataclasses.dataclass(frozen=True)
+class ThreadsPerBlock:
+    value: int
+
+
+@dataclasses.dataclass(frozen=True)
+class BlockCount:
+    value: int
+
+
+@dataclasses.dataclass(frozen=True)
+class LaunchConfiguration:
+    threads_per_block: ThreadsPerBlock
+    blocks: BlockCount
+
+
+@dataclasses.dataclass(frozen=True)
+class GemvShape:
+    output_rows: int
+    batch_size: int
+
+
+def tile_rows(output_rows: int) -> int:
+    return -(-output_rows // 16)
+
+
+def k_tiles(k: int) -> int:
+    return -(-k // 256)
+
+
+def configuration(waves: int, k_splits: int, output_rows: int) -> LaunchConfiguration:
+    return LaunchConfiguration(
+        threads_per_block=ThreadsPerBlock(waves * WAVE_SIZE), blocks=BlockCount(tile_rows(output_rows) * k_splits)
+    )
+
+
+def waves_and_splits(launch: LaunchConfiguration, output_rows: int) -> tuple[int, int]:
+    """(waves per block, K splits) of a configuration for a matrix with `output_rows` rows."""
+    tr = tile_rows(output_rows)
+    tpb = launch.threads_per_block.value
+    blocks = launch.blocks.value
+    if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= 256:
+        raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, 256]")
+    if blocks <= 0 or blocks % tr:
+        raise ValueError(f"blocks {blocks} must be a positive multiple of the {tr} tile rows")
+    return tpb // WAVE_SIZE, blocks // tr
+
+
+def candidate_configurations(output_rows: int, k: int) -> tuple[LaunchConfiguration, ...]:
+    """Every (waves, splits) worth timing: 1..4 waves, splits 1..K tiles (powers
+    of two and the exact K tile count), never more waves than K tiles per
+    split (search_space.py:17-19 enumerates threads per block the same way)."""
+    tc = k_tiles(k)
+    splits = sorted({s for s in (1, 2, 3, 4, 6, 8, 9, 12, 16, 18, 24, 32, 36, 48, 64) if s <= min(tc, MAX_K_SPLITS)} | {1})
+    out = []
+    for tpb in THREADS_PER_BLOCK_CANDIDATES:
+        waves = tpb // WAVE_SIZE
+        for s in splits:
+            if waves <= -(-tc // s):
+                out.append(configuration(waves, s, output_rows))
+    return tuple(out)
+
+
+@dataclasses.dataclass(frozen=True)
+class TimingAndAccuracy:
+    median_latency_microseconds: float
+    passes_accuracy_check: bool
+
+
+@dataclasses.dataclass(frozen=True)
+class TimedCandidate:
+    configuration: LaunchConfiguration
+    measurement: TimingAndAccuracy
+
+
+def best_configuration(timed: tuple[TimedCandidate, ...]) -> LaunchConfiguration | None:
+    """Fastest configuration that passed the accuracy check (search_space.py:51-58)."""
+    passing = [c for c in timed if c.measurement.passes_accuracy_check]
+    if not passing:
+        return None
+    return min(passing, key=lambda c: c.measurement.median_latency_microseconds).configuration
+
+
+def order_matched_configuration(raw_timed: tuple[TimedCandidate, ...], fused_timed: tuple[TimedCandidate, ...]) -> LaunchConfiguration | None:
+    """One configuration shared by the raw twin and the fused kernel with the
+    best combined time, both passing accuracy (search_space.py:61-75): with
+    one launch shape the two give bit-identical FP32 outputs."""
+    raw_ok = {c.configuration: c.measurement.median_latency_microseconds for c in raw_timed if c.measurement.passes_accuracy_check}
+    fused_ok = {c.configuration: c.measurement.median_latency_microseconds for c in fused_timed if c.measurement.passes_accuracy_check}
+    shared = [cfg for cfg in raw_ok if cfg in fused_ok]
+    if not shared:
+        return None
+    return min(shared, key=lambda cfg: raw_ok[cfg] + fused_ok[cfg])

@@ -1,0 +1,227 @@
+"""Fused SE12 decode + GEMV on the GPU vs the oracle's numpy decode + float32
+matmul on the same seeded inputs, within REL_TOL (1e-3 relative, scale
+clamped at 1). Also: the raw-BF16 twin gives bit-identical outputs under the
+same launch configuration (the reference's AC-032,
+tests/test_spec_fused_gemv.py:313-320), every launch configuration is
+deterministic, and a captured HIP graph replays to the eager result."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN_NAMES, golden_as_encoding, load_golden
+from gpu_helpers import REL_TOL, bf16_tensor, heavy_tailed_bf16, max_rel_error, normal_case, to_device, uniform_bits
+from oracle import se12_codec as o
+
+pytestmark = pytest.mark.gpu
+
+
+def _x(batch: int, cols: int, seed: int) -> np.ndarray:
+    return o.normal_bf16(batch, cols, seed=seed, std=1.0)
+
+
+def _check(kernel, enc, xbits, device, launch=None, f32=False):
+    x = bf16_tensor(xbits, device)
+    if f32:
+        x = x.float()
+    y = kernel.multiply(x, launch=launch)
+    torch.cuda.synchronize()
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xbits))
+    err = max_rel_error(y, ref)
+    assert err <= REL_TOL, f"max relative error {err:.3e}"
+    return y
+
+
+@pytest.mark.parametrize("name", GOLDEN_NAMES)
+@pytest.mark.parametrize("batch", [1, 3])
+def test_gemv_golden_vectors(gpu, name, batch):
+    from se12_amd.hip import Se12MatVecKernel
+
+    g = load_golden(name)
+    enc = golden_as_encoding(g)
+    if name in ("edge_1x214", "uniform_33x300"):
+        # inf/NaN/huge weights: a row with a NaN weight must give NaN; rows of
+        # finite weights whose sum is finite in float64 and float32 must match
+        k = Se12MatVecKernel(to_device(enc, gpu))
+        xb = _x(batch, g["cols"], seed=1)
+        y = k.multiply(bf16_tensor(xb, gpu)).cpu().numpy()
+        w = o.bf16_bits_to_f32(o.decode(enc))
+        ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+        ref64 = o.gemv_reference(enc, o.bf16_bits_to_f32(xb), fp64=True)
+        nan_rows = np.isnan(w).any(axis=1)
+        assert np.all(np.isnan(y[:, nan_rows]))
+        ok = (~np.isinf(w).any(axis=1)) & ~nan_rows & (np.abs(w).max(axis=1) < 1e30)
+        ok = ok[None, :] & np.isfinite(ref) & np.isfinite(ref64)
+        assert np.all(np.abs(y[ok] - ref[ok]) <= REL_TOL * np.maximum(np.abs(ref[ok]), 1.0))
+        return
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    _check(k, enc, _x(batch, g["cols"], seed=batch), gpu)
+
+
+def test_gemv_benchmark_shape_batch1(gpu):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits, enc = normal_case(2304, 9216, seed=0)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    _check(k, enc, _x(1, 9216, seed=1), gpu)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 16, 32])
+def test_gemv_batch_sweep(gpu, batch):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits, enc = normal_case(448, 3584, seed=11)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    _check(k, enc, _x(batch, 3584, seed=100 + batch), gpu)
+
+
+@pytest.mark.parametrize("batch", [1, 4, 7])
+def test_gemv_float32_activations(gpu, batch):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits, enc = normal_case(300, 1000, seed=12)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    rng = np.random.default_rng(batch)
+    x = rng.standard_normal((batch, 1000)).astype(np.float32)
+    y = k.multiply(torch.from_numpy(x).to(gpu))
+    ref = o.gemv_reference(enc, x)
+    assert max_rel_error(y, ref) <= REL_TOL
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (17, 257), (33, 300), (100, 2304), (2048, 2304), (64, 9216)])
+def test_gemv_ragged_and_escape_heavy(gpu, rows, cols):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits = heavy_tailed_bf16(rows, cols, seed=rows * 7 + cols)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    _check(k, enc, _x(2, cols, seed=rows), gpu)
+
+
+def test_gemv_fallback_tiles(gpu):
+    from se12_amd.hip import Se12MatVecKernel
+
+    # concentrated exponents with random escapes; a third of the tiles overflow
+    rng = np.random.default_rng(21)
+    e = rng.choice(np.arange(118, 126, dtype=np.uint8), size=(64, 1024))
+    for t in range(16):
+        if t % 3 == 0:
+            tr, tc = divmod(t, 4)
+            pos = rng.choice(4096, size=40, replace=False)
+            e[tr * 16 + pos // 256, tc * 256 + pos % 256] = rng.integers(100, 118, size=40)
+    sign = rng.integers(0, 2, size=e.shape).astype(np.uint16)
+    mant = rng.integers(0, 0x80, size=e.shape).astype(np.uint16)
+    bits = ((sign << 15) | (e.astype(np.uint16) << 7) | mant).view(np.int16)
+    enc = o.encode(bits.reshape(-1), 64, 1024)
+    assert o.fallback_tile_count(enc) == 6
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    _check(k, enc, _x(3, 1024, seed=5), gpu)
+
+
+def test_gemv_padding_of_an_infinite_codebook0_is_masked(gpu):
+    """codebook[0] = 255: padding columns decode to +inf; rows whose real
+    weights are finite must still give finite, correct outputs."""
+    from se12_amd.hip import Se12MatVecKernel
+
+    rows, cols = 32, 300
+    rng = np.random.default_rng(8)
+    bits = o.normal_bf16(rows, cols, seed=9, std=0.02)
+    bits[:16] = np.uint16(0x7F80).view(np.int16)  # +inf rows make 255 the top exponent
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    assert enc["codebook"][0] == 255
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    xb = _x(1, cols, seed=int(rng.integers(100)))
+    y = k.multiply(bf16_tensor(xb, gpu)).cpu().numpy()
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+    assert np.all(np.isfinite(y[:, 16:]))
+    assert np.all(np.abs(y[:, 16:] - ref[:, 16:]) <= REL_TOL * np.maximum(np.abs(ref[:, 16:]), 1.0))
+    assert np.array_equal(np.isnan(y[:, :16]), np.isnan(ref[:, :16]))
+
+
+def _configs(rows, cols):
+    from se12_amd.launch import candidate_configurations
+
+    return candidate_configurations(rows, cols)
+
+
+def test_every_launch_configuration_is_correct_and_deterministic(gpu):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits = heavy_tailed_bf16(272, 2800, seed=31)
+    enc = o.encode(bits.reshape(-1), 272, 2800)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    xb = _x(2, 2800, seed=32)
+    x = bf16_tensor(xb, gpu)
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+    for cfg in _configs(272, 2800):
+        y1 = k.multiply(x, launch=cfg).clone()
+        y2 = k.multiply(x, launch=cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), cfg
+        assert max_rel_error(y1, ref) <= REL_TOL, cfg
+
+
+@pytest.mark.parametrize("shape", [(2304, 9216), (272, 2800), (48, 768)])
+def test_raw_twin_is_bit_identical_under_one_launch(gpu, shape):
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+
+    rows, cols = shape
+    if shape == (48, 768):
+        g = load_golden("mixed_48x768")
+        bits, enc = g["bits"].reshape(rows, cols), golden_as_encoding(g)
+    else:
+        bits = heavy_tailed_bf16(rows, cols, seed=rows)
+        enc = o.encode(bits.reshape(-1), rows, cols)
+    fused = Se12MatVecKernel(to_device(enc, gpu))
+    raw = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
+    for batch in (1, 4, 6):
+        x = bf16_tensor(_x(batch, cols, seed=batch), gpu)
+        cfgs = [None] + list(_configs(rows, cols))[:: max(1, len(_configs(rows, cols)) // 6)]
+        for cfg in cfgs:
+            assert torch.equal(fused.multiply(x, launch=cfg), raw.multiply(x, launch=cfg)), (batch, cfg)
+
+
+def test_graph_replay_matches_eager(gpu):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits, enc = normal_case(2304, 9216, seed=0)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    x = bf16_tensor(_x(1, 9216, seed=1), gpu)
+    out = torch.empty((1, 2304), dtype=torch.float32, device=gpu)
+    eager = k.multiply(x).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        k.multiply(x, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        k.multiply(x, out=out)
+    for i in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        _ = k.multiply(x)  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_bad_arguments_raise(gpu):
+    from se12_amd import _native as nat
+    from se12_amd.hip import Se12MatVecKernel
+    from se12_amd.launch import BlockCount, LaunchConfiguration, ThreadsPerBlock
+
+    bits, enc = normal_case(64, 512, seed=2)
+    k = Se12MatVecKernel(to_device(enc, gpu), max_batch=4)
+    with pytest.raises(ValueError):
+        k.multiply(torch.zeros((1, 511), dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(nat.Se12Error):
+        k.multiply(torch.zeros((5, 512), dtype=torch.bfloat16, device=gpu))
+    with pytest.raises(nat.Se12Error):
+        k.multiply(torch.zeros((1, 512), dtype=torch.bfloat16, device=gpu),
+                   launch=LaunchConfiguration(ThreadsPerBlock(96), BlockCount(4)))
+    with pytest.raises(nat.Se12Error):
+        k.multiply(torch.zeros((1, 512), dtype=torch.bfloat16, device=gpu),
+                   launch=LaunchConfiguration(ThreadsPerBlock(64), BlockCount(5)))

@@ -235,23 +235,38 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
     return SE12_OK;
 }
 
-// The default launch, re-derived for MI355X: 4 waves per block (fewer when
-// a tile row has fewer K tiles), and enough K splits that the grid holds
-// about 8 waves per CU, each wave keeping >= 1 tile; more splits when the
-// block's slice of x would not fit the LDS budget.
+// The default launch, re-derived for MI355X (256 CUs x 4 SIMDs, wave64; the
+// batch-1 kernel runs 4 waves per SIMD, i.e. 16 waves per CU):
+//  - many tile rows (>= 2 per CU): 4 waves per block, no K split - the grid
+//    alone fills the CUs;
+//  - fewer tile rows: one block per tile row with as many waves as K tiles
+//    (up to 16), halved until every block is resident at once, so the K
+//    reduction stays inside the block (DPP + LDS) and each wave owns few tiles;
+//  - only when even that leaves fewer than ~1024 waves (very few rows with
+//    long K) are the K tiles also split across blocks (last-block reduction);
+//  - more splits while the block's slice of x exceeds its share of the LDS.
 static void default_launch(const se12_handle* h, int32_t batch, bool xf32, int32_t* waves_out, int32_t* splits_out) {
     const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
-    const int32_t waves = std::max<int32_t>(1, std::min<int32_t>(4, h->TC));
-    const int64_t target_waves = (int64_t)h->cu_count * 8;
-    int64_t splits = ceil_div(target_waves, (int64_t)h->TR * waves);
-    splits = std::min<int64_t>(splits, std::max<int64_t>(1, h->TC / waves));
-    splits = std::max<int64_t>(splits, 1);
+    const int64_t mw = gemv_max_waves(bl, xf32);
+    const int64_t cus = std::max<int32_t>(1, h->cu_count);
+    const int64_t target_waves = cus * 8;
+    const int64_t tr = h->TR, tc = h->TC;
+    int64_t waves, splits = 1;
+    if (tr >= 2 * cus) {
+        waves = std::min<int64_t>(std::min<int64_t>(4, tc), mw);
+    } else {
+        waves = std::min<int64_t>(mw, tc);
+        while (waves > 1 && tr > cus * std::max<int64_t>(1, 16 / waves)) waves = (waves + 1) / 2;
+        while (tr * splits * waves < target_waves / 2 && splits * 2 * waves <= tc && splits * 2 <= h->s_cap)
+            splits *= 2;
+    }
+    const int64_t blocks_per_cu = std::max<int64_t>(1, 16 / waves);
+    const int64_t budget = std::max<int64_t>(kLdsBudget, std::min<int64_t>(h->lds_per_block, 160 * 1024 / blocks_per_cu));
     while (splits < h->s_cap &&
-           gemv_lds_bytes(waves, bl, (int)ceil_div(h->TC, splits) * SE12_TILE_COLS, xf32) > kLdsBudget)
+           (int64_t)gemv_lds_bytes((int)waves, bl, (int)ceil_div(tc, splits) * SE12_TILE_COLS, xf32) > budget)
         ++splits;
-    splits = std::min<int64_t>(splits, h->s_cap);
-    *waves_out = waves;
-    *splits_out = (int32_t)splits;
+    *waves_out = (int32_t)waves;
+    *splits_out = (int32_t)std::min<int64_t>(splits, h->s_cap);
 }
 
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
@@ -274,10 +289,11 @@ int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, flo
     const bool xf32 = x_dtype == SE12_X_F32;
     int32_t waves, splits;
     if (launch) {
-        if (launch->threads_per_block < 64 || launch->threads_per_block > kGemvMaxThreads ||
+        const int max_threads = 64 * gemv_max_waves(std::min<int32_t>(batch, kGemvMaxBatchPerLaunch), xf32);
+        if (launch->threads_per_block < 64 || launch->threads_per_block > max_threads ||
             launch->threads_per_block % 64 != 0)
-            return fail(SE12_E_INVALID, "se12_gemv: threads_per_block %d must be a multiple of 64 in [64, %d]",
-                        launch->threads_per_block, kGemvMaxThreads);
+            return fail(SE12_E_INVALID, "se12_gemv: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d",
+                        launch->threads_per_block, max_threads, batch);
         if (launch->blocks <= 0 || launch->blocks % h->TR != 0)
             return fail(SE12_E_INVALID, "se12_gemv: blocks %d must be a positive multiple of the %d tile rows",
                         launch->blocks, h->TR);

@@ -34,8 +34,9 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
                                             Sink&& sink) {
     TileLoads t;
     load_tile(t, a.sm, a.ec, a.esc, a.fb_rank, tile, lane);
-    if (t.fallback_rank >= 0) {
-        const int16_t* raw = a.fb_raw + (int64_t)t.fallback_rank * kTile;
+    const int32_t frank = uniform_rank(t);
+    if (frank >= 0) {
+        const int16_t* raw = a.fb_raw + (int64_t)frank * kTile;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];

@@ -158,29 +158,18 @@ __device__ __forceinline__ void decode_chunk(const uint32_t* lut, uint4 sm, uint
     w[7] = merge_pair(pat[7], dup_hi(sm.w));
 }
 
-// One tile's loads for one lane.
+// One tile's loads for one lane. The per-tile escape slots and fallback rank
+// are wave-uniform but loaded like the rest (vector loads of one address):
+// scalar loads here would be waited for as soon as the prefetch is issued.
 struct TileLoads {
     uint4 sm[4];
     uint2 ec[4];
-    uint4 esc;             // wave-uniform (scalar load)
-    int32_t fallback_rank; // wave-uniform: rank among fallback tiles, or -1
+    uint4 esc;
+    int32_t fallback_rank;  // rank among fallback tiles, or -1
 };
-
-typedef __attribute__((address_space(4))) const uint32_t ku32;
-typedef __attribute__((address_space(4))) const int32_t ki32;
-
-// wave-uniform reads through the scalar cache (the tile index is uniform)
-__device__ __forceinline__ uint4 tile_esc(const uint8_t* esc, int64_t tile) {
-    ku32* p = (ku32*)(esc + tile * kEscBudget);
-    return make_uint4(p[0], p[1], p[2], p[3]);
-}
 
 // the bind-time sidecar: rank of the tile among fallback tiles, -1 if the tile
 // is not a fallback tile
-__device__ __forceinline__ int32_t tile_fallback_rank(const int32_t* rank, int64_t tile) {
-    return ((ki32*)rank)[tile];
-}
-
 __device__ __forceinline__ void load_tile(TileLoads& t, const uint8_t* sm, const uint8_t* ec, const uint8_t* esc,
                                           const int32_t* fb_rank, int64_t tile, uint32_t lane) {
     const uint8_t* smt = sm + tile * kTile + 16u * lane;
@@ -190,8 +179,13 @@ __device__ __forceinline__ void load_tile(TileLoads& t, const uint8_t* sm, const
         t.sm[j] = *reinterpret_cast<const uint4*>(smt + 1024 * j);
         t.ec[j] = *reinterpret_cast<const uint2*>(ect + 512 * j);
     }
-    t.esc = tile_esc(esc, tile);
-    t.fallback_rank = tile_fallback_rank(fb_rank, tile);
+    t.esc = *reinterpret_cast<const uint4*>(esc + tile * kEscBudget);
+    t.fallback_rank = fb_rank[tile];
+}
+
+// the (uniform) fallback rank of a loaded tile, in a scalar register
+__device__ __forceinline__ int32_t uniform_rank(const TileLoads& t) {
+    return __builtin_amdgcn_readfirstlane(t.fallback_rank);
 }
 
 // Raw BF16 pairs of chunk j of a fallback tile (tile-local order, like sm).

@@ -52,33 +52,62 @@ __device__ __forceinline__ void load_raw_tile(RawLoads& t, const uint16_t* w, in
     }
 }
 
+// Stages x[b, kb*256 .. ke*256) (zero past K) into LDS. Each thread issues up
+// to kStageUnroll 16-byte loads before its first LDS store, so a block pays
+// one memory round trip per kStageUnroll * threads items, not one per item.
+constexpr int kStageUnroll = 8;
+
 template <int B, bool XF32>
 __device__ __forceinline__ void stage_x(void* xs_raw, const GemvArgs& a, int kb, int ke, int tid, int nthreads) {
+    constexpr int EPI = XF32 ? 4 : 8;  // elements per 16-byte item
     const int ncols = (ke - kb) * kTileCols;
-    const int groups = ncols / 8;  // 8 elements per item
+    const int per_row = ncols / EPI;
+    const int total = B * per_row;
     const int64_t c0 = (int64_t)kb * kTileCols;
-    for (int i = tid; i < B * groups; i += nthreads) {
-        const int b = i / groups;
-        const int c = (i - b * groups) * 8;
-        const int64_t g = c0 + c;
-        if constexpr (XF32) {
-            const float* x = static_cast<const float*>(a.x) + (int64_t)b * a.K;
-            float* xs = static_cast<float*>(xs_raw) + (int64_t)b * a.xstride + c;
-            if (a.x_vec_ok && g + 8 <= a.K) {
-                reinterpret_cast<float4*>(xs)[0] = reinterpret_cast<const float4*>(x + g)[0];
-                reinterpret_cast<float4*>(xs)[1] = reinterpret_cast<const float4*>(x + g)[1];
-            } else {
+    for (int base = 0; base < total; base += nthreads * kStageUnroll) {
+        uint4 v[kStageUnroll];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xs[e] = (g + e < a.K) ? x[g + e] : 0.0f;
+        for (int u = 0; u < kStageUnroll; ++u) {
+            const int i = base + u * nthreads + tid;
+            if (i < total) {
+                const int b = i / per_row;
+                const int c = (i - b * per_row) * EPI;
+                const int64_t g = c0 + c;
+                if constexpr (XF32) {
+                    const float* x = static_cast<const float*>(a.x) + (int64_t)b * a.K;
+                    if (a.x_vec_ok && g + EPI <= a.K) {
+                        v[u] = *reinterpret_cast<const uint4*>(x + g);
+                    } else {
+                        uint32_t e[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) e[q] = (g + q < a.K) ? __float_as_uint(x[g + q]) : 0u;
+                        v[u] = make_uint4(e[0], e[1], e[2], e[3]);
+                    }
+                } else {
+                    const uint16_t* x = static_cast<const uint16_t*>(a.x) + (int64_t)b * a.K;
+                    if (a.x_vec_ok && g + EPI <= a.K) {
+                        v[u] = *reinterpret_cast<const uint4*>(x + g);
+                    } else {
+                        uint32_t e[4];
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const uint32_t lo = (g + 2 * q < a.K) ? (uint32_t)x[g + 2 * q] : 0u;
+                            const uint32_t hi = (g + 2 * q + 1 < a.K) ? (uint32_t)x[g + 2 * q + 1] : 0u;
+                            e[q] = lo | (hi << 16);
+                        }
+                        v[u] = make_uint4(e[0], e[1], e[2], e[3]);
+                    }
+                }
             }
-        } else {
-            const uint16_t* x = static_cast<const uint16_t*>(a.x) + (int64_t)b * a.K;
-            uint16_t* xs = static_cast<uint16_t*>(xs_raw) + (int64_t)b * a.xstride + c;
-            if (a.x_vec_ok && g + 8 <= a.K) {
-                *reinterpret_cast<uint4*>(xs) = *reinterpret_cast<const uint4*>(x + g);
-            } else {
+        }
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xs[e] = (g + e < a.K) ? x[g + e] : (uint16_t)0;
+        for (int u = 0; u < kStageUnroll; ++u) {
+            const int i = base + u * nthreads + tid;
+            if (i < total) {
+                const int b = i / per_row;
+                const int c = (i - b * per_row) * EPI;
+                char* dst = static_cast<char*>(xs_raw) + ((int64_t)b * a.xstride + c) * (XF32 ? 4 : 2);
+                *reinterpret_cast<uint4*>(dst) = v[u];
             }
         }
     }
@@ -147,8 +176,9 @@ __device__ __forceinline__ void se12_tile(const GemvArgs& a, const TileLoads& t,
     constexpr bool tail = TAIL;
     const int lim = (int)(a.K - (int64_t)kt * kTileCols);
     const int c0 = 16 * (int)(lane & 15u);
-    if (t.fallback_rank >= 0) {
-        const int16_t* raw = a.fb_raw + (int64_t)t.fallback_rank * kTile;
+    const int32_t frank = uniform_rank(t);
+    if (frank >= 0) {
+        const int16_t* raw = a.fb_raw + (int64_t)frank * kTile;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
@@ -188,7 +218,7 @@ __device__ __forceinline__ void raw_tile(const GemvArgs& a, const RawLoads& t, c
 // PF: keep the next tile's loads in flight while the current one is used
 // (two load buffers); launches with one tile per wave use PF = false.
 template <int B, bool XF32, bool RAW, bool PF>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(64 * gemv_max_waves(B, XF32)) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     const int nthreads = blockDim.x;
     const int W = nthreads >> 6;
@@ -211,27 +241,39 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[j][b] = 0.0f;
 
+    // The prefetch is issued unconditionally (the last iteration re-reads the
+    // current tile) so the compiler's wait counts stay exact: a conditional
+    // prefetch makes it wait for every outstanding load at the merge point.
     int kt = kb + w;
     if constexpr (RAW) {
         RawLoads t0, t1;
-        if (kt < ke) load_raw_tile(t0, a.wraw, a.N, a.K, tr, kt, lane, a.w_vec_ok);
+        const bool has = kt < ke;
+        if (has) load_raw_tile(t0, a.wraw, a.N, a.K, tr, kt, lane, a.w_vec_ok);
         stage_x<B, XF32>(xs, a, kb, ke, tid, nthreads);
         lds_barrier();
-        if constexpr (PF) {
-            while (kt < ke) {
-                if (kt + W < ke) load_raw_tile(t1, a.wraw, a.N, a.K, tr, kt + W, lane, a.w_vec_ok);
-                raw_tile<B, XF32>(a, t0, xs, kb, kt, lane, acc);
-                kt += W;
-                if (kt >= ke) break;
-                if (kt + W < ke) load_raw_tile(t0, a.wraw, a.N, a.K, tr, kt + W, lane, a.w_vec_ok);
-                raw_tile<B, XF32>(a, t1, xs, kb, kt, lane, acc);
-                kt += W;
-            }
-        } else {
-            while (kt < ke) {
-                raw_tile<B, XF32>(a, t0, xs, kb, kt, lane, acc);
-                kt += W;
-                if (kt < ke) load_raw_tile(t0, a.wraw, a.N, a.K, tr, kt, lane, a.w_vec_ok);
+        if (has) {
+            if constexpr (PF) {
+                while (true) {
+                    int kn = kt + W;
+                    bool more = kn < ke;
+                    load_raw_tile(t1, a.wraw, a.N, a.K, tr, more ? kn : kt, lane, a.w_vec_ok);
+                    raw_tile<B, XF32>(a, t0, xs, kb, kt, lane, acc);
+                    if (!more) break;
+                    kt = kn;
+                    kn = kt + W;
+                    more = kn < ke;
+                    load_raw_tile(t0, a.wraw, a.N, a.K, tr, more ? kn : kt, lane, a.w_vec_ok);
+                    raw_tile<B, XF32>(a, t1, xs, kb, kt, lane, acc);
+                    if (!more) break;
+                    kt = kn;
+                }
+            } else {
+                while (true) {
+                    raw_tile<B, XF32>(a, t0, xs, kb, kt, lane, acc);
+                    kt += W;
+                    if (kt >= ke) break;
+                    load_raw_tile(t0, a.wraw, a.N, a.K, tr, kt, lane, a.w_vec_ok);
+                }
             }
         }
     } else {
@@ -240,25 +282,34 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         const int kem = peel ? ke - 1 : ke;
         TileLoads t0, t1;
         const int64_t row_tiles = (int64_t)tr * a.TC;
-        if (kt < kem) load_tile(t0, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + kt, lane);
+        const bool has = kt < kem;
+        if (has) load_tile(t0, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + kt, lane);
         build_pair_lut(lut, a.codebook, tid, nthreads);
         stage_x<B, XF32>(xs, a, kb, ke, tid, nthreads);
         lds_barrier();
-        if constexpr (PF) {
-            while (kt < kem) {
-                if (kt + W < kem) load_tile(t1, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + kt + W, lane);
-                se12_tile<B, XF32, false>(a, t0, lut, xs, kb, kt, lane, acc);
-                kt += W;
-                if (kt >= kem) break;
-                if (kt + W < kem) load_tile(t0, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + kt + W, lane);
-                se12_tile<B, XF32, false>(a, t1, lut, xs, kb, kt, lane, acc);
-                kt += W;
-            }
-        } else {
-            while (kt < kem) {
-                se12_tile<B, XF32, false>(a, t0, lut, xs, kb, kt, lane, acc);
-                kt += W;
-                if (kt < kem) load_tile(t0, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + kt, lane);
+        if (has) {
+            if constexpr (PF) {
+                while (true) {
+                    int kn = kt + W;
+                    bool more = kn < kem;
+                    load_tile(t1, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + (more ? kn : kt), lane);
+                    se12_tile<B, XF32, false>(a, t0, lut, xs, kb, kt, lane, acc);
+                    if (!more) break;
+                    kt = kn;
+                    kn = kt + W;
+                    more = kn < kem;
+                    load_tile(t0, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + (more ? kn : kt), lane);
+                    se12_tile<B, XF32, false>(a, t1, lut, xs, kb, kt, lane, acc);
+                    if (!more) break;
+                    kt = kn;
+                }
+            } else {
+                while (true) {
+                    se12_tile<B, XF32, false>(a, t0, lut, xs, kb, kt, lane, acc);
+                    kt += W;
+                    if (kt >= kem) break;
+                    load_tile(t0, a.sm, a.ec, a.esc, a.fb_rank, row_tiles + kt, lane);
+                }
             }
         }
         if (peel && (a.TC - 1 - kb) % W == w) {
@@ -288,23 +339,30 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
         if (tid < 16 * B && n < a.N) a.y[(int64_t)b * a.N + n] = v;
         return;
     }
-    if (tid < 16 * B) a.partial[((int64_t)s * B + b) * a.Np + n] = v;
-    __threadfence();
+    // Cross-block reduction without cache-wide maintenance: the partials are
+    // written with device-scope (sc1) stores, each thread waits for its stores
+    // to complete before the block's arrival is counted, and the last block
+    // reads them back with device-scope loads. (A __threadfence() here would
+    // write back and invalidate the whole L2 of the XCD for every block.)
+    if (tid < 16 * B)
+        __hip_atomic_store(&a.partial[((int64_t)s * B + b) * a.Np + n], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     int* last = reinterpret_cast<int*>(red);
     if (tid == 0) {
-        const int old = atomicAdd(&a.counters[tr], 1);
+        const int old = __hip_atomic_fetch_add(&a.counters[tr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         *last = (old == S - 1) ? 1 : 0;
     }
     __syncthreads();
     if (*last) {
-        __threadfence();
         if (tid < 16 * B) {
             float sum = 0.0f;
-            for (int ss = 0; ss < S; ++ss) sum += a.partial[((int64_t)ss * B + b) * a.Np + n];
+            for (int ss = 0; ss < S; ++ss)
+                sum += __hip_atomic_load(&a.partial[((int64_t)ss * B + b) * a.Np + n], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
             if (n < a.N) a.y[(int64_t)b * a.N + n] = sum;
         }
-        if (tid == 0) a.counters[tr] = 0;
+        if (tid == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

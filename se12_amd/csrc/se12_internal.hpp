@@ -62,7 +62,9 @@ struct EncodeArgs {
 };
 
 constexpr int kGemvMaxBatchPerLaunch = 4;
-constexpr int kGemvMaxThreads = 256;
+// waves per block the kernel is compiled for: 16 (1024 threads, <= 128 VGPRs)
+// for batch 1 with BF16 x, 4 where more accumulators or FP32 x need registers
+constexpr int gemv_max_waves(int batch, bool xf32) { return (batch == 1 && !xf32) ? 16 : 4; }
 constexpr int kLutBytes = 1024;
 
 // bytes of dynamic LDS a GEMV launch needs

@@ -3,7 +3,7 @@
 Mirrors lws/domain/launch/heuristic.py:24-51 (LaunchConfiguration =
 threads_per_block + blocks) and lws/domain/launch/search_space.py:14-75
 (candidate set, best configuration, order-matched configuration), re-derived
-for this kernel's grid: a block is 1..4 wave64s working on one 16-row tile
+for this kernel's grid: a block is 1..16 wave64s working on one 16-row tile
 row, and `blocks` = tile_rows x k_splits, where the K tiles of a tile row are
 cut into `k_splits` contiguous ranges (the last block of a tile row to finish
 adds the splits in order). The default configuration itself is computed by
@@ -15,7 +15,7 @@ from __future__ import annotations
 import dataclasses
 
 WAVE_SIZE = 64
-THREADS_PER_BLOCK_CANDIDATES = (64, 128, 192, 256)
+THREADS_PER_BLOCK_CANDIDATES = (64, 128, 192, 256, 512, 576, 1024)
 MAX_K_SPLITS = 64
 
 
@@ -55,27 +55,36 @@ def configuration(waves: int, k_splits: int, output_rows: int) -> LaunchConfigur
     )
 
 
-def waves_and_splits(launch: LaunchConfiguration, output_rows: int) -> tuple[int, int]:
+def max_waves_per_block(batch: int, float32_activations: bool = False) -> int:
+    """16 wave64s (1024 threads) for batch 1 with BF16 x, else 4 (register budget)."""
+    return 16 if batch == 1 and not float32_activations else 4
+
+
+def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int = 1) -> tuple[int, int]:
     """(waves per block, K splits) of a configuration for a matrix with `output_rows` rows."""
     tr = tile_rows(output_rows)
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
-    if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= 256:
-        raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, 256]")
+    hi = WAVE_SIZE * max_waves_per_block(min(batch, 4))
+    if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= hi:
+        raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {hi}]")
     if blocks <= 0 or blocks % tr:
         raise ValueError(f"blocks {blocks} must be a positive multiple of the {tr} tile rows")
     return tpb // WAVE_SIZE, blocks // tr
 
 
-def candidate_configurations(output_rows: int, k: int) -> tuple[LaunchConfiguration, ...]:
-    """Every (waves, splits) worth timing: 1..4 waves, splits 1..K tiles (powers
-    of two and the exact K tile count), never more waves than K tiles per
-    split (search_space.py:17-19 enumerates threads per block the same way)."""
+def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_activations: bool = False) -> tuple[LaunchConfiguration, ...]:
+    """Every (waves, splits) worth timing: waves per block up to the batch's
+    limit, splits 1..K tiles, never more waves than K tiles per split
+    (search_space.py:17-19 enumerates threads per block the same way)."""
     tc = k_tiles(k)
     splits = sorted({s for s in (1, 2, 3, 4, 6, 8, 9, 12, 16, 18, 24, 32, 36, 48, 64) if s <= min(tc, MAX_K_SPLITS)} | {1})
+    mw = max_waves_per_block(min(batch, 4), float32_activations)
     out = []
     for tpb in THREADS_PER_BLOCK_CANDIDATES:
         waves = tpb // WAVE_SIZE
+        if waves > mw:
+            continue
         for s in splits:
             if waves <= -(-tc // s):
                 out.append(configuration(waves, s, output_rows))

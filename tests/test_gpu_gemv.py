@@ -41,13 +41,13 @@ def test_gemv_golden_vectors(gpu, name, batch):
 
     g = load_golden(name)
     enc = golden_as_encoding(g)
-    if name in ("edge_1x214", "uniform_33x300"):
+    w = o.bf16_bits_to_f32(o.decode(enc))
+    if not np.isfinite(w).all() or np.abs(w).max() > 1e30:
         # inf/NaN/huge weights: a row with a NaN weight must give NaN; rows of
         # finite weights whose sum is finite in float64 and float32 must match
         k = Se12MatVecKernel(to_device(enc, gpu))
         xb = _x(batch, g["cols"], seed=1)
         y = k.multiply(bf16_tensor(xb, gpu)).cpu().numpy()
-        w = o.bf16_bits_to_f32(o.decode(enc))
         ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
         ref64 = o.gemv_reference(enc, o.bf16_bits_to_f32(xb), fp64=True)
         nan_rows = np.isnan(w).any(axis=1)
@@ -140,10 +140,10 @@ def test_gemv_padding_of_an_infinite_codebook0_is_masked(gpu):
     assert np.array_equal(np.isnan(y[:, :16]), np.isnan(ref[:, :16]))
 
 
-def _configs(rows, cols):
+def _configs(rows, cols, batch=1):
     from se12_amd.launch import candidate_configurations
 
-    return candidate_configurations(rows, cols)
+    return candidate_configurations(rows, cols, batch=batch)
 
 
 def test_every_launch_configuration_is_correct_and_deterministic(gpu):
@@ -155,12 +155,28 @@ def test_every_launch_configuration_is_correct_and_deterministic(gpu):
     xb = _x(2, 2800, seed=32)
     x = bf16_tensor(xb, gpu)
     ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
-    for cfg in _configs(272, 2800):
+    for cfg in _configs(272, 2800, batch=2):
         y1 = k.multiply(x, launch=cfg).clone()
         y2 = k.multiply(x, launch=cfg)
         torch.cuda.synchronize()
         assert torch.equal(y1, y2), cfg
         assert max_rel_error(y1, ref) <= REL_TOL, cfg
+
+
+def test_every_batch1_launch_configuration(gpu):
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits = heavy_tailed_bf16(2304, 9216, seed=33)
+    enc = o.encode(bits.reshape(-1), 2304, 9216)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    xb = _x(1, 9216, seed=34)
+    x = bf16_tensor(xb, gpu)
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+    cfgs = _configs(2304, 9216, batch=1)
+    assert any(c.threads_per_block.value == 1024 for c in cfgs)
+    for cfg in cfgs:
+        y = k.multiply(x, launch=cfg)
+        assert max_rel_error(y, ref) <= REL_TOL, cfg
 
 
 @pytest.mark.parametrize("shape", [(2304, 9216), (272, 2800), (48, 768)])
@@ -178,7 +194,8 @@ def test_raw_twin_is_bit_identical_under_one_launch(gpu, shape):
     raw = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
     for batch in (1, 4, 6):
         x = bf16_tensor(_x(batch, cols, seed=batch), gpu)
-        cfgs = [None] + list(_configs(rows, cols))[:: max(1, len(_configs(rows, cols)) // 6)]
+        all_cfgs = list(_configs(rows, cols, batch=batch))
+        cfgs = [None] + all_cfgs[:: max(1, len(all_cfgs) // 6)] + all_cfgs[-2:]
         for cfg in cfgs:
             assert torch.equal(fused.multiply(x, launch=cfg), raw.multiply(x, launch=cfg)), (batch, cfg)
 

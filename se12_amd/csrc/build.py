@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import os
 import pathlib
+import re
 import shutil
 import subprocess
 import sys
@@ -37,6 +38,22 @@ HIP_FLAGS = [
 ]
 
 
+def spilling_kernels(remarks: str) -> list[str]:
+    """Kernels that hipcc's resource-usage remarks report as spilling VGPRs or
+    using scratch memory: a launch bound set too high for the variant. (SGPR
+    spills land in VGPR lanes, not memory, and are not counted.)"""
+    bad, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s+(VGPRs Spill|ScratchSize \[bytes/lane\]): (\d+)", line)
+        if m and name and int(m.group(2)) > 0 and name not in bad:
+            bad.append(name)
+    return bad
+
+
 def hipcc() -> str:
     path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(path):
@@ -59,21 +76,25 @@ def build(verbose: bool = False) -> pathlib.Path:
     for src in SOURCES:
         obj = objdir / (src + ".o")
         objects.append(obj)
-        cmd = [cc, *HIP_FLAGS, "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
-    failed = []
+    failed, spills = [], []
     for src, p in procs:
         out, _ = p.communicate()
-        lines = [ln for ln in out.splitlines() if "packed-fp32-ops" not in ln]
+        lines = [ln for ln in out.splitlines() if "packed-fp32-ops" not in ln and "remark:" not in ln
+                 and not ln.lstrip().startswith(("|", "^")) and not re.match(r"\s*\d+ \|", ln)]
         if p.returncode != 0:
             failed.append(src)
             sys.stderr.write("\n".join(lines) + "\n")
         elif verbose and lines:
             print("\n".join(lines))
+        spills += spilling_kernels(out)
     if failed:
         raise RuntimeError(f"hipcc failed on {', '.join(failed)}")
+    if spills:
+        raise RuntimeError(f"kernels spill registers or use scratch (lower their launch bounds): {', '.join(spills)}")
     tmp = LIBDIR / (LIBNAME + ".tmp")
     link = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp)]
     if verbose:

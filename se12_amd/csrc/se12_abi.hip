@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "se12_gfx950.h"
+#include "se12_device.hpp"
 #include "se12_internal.hpp"
 
 using namespace se12;
@@ -58,7 +59,6 @@ struct DeviceScope {
 };
 
 constexpr int32_t kMaxSplits = 64;
-constexpr size_t kLdsBudget = 64 * 1024;  // per block, leaves room for 2+ blocks per CU
 
 }  // namespace
 
@@ -69,7 +69,8 @@ struct se12_handle {
     int32_t TR, TC;
     se12_streams s;
     const uint16_t* wraw;
-    int32_t* fb_rank;
+    uint32_t* info;      // [T] per-tile sidecar word
+    uint32_t* lut;       // [256] pair table
     int64_t n_fallback;
     float* partial;
     int32_t* counters;
@@ -77,7 +78,6 @@ struct se12_handle {
     int32_t s_cap;
     int32_t cu_count;
     int64_t lds_per_block;
-    int32_t codebook0;  // first codebook entry: the exponent every padding weight decodes to
 };
 
 extern "C" {
@@ -134,7 +134,8 @@ static int bind_common(se12_handle* h, int64_t rows, int64_t cols, int32_t max_b
 
 static void free_handle(se12_handle* h) {
     if (!h) return;
-    if (h->fb_rank) (void)hipFree(h->fb_rank);
+    if (h->info) (void)hipFree(h->info);
+    if (h->lut) (void)hipFree(h->lut);
     if (h->partial) (void)hipFree(h->partial);
     if (h->counters) (void)hipFree(h->counters);
     delete h;
@@ -142,8 +143,10 @@ static void free_handle(se12_handle* h) {
 
 static int check_shape(int64_t rows, int64_t cols, int32_t max_batch) {
     if (rows <= 0 || cols <= 0) return fail(SE12_E_INVALID, "shape must be positive, got [%lld, %lld]", (long long)rows, (long long)cols);
-    if (ceil_div(rows, SE12_TILE_ROWS) > INT32_MAX / 2 || ceil_div(cols, SE12_TILE_COLS) > INT32_MAX / 2)
-        return fail(SE12_E_INVALID, "shape too large");
+    // tile rows index the grid's x dimension; K-tile bounds are computed in
+    // 32 bits as split * tile_cols
+    if (ceil_div(rows, SE12_TILE_ROWS) > INT32_MAX / 2 || ceil_div(cols, SE12_TILE_COLS) > (1 << 25))
+        return fail(SE12_E_INVALID, "shape [%lld, %lld] too large", (long long)rows, (long long)cols);
     if (max_batch < 1 || max_batch > SE12_MAX_BATCH)
         return fail(SE12_E_INVALID, "max_batch must be in [1, %d], got %d", SE12_MAX_BATCH, max_batch);
     return SE12_OK;
@@ -174,15 +177,21 @@ int se12_bind(const se12_streams* s, int64_t rows, int64_t cols, int32_t max_bat
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     int64_t* total_dev = nullptr;
-    hipError_t e = hipMalloc(&h->fb_rank, (size_t)h->T * sizeof(int32_t));
-    if (e == hipSuccess) e = hipMalloc(&total_dev, sizeof(int64_t));
-    if (e == hipSuccess) e = launch_fallback_rank_from_bitmap(s->fallback_bitmap_dev, h->T, h->fb_rank, total_dev, st);
     int64_t total = 0;
+    uint8_t cb[SE12_CODEBOOK_SIZE] = {0};
+    uint32_t lut[256];
+    hipError_t e = hipMalloc(&h->info, (size_t)h->T * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&h->lut, sizeof lut);
+    if (e == hipSuccess) e = hipMalloc(&total_dev, sizeof(int64_t));
+    if (e == hipSuccess) e = launch_tile_info(s->fallback_bitmap_dev, s->ec_dev, h->T, h->info, total_dev, st);
     if (e == hipSuccess) e = hipMemcpyAsync(&total, total_dev, sizeof total, hipMemcpyDeviceToHost, st);
-    uint8_t cb0 = 0;
-    if (e == hipSuccess) e = hipMemcpyAsync(&cb0, s->codebook_dev, 1, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(cb, s->codebook_dev, sizeof cb, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
-    h->codebook0 = cb0;
+    if (e == hipSuccess) {
+        for (uint32_t b = 0; b < 256; ++b) lut[b] = pair_lut_entry(cb, b);
+        e = hipMemcpyAsync(h->lut, lut, sizeof lut, hipMemcpyHostToDevice, st);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (total_dev) (void)hipFree(total_dev);
     if (e != hipSuccess) {
         free_handle(h);
@@ -235,48 +244,96 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
     return SE12_OK;
 }
 
-// The default launch, re-derived for MI355X (256 CUs x 4 SIMDs, wave64; the
-// batch-1 kernel runs 4 waves per SIMD, i.e. 16 waves per CU):
-//  - many tile rows (>= 2 per CU): 4 waves per block, no K split - the grid
-//    alone fills the CUs;
-//  - fewer tile rows: one block per tile row with as many waves as K tiles
-//    (up to 16), halved until every block is resident at once, so the K
-//    reduction stays inside the block (DPP + LDS) and each wave owns few tiles;
-//  - only when even that leaves fewer than ~1024 waves (very few rows with
-//    long K) are the K tiles also split across blocks (last-block reduction);
-//  - more splits while the block's slice of x exceeds its share of the LDS.
-static void default_launch(const se12_handle* h, int32_t batch, bool xf32, int32_t* waves_out, int32_t* splits_out) {
+// Largest block (threads) a launch at batch `bl` may use: the lightest
+// kernel variant (one tile per round, no prefetch) of the fused kernel and of
+// its raw twin must fit its VGPR budget.
+static int max_threads_for(int32_t bl, bool xf32, bool generic) {
+    return std::min(gemv_max_threads(bl, xf32, false, 1, false, generic), gemv_max_threads(bl, xf32, true, 1, false, generic));
+}
+
+// The default launch, re-derived for MI355X (256 CUs in 8 XCDs, wave64) from
+// a sweep of every (waves, splits) pair on cold data at the Gemma-2 2B/9B/27B
+// shapes. A batch-1 GEMV is one pass over the streams; the cross-block K
+// reduction (S > 1) adds a store -> counter -> reload round trip to the end of
+// every block, so a block covers a whole tile row whenever that still spreads
+// the work:
+//  - fewer tile rows than CUs: one wave per K tile (at most 16 waves), S = 1;
+//    only very long K rows on very few tile rows are split, so that every CU
+//    gets a block;
+//  - at least one tile row per CU: 4 waves (2-3 tiles each) for short rows,
+//    8 for rows of 13-32 tiles, and for longer rows 4 waves with the row cut
+//    into splits of about 24 tiles, which balances the blocks over the CUs.
+static void default_launch(const se12_handle* h, int32_t batch, bool xf32, bool generic, int32_t* waves_out,
+                           int32_t* splits_out) {
     const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
-    const int64_t mw = gemv_max_waves(bl, xf32);
+    const int64_t mw = max_threads_for(bl, xf32, generic) / 64;
     const int64_t cus = std::max<int32_t>(1, h->cu_count);
-    const int64_t target_waves = cus * 8;
     const int64_t tr = h->TR, tc = h->TC;
     int64_t waves, splits = 1;
-    if (tr >= 2 * cus) {
-        waves = std::min<int64_t>(std::min<int64_t>(4, tc), mw);
+    if (tr < cus) {
+        waves = std::min<int64_t>(16, tc);
+        if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
+    } else if (tc <= 12) {
+        waves = std::min<int64_t>(4, tc);
+    } else if (tc <= 32) {
+        waves = 8;
     } else {
-        waves = std::min<int64_t>(mw, tc);
-        while (waves > 1 && tr > cus * std::max<int64_t>(1, 16 / waves)) waves = (waves + 1) / 2;
-        while (tr * splits * waves < target_waves / 2 && splits * 2 * waves <= tc && splits * 2 <= h->s_cap)
-            splits *= 2;
+        waves = 4;
+        splits = std::max<int64_t>(1, (tc + 12) / 24);
     }
-    const int64_t blocks_per_cu = std::max<int64_t>(1, 16 / waves);
-    const int64_t budget = std::max<int64_t>(kLdsBudget, std::min<int64_t>(h->lds_per_block, 160 * 1024 / blocks_per_cu));
-    while (splits < h->s_cap &&
-           (int64_t)gemv_lds_bytes((int)waves, bl, (int)ceil_div(tc, splits) * SE12_TILE_COLS, xf32) > budget)
-        ++splits;
+    waves = std::max<int64_t>(1, std::min(waves, mw));
     *waves_out = (int32_t)waves;
-    *splits_out = (int32_t)std::min<int64_t>(splits, h->s_cap);
+    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(splits, h->s_cap));
 }
 
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
     if (!h || !out) return fail(SE12_E_INVALID, "se12_default_launch: NULL argument");
     if (batch < 1 || batch > SE12_MAX_BATCH) return fail(SE12_E_INVALID, "batch must be in [1, %d]", SE12_MAX_BATCH);
     int32_t waves, splits;
-    default_launch(h, batch, false, &waves, &splits);
+    const bool generic = h->K % SE12_TILE_COLS != 0 ||
+                         (h->format == SE12_FORMAT_RAW_BF16 && h->N % SE12_TILE_ROWS != 0);
+    default_launch(h, batch, false, generic, &waves, &splits);
     out->threads_per_block = waves * 64;
     out->blocks = h->TR * splits;
     return SE12_OK;
+}
+
+// Picks the kernel variant for a launch shape: all of a wave's tiles in one
+// round when they fit the block's VGPR budget, else rounds with the next one
+// prefetched, else plain rounds.
+static GemvPlan plan_gemv(const se12_handle* h, int32_t bl, bool xf32, bool generic, int32_t waves, int32_t splits) {
+    GemvPlan p{};
+    p.batch = bl;
+    p.xf32 = xf32;
+    p.raw = h->format == SE12_FORMAT_RAW_BF16;
+    p.generic = generic;
+    p.waves = waves;
+    p.blocks = h->TR * splits;
+    p.lds = gemv_lds_bytes(waves, bl);
+    const int threads = waves * 64;
+    const int64_t per_wave = ceil_div(ceil_div(h->TC, splits), waves);
+    auto fits = [&](int g, bool pf) { return threads <= gemv_max_threads(bl, xf32, p.raw, g, pf, false); };
+    if (generic) {
+        p.g = 1;
+        p.pf = false;
+        return p;
+    }
+    if (per_wave <= 4 && fits((int)per_wave, false)) {
+        p.g = (int)per_wave;
+        p.pf = false;
+        return p;
+    }
+    if (fits(2, true) && per_wave >= 4) {
+        p.g = 2;
+        p.pf = true;
+    } else if (fits(1, true)) {
+        p.g = 1;
+        p.pf = true;
+    } else {
+        p.g = 1;
+        p.pf = false;
+    }
+    return p;
 }
 
 int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, const se12_launch* launch,
@@ -287,9 +344,16 @@ int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, flo
     if (batch < 1 || batch > h->max_batch)
         return fail(SE12_E_INVALID, "se12_gemv: batch %d outside [1, %d] (the handle's max_batch)", batch, h->max_batch);
     const bool xf32 = x_dtype == SE12_X_F32;
+    const bool raw = h->format == SE12_FORMAT_RAW_BF16;
+    const size_t esize = xf32 ? 4 : 2;
+    // FAST kernels need whole K tiles and 16-byte aligned BF16 rows of x (and,
+    // for the raw twin, whole tile rows of an aligned W); the rest run GENERIC
+    const bool generic = xf32 || h->K % SE12_TILE_COLS != 0 || !aligned16(x) ||
+                         (raw && (h->N % SE12_TILE_ROWS != 0 || !aligned16(h->wraw)));
+    const int32_t b_first = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
     int32_t waves, splits;
     if (launch) {
-        const int max_threads = 64 * gemv_max_waves(std::min<int32_t>(batch, kGemvMaxBatchPerLaunch), xf32);
+        const int max_threads = max_threads_for(b_first, xf32, generic);
         if (launch->threads_per_block < 64 || launch->threads_per_block > max_threads ||
             launch->threads_per_block % 64 != 0)
             return fail(SE12_E_INVALID, "se12_gemv: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d",
@@ -302,28 +366,21 @@ int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, flo
         if (splits > h->s_cap)
             return fail(SE12_E_CAPACITY, "se12_gemv: %d K splits exceed the handle's limit %d", splits, h->s_cap);
     } else {
-        default_launch(h, batch, xf32, &waves, &splits);
+        default_launch(h, batch, xf32, generic, &waves, &splits);
     }
     DeviceScope ds;
     SE12_HIP(ds.enter(h->device));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const int64_t xstride = ceil_div(h->TC, splits) * SE12_TILE_COLS;
-    const size_t esize = xf32 ? 4 : 2;
     for (int32_t b0 = 0; b0 < batch; b0 += kGemvMaxBatchPerLaunch) {
         const int32_t bl = std::min<int32_t>(kGemvMaxBatchPerLaunch, batch - b0);
-        const size_t lds = gemv_lds_bytes(waves, bl, (int)xstride, xf32);
-        if ((int64_t)lds > h->lds_per_block)
-            return fail(SE12_E_CAPACITY, "se12_gemv: launch needs %zu bytes of LDS, the device allows %lld", lds,
-                        (long long)h->lds_per_block);
         GemvArgs a{};
         a.sm = h->s.sm_dev;
         a.ec = h->s.ec_dev;
         a.esc = h->s.esc_dev;
-        a.codebook = h->s.codebook_dev;
-        a.fb_rank = h->fb_rank;
+        a.lut = h->lut;
+        a.info = h->info;
         a.fb_raw = h->s.fallback_raw_dev;
         a.wraw = h->wraw;
-        a.mask_tail = (h->K % SE12_TILE_COLS != 0 && h->codebook0 == 255) ? 1 : 0;
         a.x = static_cast<const char*>(x) + (size_t)b0 * h->K * esize;
         a.y = y + (size_t)b0 * h->N;
         a.partial = h->partial;
@@ -334,10 +391,12 @@ int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, flo
         a.TR = h->TR;
         a.TC = h->TC;
         a.S = splits;
-        a.xstride = (int32_t)xstride;
-        a.x_vec_ok = (aligned16(a.x) && (xf32 ? h->K % 4 == 0 : h->K % 8 == 0)) ? 1 : 0;
-        a.w_vec_ok = (h->wraw && aligned16(h->wraw) && h->K % 8 == 0) ? 1 : 0;
-        hipError_t e = launch_gemv(a, bl, xf32, h->format == SE12_FORMAT_RAW_BF16, waves * 64, h->TR * splits, lds, st);
+        const bool gen = generic || !aligned16(a.x);
+        const GemvPlan p = plan_gemv(h, bl, xf32, gen, waves, splits);
+        if ((int64_t)(p.lds + kLutBytes) > h->lds_per_block)
+            return fail(SE12_E_CAPACITY, "se12_gemv: launch needs %zu bytes of LDS, the device allows %lld", p.lds,
+                        (long long)h->lds_per_block);
+        hipError_t e = launch_gemv(a, p, st);
         if (e != hipSuccess) return fail(SE12_E_HIP, "se12_gemv launch: %s", hipGetErrorString(e));
     }
     return SE12_OK;
@@ -350,7 +409,8 @@ static DecodeArgs decode_args(const se12_handle* h, uint16_t* out) {
     a.esc = h->s.esc_dev;
     a.codebook = h->s.codebook_dev;
     a.bitmap = h->s.fallback_bitmap_dev;
-    a.fb_rank = h->fb_rank;
+    a.lut = h->lut;
+    a.info = h->info;
     a.fb_raw = h->s.fallback_raw_dev;
     a.out = out;
     a.N = h->N;

@@ -6,10 +6,11 @@
 // (lws/adapters/cuda/kernels/se12_decode.cu:12-43,
 // lws/adapters/cuda/se12_decoder.py:147-185).
 //
-// Also here: the per-tile fallback rank (rank of a fallback tile among all
-// fallback tiles, cumsum(bitmap bits) - 1 as in lws/adapters/cuda/gemv.py:47-53,
-// and -1 for a tile that is not a fallback tile), computed once at bind time
-// by a single-block scan; the kernels read it instead of the bitmap.
+// Also here: the bind-time per-tile sidecar word. For a fallback tile it holds
+// the tile's rank among all fallback tiles (cumsum(bitmap bits) - 1, as in
+// lws/adapters/cuda/gemv.py:47-53, computed by a single-block scan); for any
+// other tile, which of its four 4-row chunks hold escape codes (one wave per
+// tile reads the tile's `ec` bytes). The kernels read it instead of the bitmap.
 #include "se12_device.hpp"
 #include "se12_internal.hpp"
 
@@ -32,11 +33,15 @@ __device__ __forceinline__ void store16(uint16_t* out_row, int64_t col, int64_t 
 template <typename Sink>
 __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t* lut, int64_t tile, uint32_t lane,
                                             Sink&& sink) {
+    TileSide side;
     TileLoads t;
-    load_tile(t, a.sm, a.ec, a.esc, a.fb_rank, tile, lane);
-    const int32_t frank = uniform_rank(t);
-    if (frank >= 0) {
-        const int16_t* raw = a.fb_raw + (int64_t)frank * kTile;
+    // lane 0: this tile's side data; other lanes: the next tile (clamped),
+    // which keeps the addresses lane-dependent (vector loads)
+    load_side(side, a.esc, a.info, (lane & 1u) && tile + 1 < a.T ? tile + 1 : tile);
+    load_tile(t, a.sm, a.ec, tile, lane);
+    const uint32_t info = side_info(side, 0);
+    if (info_is_fallback(info)) {
+        const int16_t* raw = a.fb_raw + (int64_t)info_rank(info) * kTile;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
@@ -44,11 +49,13 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
             sink(j, w);
         }
     } else {
-        uint32_t run = 0;
+        uint32_t pat[4][8];
+        lookup_tile(lut, t, pat);
+        if (info & 0xFu) resolve_tile_escapes(pat, t, info, side_esc(side, 0));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
-            decode_chunk(lut, t.sm[j], t.ec[j], t.esc, run, lane, w);
+            merge_chunk(pat[j], t.sm[j], w);
             sink(j, w);
         }
     }
@@ -56,11 +63,11 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
 
 template <bool ROWS>
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeArgs a) {
-    __shared__ uint32_t lut[256];
+    SE12_DECLARE_LUT(lut);
     const int tid = threadIdx.x;
     const uint32_t lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    build_pair_lut(lut, a.codebook, tid, blockDim.x);
+    store_block_lut(lut, reinterpret_cast<const uint4*>(a.lut)[lane], lane);
     lds_barrier();
 
     const int64_t item = (int64_t)blockIdx.x * kDecodeWaves + w;
@@ -105,7 +112,7 @@ hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream) {
 }
 
 // ---------------------------------------------------------------------------
-// fallback ranks from the bitmap (bind time, one block)
+// bind-time sidecar words
 // ---------------------------------------------------------------------------
 
 constexpr int kScanThreads = 1024;
@@ -127,8 +134,9 @@ __device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* tmp,
     return incl - v;
 }
 
-__global__ __launch_bounds__(kScanThreads) void fallback_rank_kernel(const uint8_t* bitmap, int64_t T,
-                                                                     int32_t* rank, int64_t* total_out) {
+// fallback tiles: kInfoFallback | rank; other tiles: 0 (escape bits come next)
+__global__ __launch_bounds__(kScanThreads) void fallback_info_kernel(const uint8_t* bitmap, int64_t T, uint32_t* info,
+                                                                     int64_t* total_out) {
     __shared__ int64_t tmp[kScanThreads];
     const int tid = threadIdx.x;
     int64_t chunk = (T + kScanThreads - 1) / kScanThreads;
@@ -141,15 +149,37 @@ __global__ __launch_bounds__(kScanThreads) void fallback_rank_kernel(const uint8
     int64_t base = block_exclusive_scan(count, tmp, &total);
     for (int64_t t = t0; t < t1; ++t) {
         const int bit = (bitmap[t >> 3] >> (7 - (t & 7))) & 1;
-        rank[t] = bit ? (int32_t)base : -1;
+        info[t] = bit ? (kInfoFallback | (uint32_t)base) : 0u;
         base += bit;
     }
     if (tid == 0) *total_out = total;
 }
 
-hipError_t launch_fallback_rank_from_bitmap(const uint8_t* bitmap, int64_t T, int32_t* rank, int64_t* total,
-                                            hipStream_t stream) {
-    hipLaunchKernelGGL(fallback_rank_kernel, dim3(1), dim3(kScanThreads), 0, stream, bitmap, T, rank, total);
+// escape chunk bits of every non-fallback tile: one wave per tile
+constexpr int kInfoWaves = 4;
+
+__global__ __launch_bounds__(kInfoWaves * kWave) void escape_info_kernel(const uint8_t* ec, int64_t T, uint32_t* info) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const int64_t tile = (int64_t)blockIdx.x * kInfoWaves + (threadIdx.x >> 6);
+    if (tile >= T) return;
+    const uint8_t* ect = ec + tile * (kTile / 2) + 8u * lane;
+    uint32_t mask = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint2 e = *reinterpret_cast<const uint2*>(ect + 512 * j);
+        const bool any = (escape_nibbles(e.x) | escape_nibbles(e.y)) != 0u;
+        if (wave_any(any)) mask |= 1u << j;
+    }
+    if (lane == 0 && !info_is_fallback(info[tile])) info[tile] = mask;
+}
+
+hipError_t launch_tile_info(const uint8_t* bitmap, const uint8_t* ec, int64_t T, uint32_t* info, int64_t* total,
+                            hipStream_t stream) {
+    hipLaunchKernelGGL(fallback_info_kernel, dim3(1), dim3(kScanThreads), 0, stream, bitmap, T, info, total);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || T == 0) return e;
+    const int64_t blocks = (T + kInfoWaves - 1) / kInfoWaves;
+    hipLaunchKernelGGL(escape_info_kernel, dim3((uint32_t)blocks), dim3(kInfoWaves * kWave), 0, stream, ec, T, info);
     return hipGetLastError();
 }
 

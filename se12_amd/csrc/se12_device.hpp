@@ -8,9 +8,9 @@
 // a tile row hold adjacent columns (reduced with DPP row ops).
 //
 // Decode of one chunk (16 weights, 8 BF16 pairs):
-//   pattern pair  = lut[ec byte]  (LDS, 256 dwords: both nibbles' exponent
-//                                  << 7 in each 16-bit half; bit 0 marks an
-//                                  escape code 15 in either nibble)
+//   pattern pair  = lut[ec byte]  (LDS, 256 dwords built once per matrix at
+//                                  bind time: both nibbles' exponent << 7 in
+//                                  each 16-bit half)
 //   sign/mantissa = v_perm of the sm dword duplicating each byte into both
 //                   halves of a 16-bit lane: (s<<8)|s keeps the sign at bit
 //                   15 and the mantissa at bits 6..0
@@ -23,9 +23,9 @@
 // Chunks are visited in that order (j, then lane, then position), so the rank
 // of an escape is `run` (escapes of earlier chunks) + the escapes of lower
 // lanes in this chunk (a wave scan) + the earlier escapes of this lane. The
-// scan and patch only run when some lane of the wave saw an escape in the
-// chunk (a wave-uniform branch); the rank is clamped to 15 like the reference
-// decoder's clip (codec.py:385).
+// scan and patch only run for chunks that the tile's bind-time sidecar word
+// marks as holding escapes (a wave-uniform branch); the rank is clamped to 15
+// like the reference decoder's clip (codec.py:385).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -66,13 +66,16 @@ __device__ __forceinline__ uint32_t lane_id() { return __builtin_amdgcn_mbcnt_hi
 
 __device__ __forceinline__ bool wave_any(bool p) { return __builtin_amdgcn_ballot_w64(p) != 0; }
 
-// inclusive prefix sum over the 64 lanes (slow paths only)
-__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, uint32_t lane) {
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        uint32_t u = __shfl_up(v, d, kWave);
-        if (lane >= (uint32_t)d) v += u;
-    }
+// inclusive prefix sum over the 64 lanes with DPP: shifts of 1, 2, 4, 8
+// within each 16-lane row, then the row totals carried across rows by the
+// row broadcasts of lanes 15 and 31
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v) {
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xF, 0xF, false);  // row_shr:1
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xF, 0xF, false);  // row_shr:2
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xF, 0xF, false);  // row_shr:4
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xF, 0xF, false);  // row_shr:8
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+    v += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
     return v;
 }
 
@@ -82,15 +85,30 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Fills the 256-entry pair table from the 15-byte codebook (all threads of
-// the block take part; the caller synchronizes).
-__device__ __forceinline__ void build_pair_lut(uint32_t* lut, const uint8_t* codebook, int tid, int nthreads) {
-    for (int b = tid; b < 256; b += nthreads) {
-        uint32_t c0 = b & 15u, c1 = (uint32_t)b >> 4;
-        uint32_t p0 = c0 < 15u ? ((uint32_t)codebook[c0] << 7) : 0u;
-        uint32_t p1 = c1 < 15u ? ((uint32_t)codebook[c1] << 7) : 0u;
-        lut[b] = p0 | (p1 << 16) | ((c0 == 15u || c1 == 15u) ? 1u : 0u);
-    }
+// Entry b of the pair table: the exponents of codes (b & 15) and (b >> 4),
+// each << 7, in the low and high 16-bit halves; escape code 15 contributes 0
+// (its exponent is patched in from the tile's esc slots).
+__host__ __device__ inline uint32_t pair_lut_entry(const uint8_t* codebook, uint32_t b) {
+    const uint32_t c0 = b & 15u, c1 = b >> 4;
+    const uint32_t p0 = c0 < 15u ? ((uint32_t)codebook[c0] << 7) : 0u;
+    const uint32_t p1 = c1 < 15u ? ((uint32_t)codebook[c1] << 7) : 0u;
+    return p0 | (p1 << 16);
+}
+
+// The block's pair table: a static LDS array, so it sits at LDS address 0
+// and a lookup's address is one byte-select shift (SDWA) of the ec word.
+// Every wave loads the bind-time table (1 KiB, 16 bytes per lane) as its
+// first load and stores it whole (the same values, with relaxed atomic
+// stores, so the waves' overlapping stores are well defined); an
+// unconditional store keeps the load from being sunk behind the tile loads.
+// The caller runs lds_barrier() before the first lookup.
+#define SE12_DECLARE_LUT(name) __shared__ __attribute__((aligned(16))) uint32_t name[256]
+
+__device__ __forceinline__ void store_block_lut(uint32_t* lut, uint4 v, uint32_t lane) {
+    __hip_atomic_store(&lut[4 * lane + 0], v.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(&lut[4 * lane + 1], v.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(&lut[4 * lane + 2], v.z, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(&lut[4 * lane + 3], v.w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // escape slot r (0..15) of a tile whose 16 esc bytes are in e
@@ -113,10 +131,10 @@ __device__ __forceinline__ void patch_exponent(uint32_t pat[8], uint32_t p, uint
     }
 }
 
-__device__ __forceinline__ void resolve_escapes(uint32_t pat[8], uint2 ec, uint4 esc, uint32_t& run, uint32_t lane) {
+__device__ __forceinline__ void resolve_escapes(uint32_t pat[8], uint2 ec, uint4 esc, uint32_t& run) {
     uint32_t t0 = escape_nibbles(ec.x), t1 = escape_nibbles(ec.y);
     const uint32_t cnt = __popc(t0) + __popc(t1);
-    const uint32_t incl = wave_incl_scan(cnt, lane);
+    const uint32_t incl = wave_incl_scan(cnt);
     const uint32_t total = __builtin_amdgcn_readlane(incl, kWave - 1);
     uint32_t r = run + incl - cnt;
     while (t0) {
@@ -134,10 +152,8 @@ __device__ __forceinline__ void resolve_escapes(uint32_t pat[8], uint2 ec, uint4
     run += total;
 }
 
-// Decodes one chunk (16 weights) into 8 BF16 pairs (low half = even column).
-__device__ __forceinline__ void decode_chunk(const uint32_t* lut, uint4 sm, uint2 ec, uint4 esc, uint32_t& run,
-                                             uint32_t lane, uint32_t w[8]) {
-    uint32_t pat[8];
+// The 8 pattern pairs of one chunk (one LDS lookup per ec byte).
+__device__ __forceinline__ void lookup_chunk(const uint32_t* lut, uint2 ec, uint32_t pat[8]) {
     pat[0] = lut[ec.x & 0xFFu];
     pat[1] = lut[(ec.x >> 8) & 0xFFu];
     pat[2] = lut[(ec.x >> 16) & 0xFFu];
@@ -146,8 +162,10 @@ __device__ __forceinline__ void decode_chunk(const uint32_t* lut, uint4 sm, uint
     pat[5] = lut[(ec.y >> 8) & 0xFFu];
     pat[6] = lut[(ec.y >> 16) & 0xFFu];
     pat[7] = lut[ec.y >> 24];
-    const uint32_t mark = (pat[0] | pat[1] | pat[2] | pat[3] | pat[4] | pat[5] | pat[6] | pat[7]) & 1u;
-    if (wave_any(mark != 0u)) resolve_escapes(pat, ec, esc, run, lane);
+}
+
+// Rebuilds the 8 BF16 pairs of a chunk from its patterns and sm bytes.
+__device__ __forceinline__ void merge_chunk(const uint32_t pat[8], uint4 sm, uint32_t w[8]) {
     w[0] = merge_pair(pat[0], dup_lo(sm.x));
     w[1] = merge_pair(pat[1], dup_hi(sm.x));
     w[2] = merge_pair(pat[2], dup_lo(sm.y));
@@ -158,20 +176,23 @@ __device__ __forceinline__ void decode_chunk(const uint32_t* lut, uint4 sm, uint
     w[7] = merge_pair(pat[7], dup_hi(sm.w));
 }
 
-// One tile's loads for one lane. The per-tile escape slots and fallback rank
-// are wave-uniform but loaded like the rest (vector loads of one address):
-// scalar loads here would be waited for as soon as the prefetch is issued.
+// Per-tile word built at bind time (one per tile):
+//   bit 31 set   -> fallback tile, bits 0..30 = its rank among fallback tiles
+//   bit 31 clear -> bit j (j = 0..3) set iff chunk j (tile rows 4j..4j+3)
+//                   holds at least one escape code
+constexpr uint32_t kInfoFallback = 0x80000000u;
+
+__device__ __forceinline__ bool info_is_fallback(uint32_t info) { return (info & kInfoFallback) != 0u; }
+__device__ __forceinline__ uint32_t info_rank(uint32_t info) { return info & ~kInfoFallback; }
+
+// One tile's `sm` and `ec` loads for one lane.
 struct TileLoads {
     uint4 sm[4];
     uint2 ec[4];
-    uint4 esc;
-    int32_t fallback_rank;  // rank among fallback tiles, or -1
 };
 
-// the bind-time sidecar: rank of the tile among fallback tiles, -1 if the tile
-// is not a fallback tile
-__device__ __forceinline__ void load_tile(TileLoads& t, const uint8_t* sm, const uint8_t* ec, const uint8_t* esc,
-                                          const int32_t* fb_rank, int64_t tile, uint32_t lane) {
+__device__ __forceinline__ void load_tile(TileLoads& t, const uint8_t* sm, const uint8_t* ec, int64_t tile,
+                                          uint32_t lane) {
     const uint8_t* smt = sm + tile * kTile + 16u * lane;
     const uint8_t* ect = ec + tile * (kTile / 2) + 8u * lane;
 #pragma unroll
@@ -179,13 +200,45 @@ __device__ __forceinline__ void load_tile(TileLoads& t, const uint8_t* sm, const
         t.sm[j] = *reinterpret_cast<const uint4*>(smt + 1024 * j);
         t.ec[j] = *reinterpret_cast<const uint2*>(ect + 512 * j);
     }
-    t.esc = *reinterpret_cast<const uint4*>(esc + tile * kEscBudget);
-    t.fallback_rank = fb_rank[tile];
 }
 
-// the (uniform) fallback rank of a loaded tile, in a scalar register
-__device__ __forceinline__ int32_t uniform_rank(const TileLoads& t) {
-    return __builtin_amdgcn_readfirstlane(t.fallback_rank);
+// The wave-uniform side data of up to 64 tiles, one tile per lane (lane g
+// holds tile g of the caller's list): the sidecar word and the 16 escape
+// slots. The per-lane addresses differ, so these stay vector loads (a scalar
+// load would share its wait counter with the LDS lookups and be waited for
+// at the first lookup). Read back with readlane.
+struct TileSide {
+    uint32_t info;
+    uint4 esc;
+};
+
+__device__ __forceinline__ void load_side(TileSide& s, const uint8_t* esc, const uint32_t* info, int64_t tile) {
+    s.info = info[tile];
+    s.esc = *reinterpret_cast<const uint4*>(esc + tile * kEscBudget);
+}
+
+__device__ __forceinline__ uint32_t side_info(const TileSide& s, int g) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)s.info, g);
+}
+
+__device__ __forceinline__ uint4 side_esc(const TileSide& s, int g) {
+    return make_uint4((uint32_t)__builtin_amdgcn_readlane((int)s.esc.x, g), (uint32_t)__builtin_amdgcn_readlane((int)s.esc.y, g),
+                      (uint32_t)__builtin_amdgcn_readlane((int)s.esc.z, g), (uint32_t)__builtin_amdgcn_readlane((int)s.esc.w, g));
+}
+
+// All 32 pattern lookups of a tile (issued back to back).
+__device__ __forceinline__ void lookup_tile(const uint32_t* lut, const TileLoads& t, uint32_t pat[4][8]) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) lookup_chunk(lut, t.ec[j], pat[j]);
+}
+
+// Patches the escape exponents into the chunks that the tile's sidecar word
+// (wave-uniform) marks as holding escapes; escape-free chunks cost nothing.
+__device__ __forceinline__ void resolve_tile_escapes(uint32_t pat[4][8], const TileLoads& t, uint32_t info, uint4 esc) {
+    uint32_t run = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (info & (1u << j)) resolve_escapes(pat[j], t.ec[j], esc, run);
 }
 
 // Raw BF16 pairs of chunk j of a fallback tile (tile-local order, like sm).

@@ -103,7 +103,7 @@ __global__ __launch_bounds__(kEncWaves * kWave) void encode_count_kernel(EncodeA
         chunk_codes(a, code_of, row, col, v, codes, m);
         count += __popc(m);
     }
-    const uint32_t total = __builtin_amdgcn_readlane(wave_incl_scan(count, lane), kWave - 1);
+    const uint32_t total = __builtin_amdgcn_readlane(wave_incl_scan(count), kWave - 1);
     if (lane == 0) a.tile_escapes[tile] = (int32_t)total;
 }
 
@@ -185,8 +185,8 @@ __global__ __launch_bounds__(kEncWaves * kWave) void encode_write_kernel(EncodeA
     }
 
     // escape ranks: chunk j, then lane, then position (tile-local row-major)
-    const uint32_t s01 = wave_incl_scan(cnt[0] | (cnt[1] << 16), lane);
-    const uint32_t s23 = wave_incl_scan(cnt[2] | (cnt[3] << 16), lane);
+    const uint32_t s01 = wave_incl_scan(cnt[0] | (cnt[1] << 16));
+    const uint32_t s23 = wave_incl_scan(cnt[2] | (cnt[3] << 16));
     const uint32_t t01 = __builtin_amdgcn_readlane(s01, kWave - 1);
     const uint32_t t23 = __builtin_amdgcn_readlane(s23, kWave - 1);
     const uint32_t tot[4] = {t01 & 0xFFFFu, t01 >> 16, t23 & 0xFFFFu, t23 >> 16};

@@ -11,8 +11,8 @@ struct GemvArgs {
     const uint8_t* sm;
     const uint8_t* ec;
     const uint8_t* esc;
-    const uint8_t* codebook;
-    const int32_t* fb_rank;   // per-tile rank among fallback tiles, -1 if not one
+    const uint32_t* lut;      // [256] pair table built at bind time
+    const uint32_t* info;     // [T] per-tile sidecar word (fallback rank / escape chunks)
     const int16_t* fb_raw;
     const uint16_t* wraw;     // raw twin: row-major [N, K] BF16 bits
     const void* x;            // [B, K] BF16 or FP32
@@ -22,10 +22,21 @@ struct GemvArgs {
     int64_t N, K, Np;
     int32_t TR, TC;
     int32_t S;                // K splits per tile row
-    int32_t xstride;          // LDS elements per batch row of x
-    int32_t x_vec_ok;         // x rows allow 16-byte loads
-    int32_t w_vec_ok;         // raw rows allow 16-byte loads
-    int32_t mask_tail;        // K % 256 != 0 and codebook[0] == 255
+};
+
+// How one GEMV launch runs: the launch shape (waves per block, blocks =
+// tile rows x splits) fixes the results; the variant (tiles per round `g`,
+// prefetch `pf`, `generic` edge handling) only changes speed.
+struct GemvPlan {
+    int batch;
+    bool xf32;
+    bool raw;
+    bool generic;
+    int g;
+    bool pf;
+    int waves;
+    int blocks;
+    size_t lds;
 };
 
 struct DecodeArgs {
@@ -34,7 +45,8 @@ struct DecodeArgs {
     const uint8_t* esc;
     const uint8_t* codebook;
     const uint8_t* bitmap;
-    const int32_t* fb_rank;
+    const uint32_t* lut;      // [256] pair table built at bind time
+    const uint32_t* info;     // [T] per-tile sidecar word
     const int16_t* fb_raw;
     const int64_t* rows;      // decode_rows only
     uint16_t* out;
@@ -62,22 +74,34 @@ struct EncodeArgs {
 };
 
 constexpr int kGemvMaxBatchPerLaunch = 4;
-// waves per block the kernel is compiled for: 16 (1024 threads, <= 128 VGPRs)
-// for batch 1 with BF16 x, 4 where more accumulators or FP32 x need registers
-constexpr int gemv_max_waves(int batch, bool xf32) { return (batch == 1 && !xf32) ? 16 : 4; }
 constexpr int kLutBytes = 1024;
 
-// bytes of dynamic LDS a GEMV launch needs
-inline size_t gemv_lds_bytes(int waves, int batch, int xstride, bool xf32) {
-    return (size_t)kLutBytes + (size_t)waves * batch * 16 * sizeof(float) +
-           (size_t)batch * xstride * (xf32 ? 4 : 2);
+// Largest block (threads) of a GEMV kernel variant, from its VGPR demand
+// (512 VGPRs per SIMD lane: 1024 threads = 4 waves per SIMD = 128 VGPRs
+// each, 512 threads = 256). The FAST estimates are fitted to hipcc's
+// allocation (per round: a tile's streams + its x slice, 37 VGPRs at batch 1,
+// 40 for the raw twin; 8 more per extra batch row); the GENERIC variants run
+// one tile per round without prefetch. The build fails if any variant spills.
+constexpr int gemv_vgpr_estimate(int batch, bool raw, int g, bool pf) {
+    return raw ? 24 + 4 * (batch - 1) + (pf ? 2 : 1) * g * (40 + 8 * (batch - 1))
+               : 57 + 4 * (batch - 1) + (pf ? 2 : 1) * g * (37 + 8 * (batch - 1));
+}
+constexpr int gemv_max_threads(int batch, bool xf32, bool raw, int g, bool pf, bool generic) {
+    return generic ? (batch >= 2 ? 512 : 1024)
+                   : gemv_vgpr_estimate(batch, raw, g, pf) <= 128 ? 1024
+                   : gemv_vgpr_estimate(batch, raw, g, pf) <= 256 ? 512 : 256;
 }
 
-hipError_t launch_gemv(const GemvArgs& a, int batch, bool xf32, bool raw, int threads, int blocks, size_t lds,
-                       hipStream_t stream);
+// bytes of dynamic LDS a GEMV launch needs (the cross-wave reduction; the
+// 1 KiB pair table is static)
+inline size_t gemv_lds_bytes(int waves, int batch) { return (size_t)waves * batch * 16 * sizeof(float); }
+
+hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream);
-hipError_t launch_fallback_rank_from_bitmap(const uint8_t* bitmap, int64_t T, int32_t* rank, int64_t* total,
-                                            hipStream_t stream);
+// Bind-time sidecar: one word per tile (fallback rank, or the chunks holding
+// escape codes) and the fallback tile count.
+hipError_t launch_tile_info(const uint8_t* bitmap, const uint8_t* ec, int64_t T, uint32_t* info, int64_t* total,
+                            hipStream_t stream);
 hipError_t launch_encode_histogram(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_count(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_scan(const EncodeArgs& a, hipStream_t stream);

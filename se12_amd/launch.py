@@ -6,8 +6,10 @@ threads_per_block + blocks) and lws/domain/launch/search_space.py:14-75
 for this kernel's grid: a block is 1..16 wave64s working on one 16-row tile
 row, and `blocks` = tile_rows x k_splits, where the K tiles of a tile row are
 cut into `k_splits` contiguous ranges (the last block of a tile row to finish
-adds the splits in order). The default configuration itself is computed by
-the library (se12_default_launch) from the device's CU count.
+adds the splits in order). The launch shape fixes the order of every sum, so
+the fused kernel and its raw twin agree bit for bit under one configuration.
+The default configuration itself is computed by the library
+(se12_default_launch) from the device's CU count.
 """
 
 from __future__ import annotations
@@ -15,7 +17,8 @@ from __future__ import annotations
 import dataclasses
 
 WAVE_SIZE = 64
-THREADS_PER_BLOCK_CANDIDATES = (64, 128, 192, 256, 512, 576, 1024)
+WAVES_PER_BLOCK_CANDIDATES = (1, 2, 3, 4, 6, 8, 9, 12, 16)
+K_SPLIT_CANDIDATES = (1, 2, 3, 4, 6, 8, 9, 12, 16, 18, 24, 32, 36, 48, 64)
 MAX_K_SPLITS = 64
 
 
@@ -55,17 +58,30 @@ def configuration(waves: int, k_splits: int, output_rows: int) -> LaunchConfigur
     )
 
 
-def max_waves_per_block(batch: int, float32_activations: bool = False) -> int:
-    """16 wave64s (1024 threads) for batch 1 with BF16 x, else 4 (register budget)."""
-    return 16 if batch == 1 and not float32_activations else 4
+def runs_generic(output_rows: int, k: int, float32_activations: bool = False) -> bool:
+    """Whether the kernels take their edge-handling variants: FP32 x, K not a
+    whole number of 256-column tiles, or (for the raw twin) output rows not a
+    whole number of 16-row tiles."""
+    return float32_activations or k % 256 != 0 or output_rows % 16 != 0
 
 
-def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int = 1) -> tuple[int, int]:
+def max_waves_per_block(batch: int, float32_activations: bool = False, generic: bool = False) -> int:
+    """16 wave64s (1024 threads), or 8 where a launch needs more registers per
+    lane: 4 batch rows per launch, or 2-4 rows in the edge-handling variants."""
+    b = min(batch, 4)
+    if generic or float32_activations:
+        return 8 if b >= 2 else 16
+    return 8 if b >= 4 else 16
+
+
+def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int = 1, k: int | None = None,
+                     float32_activations: bool = False) -> tuple[int, int]:
     """(waves per block, K splits) of a configuration for a matrix with `output_rows` rows."""
     tr = tile_rows(output_rows)
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
-    hi = WAVE_SIZE * max_waves_per_block(min(batch, 4))
+    generic = runs_generic(output_rows, k, float32_activations) if k is not None else float32_activations
+    hi = WAVE_SIZE * max_waves_per_block(batch, float32_activations, generic)
     if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= hi:
         raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {hi}]")
     if blocks <= 0 or blocks % tr:
@@ -75,14 +91,14 @@ def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int =
 
 def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_activations: bool = False) -> tuple[LaunchConfiguration, ...]:
     """Every (waves, splits) worth timing: waves per block up to the batch's
-    limit, splits 1..K tiles, never more waves than K tiles per split
-    (search_space.py:17-19 enumerates threads per block the same way)."""
+    limit (valid for the fused kernel and its raw twin alike), K splits up to
+    the K tiles, never more waves than tiles per split (search_space.py:17-19
+    enumerates threads per block the same way)."""
     tc = k_tiles(k)
-    splits = sorted({s for s in (1, 2, 3, 4, 6, 8, 9, 12, 16, 18, 24, 32, 36, 48, 64) if s <= min(tc, MAX_K_SPLITS)} | {1})
-    mw = max_waves_per_block(min(batch, 4), float32_activations)
+    mw = max_waves_per_block(batch, float32_activations, runs_generic(output_rows, k, float32_activations))
+    splits = [s for s in K_SPLIT_CANDIDATES if s <= min(tc, MAX_K_SPLITS)]
     out = []
-    for tpb in THREADS_PER_BLOCK_CANDIDATES:
-        waves = tpb // WAVE_SIZE
+    for waves in WAVES_PER_BLOCK_CANDIDATES:
         if waves > mw:
             continue
         for s in splits:

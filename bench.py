@@ -3,19 +3,21 @@
 Workload (one "step"): every linear of a 26-layer Gemma-2-2B at batch 1 -
 per layer q 2048x2304, k 1024x2304, v 1024x2304, o 2304x2048, gate 9216x2304,
 up 9216x2304, down 2304x9216 - i.e. 182 fused SE12 GEMVs over 3.04 GB of SE12
-streams (2.03 G weights), far beyond the 256 MB Infinity Cache, so every step
+streams (2.02 G weights), far beyond the 256 MB Infinity Cache, so every step
 streams from HBM. Weights are BF16 N(0, 0.02) drawn on the device (torch
 generator seeded per layer and projection) and SE12-encoded on the GPU;
 activations are BF16 N(0, 1) seeded per layer. The step is captured once in a
 HIP graph and replayed; the timed region is bracketed by synchronizations and
-HIP events on the replay stream.
+HIP events on the replay stream. Every GEMV uses the library's default launch.
 
 Printed JSON (one line on stdout): value = BF16-equivalent weight GB/s of the
 whole step (2 bytes x weights / step time, the reference's convention,
-lws/bench/micro.py:162-165), the per-shape microseconds, the same step through
-hipBLASLt BF16 (torch.nn.functional.linear) and through the raw-BF16 twin
-kernel, a roofline line for the fused GEMV kernel and the oracle's numpy
-decode + matmul timed on the host as the CPU baseline.
+lws/bench/micro.py:162-165); the same step through hipBLASLt BF16
+(torch.nn.functional.linear) and through the raw-BF16 twin kernel; per-shape
+microseconds; a roofline object for the dominant kernel - the fused GEMV at
+the 2304x9216 down_proj shape, timed live as 26 back-to-back launches over the
+26 layers' (cold) matrices; and the oracle's numpy decode + matmul timed on
+the host as the CPU baseline.
 """
 
 from __future__ import annotations
@@ -215,7 +217,16 @@ def main(argv=None) -> int:
         },
     }
 
-    achieved = (se12_bytes + act_bytes) / (ms * 1e-3) / 1e9
+    # dominant kernel: the 26 down_proj GEMVs (2304x9216, 31.9 MB of streams
+    # each, 830 MB in all: every launch reads cold HBM), timed on the replay
+    # stream with HIP events around `steps` replays of a 26-launch graph
+    down = [layer[6] for layer in stack]
+    g_down = capture(lambda: [e["kern"].multiply(e["x"], out=e["y"]) for e in down])
+    ms_down = time_graph(g_down, args.steps, args.warmup)
+    us_launch = ms_down * 1e3 / len(down)
+    bytes_launch = down[0]["enc"].byte_size() + down[0]["k"] * 2 + down[0]["n"] * 4
+    achieved = bytes_launch / (us_launch * 1e-6) / 1e9
+    launch = down[0]["kern"].default_launch(1)
     result["roofline"] = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
@@ -223,10 +234,15 @@ def main(argv=None) -> int:
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBPS, 4),
         "traffic": None,
-        "kernel": "se12::gemv_kernel<1,bf16,se12>",
-        "avg_launch_us": round(ms * 1e3 / len(flat), 3),
-        "algorithmic_bytes_per_launch": round((se12_bytes + act_bytes) / len(flat)),
+        "kernel": "se12::gemv_kernel (fused SE12 decode + GEMV, batch 1)",
+        "shape": [down[0]["n"], down[0]["k"]],
+        "launch": {"threads_per_block": launch.threads_per_block.value, "blocks": launch.blocks.value},
+        "avg_launch_us": round(us_launch, 3),
+        "algorithmic_bytes_per_launch": bytes_launch,
+        "bf16_equiv_gbps": round(2 * down[0]["n"] * down[0]["k"] / (us_launch * 1e-6) / 1e9, 1),
     }
+    log(f"[bench] down_proj launches: {us_launch:.2f} us each -> {achieved:.0f} GB/s of SE12 streams")
+    del g_down
 
     if not args.only_fused:
         def bf16_step():
@@ -262,8 +278,10 @@ def main(argv=None) -> int:
             g = capture(lambda col=col: [e["kern"].multiply(e["x"], out=e["y"]) for e in col])
             ms_s = time_graph(g, 10, 3, flush=flush)
             us = ms_s * 1e3 / len(col)
+            lc = col[0]["kern"].default_launch(1)
             per_shape[name] = {"shape": [n, k], "us": round(us, 3), "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
-                               "se12_gbps": round(col[0]["enc"].byte_size() / (us * 1e-6) / 1e9, 1)}
+                               "se12_gbps": round(col[0]["enc"].byte_size() / (us * 1e-6) / 1e9, 1),
+                               "launch": [lc.threads_per_block.value, lc.blocks.value]}
             if not args.only_fused:
                 gb = capture(lambda col=col: [torch.nn.functional.linear(e["x"], e["w"]) for e in col])
                 us_b = time_graph(gb, 10, 3, flush=flush) * 1e3 / len(col)

@@ -252,17 +252,21 @@ static int max_threads_for(int32_t bl, bool xf32, bool generic) {
 }
 
 // The default launch, re-derived for MI355X (256 CUs in 8 XCDs, wave64) from
-// a sweep of every (waves, splits) pair on cold data at the Gemma-2 2B/9B/27B
-// shapes. A batch-1 GEMV is one pass over the streams; the cross-block K
-// reduction (S > 1) adds a store -> counter -> reload round trip to the end of
-// every block, so a block covers a whole tile row whenever that still spreads
-// the work:
-//  - fewer tile rows than CUs: one wave per K tile (at most 16 waves), S = 1;
-//    only very long K rows on very few tile rows are split, so that every CU
-//    gets a block;
-//  - at least one tile row per CU: 4 waves (2-3 tiles each) for short rows,
-//    8 for rows of 13-32 tiles, and for longer rows 4 waves with the row cut
-//    into splits of about 24 tiles, which balances the blocks over the CUs.
+// sweeps of every (waves, splits) pair on cold data at the Gemma-2 2B/9B/27B
+// shapes and the 256000x2304 LM head. A batch-1 GEMV is one pass over the
+// streams. What pays: enough tiles in flight per CU to cover HBM latency but
+// not so many that every wave's data lands at the end of the pass (the
+// decode would then all run after the last byte arrives), and no cross-block
+// K reduction (S > 1 adds a store -> counter -> reload round trip to the end
+// of every block) unless a row is very long:
+//  - fewer tile rows than CUs: one wave per K tile for rows of <= 16 tiles;
+//    8 waves (each streaming its tiles with the next one prefetched) for
+//    longer rows; very long rows on very few tile rows are split so that
+//    every CU gets a block;
+//  - many tile rows: 3 waves for matrices up to ~50 MB of streams, 8 for
+//    larger ones with short rows (6 for very tall matrices such as an LM
+//    head), and 8 waves with splits of ~36 tiles for rows longer than 32
+//    tiles.
 static void default_launch(const se12_handle* h, int32_t batch, bool xf32, bool generic, int32_t* waves_out,
                            int32_t* splits_out) {
     const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
@@ -271,15 +275,15 @@ static void default_launch(const se12_handle* h, int32_t batch, bool xf32, bool 
     const int64_t tr = h->TR, tc = h->TC;
     int64_t waves, splits = 1;
     if (tr < cus) {
-        waves = std::min<int64_t>(16, tc);
+        waves = tc <= 16 ? tc : 8;
         if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
-    } else if (tc <= 12) {
-        waves = std::min<int64_t>(4, tc);
-    } else if (tc <= 32) {
+    } else if (tc > 32) {
         waves = 8;
+        splits = std::max<int64_t>(1, (tc + 18) / 36);
+    } else if (tr * tc <= 8192) {
+        waves = std::min<int64_t>(3, tc);
     } else {
-        waves = 4;
-        splits = std::max<int64_t>(1, (tc + 12) / 24);
+        waves = std::min<int64_t>(tr >= 4096 ? 6 : 8, tc);
     }
     waves = std::max<int64_t>(1, std::min(waves, mw));
     *waves_out = (int32_t)waves;
@@ -298,9 +302,9 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
     return SE12_OK;
 }
 
-// Picks the kernel variant for a launch shape: all of a wave's tiles in one
-// round when they fit the block's VGPR budget, else rounds with the next one
-// prefetched, else plain rounds.
+// Picks the kernel variant for a launch shape: a wave that owns 4 or more
+// tiles streams them with the next tile's loads in flight (PF) when the
+// block's register budget allows; otherwise it takes one tile per round.
 static GemvPlan plan_gemv(const se12_handle* h, int32_t bl, bool xf32, bool generic, int32_t waves, int32_t splits) {
     GemvPlan p{};
     p.batch = bl;
@@ -310,29 +314,9 @@ static GemvPlan plan_gemv(const se12_handle* h, int32_t bl, bool xf32, bool gene
     p.waves = waves;
     p.blocks = h->TR * splits;
     p.lds = gemv_lds_bytes(waves, bl);
-    const int threads = waves * 64;
+    p.g = 1;
     const int64_t per_wave = ceil_div(ceil_div(h->TC, splits), waves);
-    auto fits = [&](int g, bool pf) { return threads <= gemv_max_threads(bl, xf32, p.raw, g, pf, false); };
-    if (generic) {
-        p.g = 1;
-        p.pf = false;
-        return p;
-    }
-    if (per_wave <= 4 && fits((int)per_wave, false)) {
-        p.g = (int)per_wave;
-        p.pf = false;
-        return p;
-    }
-    if (fits(2, true) && per_wave >= 4) {
-        p.g = 2;
-        p.pf = true;
-    } else if (fits(1, true)) {
-        p.g = 1;
-        p.pf = true;
-    } else {
-        p.g = 1;
-        p.pf = false;
-    }
+    p.pf = !generic && per_wave >= 4 && waves * 64 <= gemv_max_threads(bl, xf32, p.raw, 1, true, false);
     return p;
 }
 

@@ -134,9 +134,19 @@ __device__ __forceinline__ void patch_exponent(uint32_t pat[8], uint32_t p, uint
 __device__ __forceinline__ void resolve_escapes(uint32_t pat[8], uint2 ec, uint4 esc, uint32_t& run) {
     uint32_t t0 = escape_nibbles(ec.x), t1 = escape_nibbles(ec.y);
     const uint32_t cnt = __popc(t0) + __popc(t1);
-    const uint32_t incl = wave_incl_scan(cnt);
-    const uint32_t total = __builtin_amdgcn_readlane(incl, kWave - 1);
-    uint32_t r = run + incl - cnt;
+    // escapes of lower lanes: a mask count when no lane holds more than one
+    // escape in the chunk (the common case), else a wave prefix sum
+    uint32_t below, total;
+    if (__builtin_amdgcn_ballot_w64(cnt > 1u) == 0) {
+        const uint64_t has = __builtin_amdgcn_ballot_w64(cnt != 0u);
+        below = __builtin_amdgcn_mbcnt_hi((uint32_t)(has >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)has, 0u));
+        total = (uint32_t)__builtin_popcountll(has);
+    } else {
+        const uint32_t incl = wave_incl_scan(cnt);
+        below = incl - cnt;
+        total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    }
+    uint32_t r = run + below;
     while (t0) {
         const uint32_t p = (uint32_t)__builtin_ctz(t0) >> 2;
         t0 &= t0 - 1u;

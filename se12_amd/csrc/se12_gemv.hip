@@ -14,12 +14,13 @@
 // round the block's waves read W consecutive tiles (contiguous HBM). The
 // launch shape (W, S) alone fixes every accumulation order.
 //
-// Memory pipeline: a wave issues the loads of G tiles (and the matching x
-// slices, read straight from L2) at once; when it owns more than G tiles it
-// keeps the next G in flight while it decodes the current ones (PF; the
-// GENERIC variants take one tile per round without prefetch). With
-// G >= the wave's tile count every load of the kernel is in flight from the
-// start. The block's waves meet once before decoding, after wave 0 has copied
+// Memory pipeline: a wave takes its tiles one round at a time (G tiles per
+// round; the library launches G = 1) and reads the matching x slices
+// straight from L2. A wave that owns 4 or more tiles keeps the next round's
+// loads in flight while it decodes the current one (PF); with fewer, it
+// loads, waits and decodes in turn, which staggers the chip's requests so
+// that decode work overlaps the rest of the pass instead of piling up after
+// its last byte (measured on MI355X: issuing every tile at once was slower). The block's waves meet once before decoding, after wave 0 has copied
 // the bind-time pair table into LDS, and once for the final reduction.
 //
 // Reductions, all in a fixed order: DPP over the 16 lanes of a tile row,
@@ -180,7 +181,8 @@ struct Round {
 };
 
 template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC>
-__global__ __launch_bounds__(gemv_max_threads(B, XF32, RAW, G, PF, GENERIC)) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(gemv_max_threads(B, XF32, RAW, G, PF, GENERIC))
+__attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(GemvArgs a) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) float red[];
     const int W = blockDim.x >> 6;
@@ -328,15 +330,8 @@ hipError_t launch_b(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
     if (p.generic)
         return p.xf32 ? go<B, true, RAW, 1, false, true>(a, threads, p.blocks, p.lds, stream)
                       : go<B, false, RAW, 1, false, true>(a, threads, p.blocks, p.lds, stream);
-    switch (p.g * 2 + (p.pf ? 1 : 0)) {
-        case 2: return go<B, false, RAW, 1, false, false>(a, threads, p.blocks, p.lds, stream);
-        case 3: return go<B, false, RAW, 1, true, false>(a, threads, p.blocks, p.lds, stream);
-        case 4: return go<B, false, RAW, 2, false, false>(a, threads, p.blocks, p.lds, stream);
-        case 5: return go<B, false, RAW, 2, true, false>(a, threads, p.blocks, p.lds, stream);
-        case 6: return go<B, false, RAW, 3, false, false>(a, threads, p.blocks, p.lds, stream);
-        case 8: return go<B, false, RAW, 4, false, false>(a, threads, p.blocks, p.lds, stream);
-        default: return hipErrorInvalidValue;
-    }
+    return p.pf ? go<B, false, RAW, 1, true, false>(a, threads, p.blocks, p.lds, stream)
+                : go<B, false, RAW, 1, false, false>(a, threads, p.blocks, p.lds, stream);
 }
 
 }  // namespace

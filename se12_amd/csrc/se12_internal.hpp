@@ -92,6 +92,14 @@ constexpr int gemv_max_threads(int batch, bool xf32, bool raw, int g, bool pf, b
                    : gemv_vgpr_estimate(batch, raw, g, pf) <= 256 ? 512 : 256;
 }
 
+// Minimum waves per SIMD the compiler must leave room for (register
+// allocation target) for the variants whose occupancy sits on a VGPR
+// granule boundary: the batch-1 single-tile rounds at 5 waves (96 VGPRs),
+// two tiles per round at 4 (128). 1 = no target.
+constexpr int gemv_waves_per_simd(int batch, bool raw, int g, bool pf, bool generic) {
+    return (raw || generic || batch != 1 || pf) ? 1 : g == 1 ? 5 : g == 2 ? 4 : 1;
+}
+
 // bytes of dynamic LDS a GEMV launch needs (the cross-wave reduction; the
 // 1 KiB pair table is static)
 inline size_t gemv_lds_bytes(int waves, int batch) { return (size_t)waves * batch * 16 * sizeof(float); }

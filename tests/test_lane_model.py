@@ -1,11 +1,12 @@
 """A numpy model of the per-lane decode the HIP kernels run (se12_device.hpp),
 checked against the oracle on the CPU: lane l of the wave owning a tile reads
 sm bytes [1024*j + 16*l, +16) and ec bytes [512*j + 8*l, +8) for chunks
-j = 0..3, looks up each ec byte in the 256-entry pair table, duplicates sm
-bytes with the v_perm selectors 0x01010000 / 0x03030202, merges with the
-exponent mask 0x7F807F80, and ranks escapes by (chunk, lane, position) with a
-wave prefix sum. The reference checked its own warp-32 rank scheme the same
-way before writing CUDA (tests/test_spec_fused_gemv.py:209-271)."""
+j = 0..3, looks up each ec byte in the 256-entry pair table (built at bind
+time from the codebook; code 15 contributes exponent 0), duplicates sm bytes with the v_perm selectors 0x01010000 /
+0x03030202, merges with the exponent mask 0x7F807F80, and ranks escapes by
+(chunk, lane, position) - only in the chunks the per-tile sidecar word marks.
+The reference checked its own warp-32 rank scheme the same way before writing
+CUDA (tests/test_spec_fused_gemv.py:209-271)."""
 
 from __future__ import annotations
 
@@ -26,17 +27,45 @@ def perm(hi: int, lo: int, sel: int) -> int:
     return out
 
 
+def packed_codebook(codebook) -> list[int]:
+    """The 15 codebook bytes as 4 little-endian words, byte 15 = 0."""
+    b = list(int(c) for c in codebook) + [0]
+    return [b[4 * k] | b[4 * k + 1] << 8 | b[4 * k + 2] << 16 | b[4 * k + 3] << 24 for k in range(4)]
+
+
 def pair_lut(codebook) -> list[int]:
-    lut = []
-    for b in range(256):
-        c0, c1 = b & 15, b >> 4
-        p0 = (int(codebook[c0]) << 7) if c0 < 15 else 0
-        p1 = (int(codebook[c1]) << 7) if c1 < 15 else 0
-        lut.append(p0 | (p1 << 16) | (1 if 15 in (c0, c1) else 0))
+    """The pair table, built the way the kernels' table is laid out: entry
+    4l + i holds high code l >> 2 and low code 4(l & 3) + i, read from the
+    codebook packed into 4 little-endian words whose byte 15 is 0."""
+    words = packed_codebook(codebook)
+
+    def byte(c):
+        return (words[c >> 2] >> (8 * (c & 3))) & 0xFF
+
+    lut = [0] * 256
+    for lane in range(64):
+        hi = byte(lane >> 2) << 23
+        lo = words[lane & 3]
+        for i in range(4):
+            lut[4 * lane + i] = (((lo >> (8 * i)) & 0xFF) << 7) | hi
     return lut
 
 
-def lane_model_decode_tile(sm_tile: bytes, ec_tile: bytes, esc_tile, lut) -> np.ndarray:
+def tile_info_words(enc: dict) -> np.ndarray:
+    """The bind-time sidecar: fallback tiles -> 0x80000000 | rank among
+    fallback tiles; others -> bit j set iff chunk j (tile rows 4j..4j+3)
+    holds an escape code."""
+    rows, cols = enc["shape"]
+    ntr, ntc = o.tile_grid(rows, cols)
+    t = ntr * ntc
+    fb = o.unpack_bitmap(enc["fallback_bitmap"], t)
+    ranks = np.cumsum(fb) - 1
+    codes = o.unpack_codes(enc["ec"]).reshape(t, 4, 1024)
+    chunk_bits = ((codes == 15).any(axis=2) * (1 << np.arange(4))).sum(axis=1)
+    return np.where(fb, 0x80000000 | ranks, chunk_bits).astype(np.uint64)
+
+
+def lane_model_decode_tile(sm_tile: bytes, ec_tile: bytes, esc_tile, lut, info: int) -> np.ndarray:
     out = np.zeros(4096, dtype=np.uint16)
     run = 0
     for j in range(4):
@@ -49,9 +78,11 @@ def lane_model_decode_tile(sm_tile: bytes, ec_tile: bytes, esc_tile, lut) -> np.
                 if ((ecb[p >> 1] >> (4 * (p & 1))) & 15) == 15:
                     m |= 1 << p
             escmasks.append(m)
-        if any(p & 1 for lane_p in pats for p in lane_p):  # wave-uniform slow path
+        if info >> j & 1:  # wave-uniform: only chunks the sidecar marks
             counts = [bin(m).count("1") for m in escmasks]
             incl = np.cumsum(counts)
+            if max(counts) <= 1:  # the kernel's mask-count path gives the same ranks
+                assert [sum(1 for c in counts[:lane] if c) for lane in range(64)] == [int(incl[i]) - counts[i] for i in range(64)]
             for lane in range(64):
                 r = run + int(incl[lane]) - counts[lane]
                 for p in range(16):
@@ -81,12 +112,12 @@ def test_lane_model_reproduces_the_oracle(name):
     tiles = o.decode_tiles(enc)
     ntr, ntc, _ = tiles.shape
     lut = pair_lut(enc["codebook"])
-    fallback = o.unpack_bitmap(enc["fallback_bitmap"], ntr * ntc)
+    info = tile_info_words(enc)
     sm, ec = enc["sm"].tobytes(), enc["ec"].tobytes()
     for t in range(ntr * ntc):
-        if fallback[t]:
+        if info[t] >> 31:
             continue
-        got = lane_model_decode_tile(sm[4096 * t: 4096 * (t + 1)], ec[2048 * t: 2048 * (t + 1)], enc["esc"][t], lut)
+        got = lane_model_decode_tile(sm[4096 * t: 4096 * (t + 1)], ec[2048 * t: 2048 * (t + 1)], enc["esc"][t], lut, int(info[t]))
         assert np.array_equal(got, tiles.reshape(-1, 4096)[t].view(np.uint16)), f"tile {t}"
 
 
@@ -101,5 +132,38 @@ def test_lane_model_on_escape_dense_tile():
     bits = ((sign << 15) | (e.astype(np.uint16) << 7) | mant).view(np.int16)
     enc = o.encode(bits, 16, 256)
     assert o.fallback_tile_count(enc) == 0
-    got = lane_model_decode_tile(enc["sm"].tobytes(), enc["ec"].tobytes(), enc["esc"][0], pair_lut(enc["codebook"]))
+    info = int(tile_info_words(enc)[0])
+    assert info == 0b1111 or info & 1  # escapes in chunk 0 at least
+    got = lane_model_decode_tile(enc["sm"].tobytes(), enc["ec"].tobytes(), enc["esc"][0], pair_lut(enc["codebook"]), info)
     assert np.array_equal(got.view(np.int16), bits)
+
+
+def test_pair_table_matches_the_codebook_rule():
+    """Entry b = (codebook[b & 15] << 7) | (codebook[b >> 4] << 23), code 15 -> 0."""
+    cb = np.array([122, 121, 120, 123, 119, 118, 124, 117, 116, 125, 115, 114, 126, 113, 255], dtype=np.uint8)
+    lut = pair_lut(cb)
+    for b in range(256):
+        c0, c1 = b & 15, b >> 4
+        e0 = int(cb[c0]) if c0 < 15 else 0
+        e1 = int(cb[c1]) if c1 < 15 else 0
+        assert lut[b] == (e0 << 7) | (e1 << 23), b
+
+
+def test_tile_info_words_on_the_golden_vectors():
+    """Fallback tiles carry their rank; other tiles mark exactly the chunks
+    whose codes include 15 (checked tile by tile against the decoded codes)."""
+    for name in ["mixed_48x768", "uniform_33x300", "fallback_16x256", "normal_32x512"]:
+        enc = golden_as_encoding(load_golden(name))
+        info = tile_info_words(enc)
+        rows, cols = enc["shape"]
+        ntr, ntc = o.tile_grid(rows, cols)
+        fb = o.unpack_bitmap(enc["fallback_bitmap"], ntr * ntc)
+        codes = o.unpack_codes(enc["ec"]).reshape(-1, 4096)
+        rank = 0
+        for t in range(ntr * ntc):
+            if fb[t]:
+                assert info[t] == 0x80000000 | rank
+                rank += 1
+            else:
+                for j in range(4):
+                    assert bool(info[t] >> j & 1) == bool((codes[t, 1024 * j:1024 * (j + 1)] == 15).any())

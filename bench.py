@@ -4,7 +4,11 @@ Workload (one "step"): every linear of a 26-layer Gemma-2-2B at batch 1 -
 per layer q 2048x2304, k 1024x2304, v 1024x2304, o 2304x2048, gate 9216x2304,
 up 9216x2304, down 2304x9216 - i.e. 182 fused SE12 GEMVs over 3.04 GB of SE12
 streams (2.02 G weights), far beyond the 256 MB Infinity Cache, so every step
-streams from HBM. Weights are BF16 N(0, 0.02) drawn on the device (torch
+streams from HBM. The step runs the way a decode runtime issues it: the
+projections that read the same input share one launch (q/k/v, then gate/up),
+so 4 launches per layer; the same step with one launch per GEMV (7 per layer)
+is reported beside it, and the hipBLASLt BF16 comparison gets the same
+grouping (one GEMV over the concatenated q/k/v and gate/up weights). Weights are BF16 N(0, 0.02) drawn on the device (torch
 generator seeded per layer and projection) and SE12-encoded on the GPU;
 activations are BF16 N(0, 1) seeded per layer. The step is captured once in a
 HIP graph and replayed; the timed region is bracketed by synchronizations and
@@ -12,9 +16,9 @@ HIP events on the replay stream. Every GEMV uses the library's default launch.
 
 Printed JSON (one line on stdout): value = BF16-equivalent weight GB/s of the
 whole step (2 bytes x weights / step time, the reference's convention,
-lws/bench/micro.py:162-165); the same step through hipBLASLt BF16
-(torch.nn.functional.linear) and through the raw-BF16 twin kernel; per-shape
-microseconds; a roofline object for the dominant kernel - the fused GEMV at
+lws/bench/micro.py:162-165); the same step with one launch per GEMV; the
+step through hipBLASLt BF16 (torch.nn.functional.linear) and through the
+raw-BF16 twin kernel; per-shape microseconds; a roofline object for the dominant kernel - the fused GEMV at
 the 2304x9216 down_proj shape, timed live as 26 back-to-back launches over the
 26 layers' (cold) matrices; and the oracle's numpy decode + matmul timed on
 the host as the CPU baseline.
@@ -185,14 +189,34 @@ def main(argv=None) -> int:
     act_bytes = sum(e["k"] * 2 + e["n"] * 4 for e in flat)
     bf16_bytes = 2 * weights
 
+    from se12_amd.hip import multiply_grouped
+
+    # per layer: [q, k, v] | o | [gate, up] | down
+    GROUPS = ((0, 1, 2), (3,), (4, 5), (6,))
+
     def fused_step():
+        for layer in stack:
+            for grp in GROUPS:
+                if len(grp) == 1:
+                    e = layer[grp[0]]
+                    e["kern"].multiply(e["x"], out=e["y"])
+                else:
+                    es = [layer[i] for i in grp]
+                    multiply_grouped([e["kern"] for e in es], es[0]["x"], outs=[e["y"] for e in es])
+
+    def separate_step():
         for e in flat:
             e["kern"].multiply(e["x"], out=e["y"])
 
     g_fused = capture(fused_step)
     ms = time_graph(g_fused, args.steps, args.warmup)
     value = bf16_bytes / (ms * 1e-3) / 1e9
-    log(f"[bench] fused step {ms:.3f} ms -> {value:.1f} GB/s BF16-equivalent")
+    log(f"[bench] fused step (grouped launches) {ms:.3f} ms -> {value:.1f} GB/s BF16-equivalent")
+    del g_fused
+    g_sep = capture(separate_step)
+    ms_sep = time_graph(g_sep, args.steps, args.warmup)
+    log(f"[bench] fused step (one launch per GEMV) {ms_sep:.3f} ms -> {bf16_bytes / (ms_sep * 1e-3) / 1e9:.1f} GB/s")
+    del g_sep
 
     result = {
         "metric": METRIC,
@@ -210,12 +234,16 @@ def main(argv=None) -> int:
         "config": {
             "workload": f"gemma-2-2b linear stack: {args.layers} layers x 7 projections, batch 1",
             "gemvs_per_step": len(flat),
+            "launches_per_step": len(stack) * len(GROUPS),
             "weights_per_step": weights,
             "se12_bytes_per_step": se12_bytes,
             "bf16_bytes_per_step": bf16_bytes,
             "batch": 1,
         },
     }
+
+    result["one_launch_per_gemv"] = {"ms_per_step": round(ms_sep, 4), "gbps": round(bf16_bytes / (ms_sep * 1e-3) / 1e9, 1),
+                                     "launches_per_step": len(flat)}
 
     # dominant kernel: the 26 down_proj GEMVs (2304x9216, 31.9 MB of streams
     # each, 830 MB in all: every launch reads cold HBM), timed on the replay
@@ -245,25 +273,43 @@ def main(argv=None) -> int:
     del g_down
 
     if not args.only_fused:
+        # hipBLASLt BF16 with the same grouping: one GEMV over concatenated weights
+        cat = []
+        for layer in stack:
+            cat.append([(torch.cat([layer[i]["w"] for i in grp]) if len(grp) > 1 else layer[grp[0]]["w"], layer[grp[0]]["x"])
+                        for grp in GROUPS])
+
         def bf16_step():
+            for layer in cat:
+                for w, x in layer:
+                    torch.nn.functional.linear(x, w)
+
+        def bf16_separate_step():
             for e in flat:
                 torch.nn.functional.linear(e["x"], e["w"])
 
         g_bf16 = capture(bf16_step)
         ms_bf16 = time_graph(g_bf16, args.steps, args.warmup)
-        raw = [RawBf16MatVecKernel(e["w"], max_batch=1) for e in flat]
+        del g_bf16
+        g_bf16s = capture(bf16_separate_step)
+        ms_bf16_sep = time_graph(g_bf16s, args.steps, args.warmup)
+        del g_bf16s, cat
+        raw = [[RawBf16MatVecKernel(e["w"], max_batch=1) for e in layer] for layer in stack]
 
         def raw_step():
-            for e, r in zip(flat, raw):
-                r.multiply(e["x"], out=e["y"])
+            for layer, rl in zip(stack, raw):
+                for grp in GROUPS:
+                    multiply_grouped([rl[i] for i in grp], layer[grp[0]]["x"], outs=[layer[i]["y"] for i in grp])
 
         g_raw = capture(raw_step)
         ms_raw = time_graph(g_raw, args.steps, args.warmup)
         result["bf16_hipblaslt"] = {"ms_per_step": round(ms_bf16, 4), "gbps": round(bf16_bytes / (ms_bf16 * 1e-3) / 1e9, 1),
-                                   "speedup_of_se12": round(ms_bf16 / ms, 4)}
+                                   "speedup_of_se12": round(ms_bf16 / ms, 4),
+                                   "one_launch_per_gemv_ms": round(ms_bf16_sep, 4),
+                                   "one_launch_per_gemv_speedup_of_se12": round(ms_bf16_sep / ms_sep, 4)}
         result["raw_bf16_twin"] = {"ms_per_step": round(ms_raw, 4), "gbps": round(bf16_bytes / (ms_raw * 1e-3) / 1e9, 1),
                                   "speedup_of_se12": round(ms_raw / ms, 4)}
-        log(f"[bench] hipBLASLt bf16 {ms_bf16:.3f} ms, raw twin {ms_raw:.3f} ms")
+        log(f"[bench] hipBLASLt bf16 {ms_bf16:.3f} ms (one launch per GEMV {ms_bf16_sep:.3f} ms), raw twin {ms_raw:.3f} ms")
         del g_raw, raw
 
     if not args.no_per_shape:

@@ -32,6 +32,7 @@ extern "C" {
 #define SE12_CODEBOOK_SIZE 15
 #define SE12_ESCAPE_CODE 15
 #define SE12_MAX_BATCH 32
+#define SE12_MAX_GROUP 4
 
 /* status codes */
 #define SE12_OK 0
@@ -142,6 +143,20 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out);
  * gemv_raw_bf16.cu:18-25). */
 int se12_gemv(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch, float* y_dev,
               const se12_launch* launch, void* stream);
+
+/* One launch computing y[i] = W_i x for `count` (1..4) handles of one format
+ * bound to matrices with the same number of columns and device (e.g. the q,
+ * k and v projections, or gate and up, which read the same x). Each y[i] is
+ * FP32 [batch, rows_i]. `launch` counts the handles' tile rows together:
+ * blocks = (sum of tile rows) x K splits; NULL selects the default for the
+ * combined shape. Results equal those of separate se12_gemv calls under the
+ * same waves per block and K splits. Same stream, allocation and ordering
+ * rules as se12_gemv; calls on any of the handles must be ordered. No
+ * reference counterpart: it serves a runtime that fuses the projections
+ * that share an input (lws/adapters/cuda/gemv.py:196-226 runs one GEMV per
+ * matrix). */
+int se12_gemv_grouped(se12_handle* const* handles, int32_t count, const void* x_dev, int32_t x_dtype,
+                      int32_t batch, float* const* y_dev, const se12_launch* launch, void* stream);
 
 /* Decodes the whole matrix to row-major BF16 bits [rows, cols] (cropped).
  * Replaces the lws_se12_decode launch plus the device untile/crop of

@@ -26,6 +26,7 @@ X_F32 = 1
 FORMAT_SE12 = 0
 FORMAT_RAW_BF16 = 1
 MAX_BATCH = 32
+MAX_GROUP = 4
 
 c_void_p = ctypes.c_void_p
 c_i32 = ctypes.c_int32
@@ -103,6 +104,10 @@ SIGNATURES = {
     ),
     "se12_default_launch": (c_i32, [c_void_p, c_i32, ctypes.POINTER(Launch)]),
     "se12_gemv": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, ctypes.POINTER(Launch), c_void_p]),
+    "se12_gemv_grouped": (
+        c_i32,
+        [ctypes.POINTER(c_void_p), c_i32, c_void_p, c_i32, c_i32, ctypes.POINTER(c_void_p), ctypes.POINTER(Launch), c_void_p],
+    ),
     "se12_decode": (c_i32, [c_void_p, c_void_p, c_void_p]),
     "se12_decode_rows": (c_i32, [c_void_p, c_void_p, c_i64, c_void_p, c_void_p]),
     "se12_codebook_from_histogram": (c_i32, [ctypes.POINTER(ctypes.c_uint64), c_u8p]),

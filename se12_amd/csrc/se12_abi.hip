@@ -16,6 +16,8 @@
 
 using namespace se12;
 
+static_assert(kMaxGroup == SE12_MAX_GROUP, "group size of the C ABI and the kernels");
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -267,12 +269,11 @@ static int max_threads_for(int32_t bl, bool xf32, bool generic) {
 //    larger ones with short rows (6 for very tall matrices such as an LM
 //    head), and 8 waves with splits of ~36 tiles for rows longer than 32
 //    tiles.
-static void default_launch(const se12_handle* h, int32_t batch, bool xf32, bool generic, int32_t* waves_out,
-                           int32_t* splits_out) {
+static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_cap, int32_t batch, bool xf32,
+                           bool generic, int32_t* waves_out, int32_t* splits_out) {
     const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
     const int64_t mw = max_threads_for(bl, xf32, generic) / 64;
-    const int64_t cus = std::max<int32_t>(1, h->cu_count);
-    const int64_t tr = h->TR, tc = h->TC;
+    const int64_t cus = std::max<int32_t>(1, cu_count);
     int64_t waves, splits = 1;
     if (tr < cus) {
         waves = tc <= 16 ? tc : 8;
@@ -287,7 +288,7 @@ static void default_launch(const se12_handle* h, int32_t batch, bool xf32, bool 
     }
     waves = std::max<int64_t>(1, std::min(waves, mw));
     *waves_out = (int32_t)waves;
-    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(splits, h->s_cap));
+    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(splits, s_cap));
 }
 
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
@@ -296,7 +297,7 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
     int32_t waves, splits;
     const bool generic = h->K % SE12_TILE_COLS != 0 ||
                          (h->format == SE12_FORMAT_RAW_BF16 && h->N % SE12_TILE_ROWS != 0);
-    default_launch(h, batch, false, generic, &waves, &splits);
+    default_launch(h->TR, h->TC, h->cu_count, h->s_cap, batch, false, generic, &waves, &splits);
     out->threads_per_block = waves * 64;
     out->blocks = h->TR * splits;
     return SE12_OK;
@@ -305,85 +306,124 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
 // Picks the kernel variant for a launch shape: a wave that owns 4 or more
 // tiles streams them with the next tile's loads in flight (PF) when the
 // block's register budget allows; otherwise it takes one tile per round.
-static GemvPlan plan_gemv(const se12_handle* h, int32_t bl, bool xf32, bool generic, int32_t waves, int32_t splits) {
+static GemvPlan plan_gemv(int64_t tr, int64_t tc, bool raw, int32_t bl, bool xf32, bool generic, int32_t waves,
+                          int32_t splits) {
     GemvPlan p{};
     p.batch = bl;
     p.xf32 = xf32;
-    p.raw = h->format == SE12_FORMAT_RAW_BF16;
+    p.raw = raw;
     p.generic = generic;
     p.waves = waves;
-    p.blocks = h->TR * splits;
+    p.blocks = (int32_t)(tr * splits);
     p.lds = gemv_lds_bytes(waves, bl);
     p.g = 1;
-    const int64_t per_wave = ceil_div(ceil_div(h->TC, splits), waves);
+    const int64_t per_wave = ceil_div(ceil_div(tc, splits), waves);
     p.pf = !generic && per_wave >= 4 && waves * 64 <= gemv_max_threads(bl, xf32, p.raw, 1, true, false);
     return p;
 }
 
-int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, const se12_launch* launch,
-              void* stream) {
-    if (!h) return fail(SE12_E_INVALID, "se12_gemv: NULL handle");
-    if (!x || !y) return fail(SE12_E_INVALID, "se12_gemv: NULL x or y");
-    if (x_dtype != SE12_X_BF16 && x_dtype != SE12_X_F32) return fail(SE12_E_INVALID, "se12_gemv: unknown x_dtype %d", x_dtype);
-    if (batch < 1 || batch > h->max_batch)
-        return fail(SE12_E_INVALID, "se12_gemv: batch %d outside [1, %d] (the handle's max_batch)", batch, h->max_batch);
+// One GEMV launch (per 4 batch rows) over `count` handles that share x: a
+// single matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped.
+static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, const void* x, int32_t x_dtype,
+                      int32_t batch, float* const* ys, const se12_launch* launch, void* stream) {
+    if (count < 1 || count > kMaxGroup) return fail(SE12_E_INVALID, "%s: %d matrices, expected 1..%d", fn, count, kMaxGroup);
+    if (!x) return fail(SE12_E_INVALID, "%s: NULL x", fn);
+    if (x_dtype != SE12_X_BF16 && x_dtype != SE12_X_F32) return fail(SE12_E_INVALID, "%s: unknown x_dtype %d", fn, x_dtype);
+    int64_t tr_total = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        const se12_handle* h = hs[i];
+        if (!h) return fail(SE12_E_INVALID, "%s: NULL handle %d", fn, i);
+        if (!ys[i]) return fail(SE12_E_INVALID, "%s: NULL y %d", fn, i);
+        if (batch < 1 || batch > h->max_batch)
+            return fail(SE12_E_INVALID, "%s: batch %d outside [1, %d] (the handle's max_batch)", fn, batch, h->max_batch);
+        if (h->K != hs[0]->K || h->format != hs[0]->format || h->device != hs[0]->device)
+            return fail(SE12_E_INVALID, "%s: grouped matrices need one K, one format and one device", fn);
+        tr_total += h->TR;
+    }
+    const se12_handle* h0 = hs[0];
     const bool xf32 = x_dtype == SE12_X_F32;
-    const bool raw = h->format == SE12_FORMAT_RAW_BF16;
+    const bool raw = h0->format == SE12_FORMAT_RAW_BF16;
     const size_t esize = xf32 ? 4 : 2;
     // FAST kernels need whole K tiles and 16-byte aligned BF16 rows of x (and,
     // for the raw twin, whole tile rows of an aligned W); the rest run GENERIC
-    const bool generic = xf32 || h->K % SE12_TILE_COLS != 0 || !aligned16(x) ||
-                         (raw && (h->N % SE12_TILE_ROWS != 0 || !aligned16(h->wraw)));
+    bool generic = xf32 || h0->K % SE12_TILE_COLS != 0 || !aligned16(x);
+    for (int32_t i = 0; i < count; ++i)
+        generic = generic || (raw && (hs[i]->N % SE12_TILE_ROWS != 0 || !aligned16(hs[i]->wraw)));
     const int32_t b_first = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
     int32_t waves, splits;
     if (launch) {
         const int max_threads = max_threads_for(b_first, xf32, generic);
         if (launch->threads_per_block < 64 || launch->threads_per_block > max_threads ||
             launch->threads_per_block % 64 != 0)
-            return fail(SE12_E_INVALID, "se12_gemv: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d",
+            return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d", fn,
                         launch->threads_per_block, max_threads, batch);
-        if (launch->blocks <= 0 || launch->blocks % h->TR != 0)
-            return fail(SE12_E_INVALID, "se12_gemv: blocks %d must be a positive multiple of the %d tile rows",
-                        launch->blocks, h->TR);
+        if (launch->blocks <= 0 || launch->blocks % tr_total != 0)
+            return fail(SE12_E_INVALID, "%s: blocks %d must be a positive multiple of the %lld tile rows", fn,
+                        launch->blocks, (long long)tr_total);
         waves = launch->threads_per_block / 64;
-        splits = launch->blocks / h->TR;
-        if (splits > h->s_cap)
-            return fail(SE12_E_CAPACITY, "se12_gemv: %d K splits exceed the handle's limit %d", splits, h->s_cap);
+        splits = (int32_t)(launch->blocks / tr_total);
+        if (splits > h0->s_cap)
+            return fail(SE12_E_CAPACITY, "%s: %d K splits exceed the handle's limit %d", fn, splits, h0->s_cap);
     } else {
-        default_launch(h, batch, xf32, generic, &waves, &splits);
+        default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, &waves, &splits);
     }
+    if (tr_total * splits > INT32_MAX) return fail(SE12_E_INVALID, "%s: grid too large", fn);
     DeviceScope ds;
-    SE12_HIP(ds.enter(h->device));
+    SE12_HIP(ds.enter(h0->device));
     hipStream_t st = static_cast<hipStream_t>(stream);
     for (int32_t b0 = 0; b0 < batch; b0 += kGemvMaxBatchPerLaunch) {
         const int32_t bl = std::min<int32_t>(kGemvMaxBatchPerLaunch, batch - b0);
-        GemvArgs a{};
-        a.sm = h->s.sm_dev;
-        a.ec = h->s.ec_dev;
-        a.esc = h->s.esc_dev;
-        a.lut = h->lut;
-        a.info = h->info;
-        a.fb_raw = h->s.fallback_raw_dev;
-        a.wraw = h->wraw;
-        a.x = static_cast<const char*>(x) + (size_t)b0 * h->K * esize;
-        a.y = y + (size_t)b0 * h->N;
-        a.partial = h->partial;
-        a.counters = h->counters;
-        a.N = h->N;
-        a.K = h->K;
-        a.Np = h->Np;
-        a.TR = h->TR;
-        a.TC = h->TC;
-        a.S = splits;
-        const bool gen = generic || !aligned16(a.x);
-        const GemvPlan p = plan_gemv(h, bl, xf32, gen, waves, splits);
-        if ((int64_t)(p.lds + kLutBytes) > h->lds_per_block)
-            return fail(SE12_E_CAPACITY, "se12_gemv: launch needs %zu bytes of LDS, the device allows %lld", p.lds,
-                        (long long)h->lds_per_block);
-        hipError_t e = launch_gemv(a, p, st);
-        if (e != hipSuccess) return fail(SE12_E_HIP, "se12_gemv launch: %s", hipGetErrorString(e));
+        GemvGroupArgs g{};
+        g.count = count;
+        int32_t start = 0;
+        for (int32_t i = 0; i < count; ++i) {
+            const se12_handle* h = hs[i];
+            GemvArgs& a = g.m[i];
+            a.sm = h->s.sm_dev;
+            a.ec = h->s.ec_dev;
+            a.esc = h->s.esc_dev;
+            a.lut = h->lut;
+            a.info = h->info;
+            a.fb_raw = h->s.fallback_raw_dev;
+            a.wraw = h->wraw;
+            a.x = static_cast<const char*>(x) + (size_t)b0 * h->K * esize;
+            a.y = ys[i] + (size_t)b0 * h->N;
+            a.partial = h->partial;
+            a.counters = h->counters;
+            a.N = h->N;
+            a.K = h->K;
+            a.Np = h->Np;
+            a.TR = h->TR;
+            a.TC = h->TC;
+            a.S = splits;
+            g.tr_start[i] = start;
+            start += h->TR;
+        }
+        for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
+        const bool gen = generic || !aligned16(g.m[0].x);
+        const GemvPlan p = plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
+        if ((int64_t)(p.lds + kLutBytes) > h0->lds_per_block)
+            return fail(SE12_E_CAPACITY, "%s: launch needs %zu bytes of LDS, the device allows %lld", fn, p.lds,
+                        (long long)h0->lds_per_block);
+        hipError_t e = launch_gemv(g, p, st);
+        if (e != hipSuccess) return fail(SE12_E_HIP, "%s launch: %s", fn, hipGetErrorString(e));
     }
     return SE12_OK;
+}
+
+int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, const se12_launch* launch,
+              void* stream) {
+    if (!h) return fail(SE12_E_INVALID, "se12_gemv: NULL handle");
+    if (!x || !y) return fail(SE12_E_INVALID, "se12_gemv: NULL x or y");
+    se12_handle* hs[1] = {h};
+    float* ys[1] = {y};
+    return gemv_group("se12_gemv", hs, 1, x, x_dtype, batch, ys, launch, stream);
+}
+
+int se12_gemv_grouped(se12_handle* const* handles, int32_t count, const void* x, int32_t x_dtype, int32_t batch,
+                      float* const* y, const se12_launch* launch, void* stream) {
+    if (!handles || !y) return fail(SE12_E_INVALID, "se12_gemv_grouped: NULL handles or y");
+    return gemv_group("se12_gemv_grouped", handles, count, x, x_dtype, batch, y, launch, stream);
 }
 
 static DecodeArgs decode_args(const se12_handle* h, uint16_t* out) {

@@ -10,6 +10,8 @@
 //
 // Grid: block = W wave64s, one (tile row, K split) per block: blockIdx.x =
 // tile row, blockIdx.y = split s, covering the K tiles [s*TC/S, (s+1)*TC/S).
+// A grouped launch serves up to 4 matrices with the same K (q/k/v, gate/up)
+// that share x: their tile rows follow one another along blockIdx.x.
 // Wave w of a block takes the split's tiles w, w + W, w + 2W, ... so in each
 // round the block's waves read W consecutive tiles (contiguous HBM). The
 // launch shape (W, S) alone fixes every accumulation order.
@@ -182,14 +184,19 @@ struct Round {
 
 template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC>
 __global__ __launch_bounds__(gemv_max_threads(B, XF32, RAW, G, PF, GENERIC))
-__attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(GemvArgs a) {
+__attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(GemvGroupArgs ga) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) float red[];
+    // the block's matrix (wave-uniform) and its tile row
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i) mi += (i < ga.count && (int)blockIdx.x >= ga.tr_start[i]) ? 1 : 0;
+    const GemvArgs& a = ga.m[mi];
+    const int tr = (int)blockIdx.x - ga.tr_start[mi];
     const int W = blockDim.x >> 6;
     const uint32_t lane = threadIdx.x & 63u;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int S = a.S;
-    const int tr = blockIdx.x;
     const int s = blockIdx.y;
     const int kb = (int)(((uint32_t)s * (uint32_t)a.TC) / (uint32_t)S);
     const int ke = (int)(((uint32_t)(s + 1) * (uint32_t)a.TC) / (uint32_t)S);
@@ -319,13 +326,15 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
 namespace {
 
 template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC>
-hipError_t go(const GemvArgs& a, int threads, int blocks, size_t lds, hipStream_t stream) {
-    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC>), dim3(a.TR, a.S), dim3(threads), lds, stream, a);
+hipError_t go(const GemvGroupArgs& a, int threads, int blocks, size_t lds, hipStream_t stream) {
+    (void)blocks;
+    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC>), dim3(a.tr_start[a.count], a.m[0].S), dim3(threads), lds,
+                       stream, a);
     return hipGetLastError();
 }
 
 template <int B, bool RAW>
-hipError_t launch_b(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
+hipError_t launch_b(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream) {
     const int threads = p.waves * 64;
     if (p.generic)
         return p.xf32 ? go<B, true, RAW, 1, false, true>(a, threads, p.blocks, p.lds, stream)
@@ -336,7 +345,7 @@ hipError_t launch_b(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
 
 }  // namespace
 
-hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t stream) {
+hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream) {
     switch (p.batch * 2 + (p.raw ? 1 : 0)) {
         case 2: return launch_b<1, false>(a, p, stream);
         case 3: return launch_b<1, true>(a, p, stream);

@@ -24,6 +24,17 @@ struct GemvArgs {
     int32_t S;                // K splits per tile row
 };
 
+// One launch over up to kMaxGroup matrices that share x (same K): the grid's
+// rows are the matrices' tile rows one after another, matrix i starting at
+// grid row tr_start[i] (tr_start[count] = the grid's rows).
+constexpr int kMaxGroup = 4;
+
+struct GemvGroupArgs {
+    GemvArgs m[kMaxGroup];
+    int32_t tr_start[kMaxGroup + 1];
+    int32_t count;
+};
+
 // How one GEMV launch runs: the launch shape (waves per block, blocks =
 // tile rows x splits) fixes the results; the variant (tiles per round `g`,
 // prefetch `pf`, `generic` edge handling) only changes speed.
@@ -104,7 +115,7 @@ constexpr int gemv_waves_per_simd(int batch, bool raw, int g, bool pf, bool gene
 // 1 KiB pair table is static)
 inline size_t gemv_lds_bytes(int waves, int batch) { return (size_t)waves * batch * 16 * sizeof(float); }
 
-hipError_t launch_gemv(const GemvArgs& a, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream);
 // Bind-time sidecar: one word per tile (fallback rank, or the chunks holding
 // escape codes) and the fallback tile count.

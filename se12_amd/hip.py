@@ -166,6 +166,45 @@ class RawBf16MatVecKernel(_GemvBase):
         self.handle = bind_raw_bf16(self.weights, max_batch)
 
 
+def multiply_grouped(kernels, activations: torch.Tensor, launch: LaunchConfiguration | None = None,
+                     outs: list[torch.Tensor] | None = None) -> list[torch.Tensor]:
+    """y_i = x . W_i^T for up to 4 bound matrices with the same K (e.g. q, k, v
+    or gate, up) in one launch; all of one format (fused SE12 or raw twin).
+    `launch` counts the matrices' tile rows together (blocks = their sum x K
+    splits). Outputs equal separate `multiply` calls under the same waves per
+    block and K splits."""
+    kernels = list(kernels)
+    if not 1 <= len(kernels) <= nat.MAX_GROUP:
+        raise ValueError(f"1..{nat.MAX_GROUP} matrices per grouped launch, got {len(kernels)}")
+    k0 = kernels[0]
+    x = activations.unsqueeze(0) if activations.dim() == 1 else activations
+    for k in kernels:
+        if k.cols != k0.cols or k.device != k0.device or type(k) is not type(k0):
+            raise ValueError("grouped matrices need one K, one device and one format")
+    if x.dim() != 2 or x.shape[1] != k0.cols:
+        raise ValueError(f"activations must be [B, {k0.cols}], got {tuple(activations.shape)}")
+    if x.device != k0.device:
+        raise ValueError(f"activations on {x.device}, weights on {k0.device}")
+    if x.dtype == torch.bfloat16:
+        xd = nat.X_BF16
+    elif x.dtype == torch.float32:
+        xd = nat.X_F32
+    else:
+        raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
+    x = x.contiguous()
+    b = x.shape[0]
+    if outs is None:
+        outs = [torch.empty((b, k.rows), dtype=torch.float32, device=k0.device) for k in kernels]
+    for k, o in zip(kernels, outs):
+        if o.shape != (b, k.rows) or o.dtype != torch.float32 or not o.is_contiguous():
+            raise ValueError("each out must be a contiguous float32 [B, rows] tensor")
+    n = len(kernels)
+    hs = (ctypes.c_void_p * n)(*[k.handle.raw.value for k in kernels])
+    ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    nat.check(nat.lib().se12_gemv_grouped(hs, n, nat.ptr(x), xd, b, ys, _launch_struct(launch), nat.stream_ptr()))
+    return outs
+
+
 @dataclasses.dataclass(frozen=True)
 class RowIndices:
     """Row indices in request order (weight_decoder.py:18-23)."""

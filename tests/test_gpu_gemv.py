@@ -7,6 +7,8 @@ deterministic, and a captured HIP graph replays to the eager result."""
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -242,3 +244,59 @@ def test_bad_arguments_raise(gpu):
     with pytest.raises(nat.Se12Error):
         k.multiply(torch.zeros((1, 512), dtype=torch.bfloat16, device=gpu),
                    launch=LaunchConfiguration(ThreadsPerBlock(64), BlockCount(5)))
+
+
+def test_grouped_launch_equals_separate_launches(gpu):
+    """q/k/v-like matrices sharing x in one launch: bit-identical to separate
+    launches under the same waves per block and K splits, and within the
+    tolerance of the oracle under the default launch."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped
+    from se12_amd.launch import BlockCount, LaunchConfiguration, ThreadsPerBlock
+
+    cols = 2304
+    shapes = [(272, cols), (128, cols), (48, cols)]
+    bits = [heavy_tailed_bf16(r, c, seed=40 + i) for i, (r, c) in enumerate(shapes)]
+    encs = [o.encode(b.reshape(-1), r, c) for b, (r, c) in zip(bits, shapes)]
+    kerns = [Se12MatVecKernel(to_device(e, gpu), max_batch=8) for e in encs]
+    raws = [RawBf16MatVecKernel(bf16_tensor(b, gpu), max_batch=8) for b in bits]
+    tr_total = sum(-(-r // 16) for r, _ in shapes)
+    for batch in (1, 3, 6):
+        xb = _x(batch, cols, seed=50 + batch)
+        x = bf16_tensor(xb, gpu)
+        ys = multiply_grouped(kerns, x)
+        for y, e in zip(ys, encs):
+            ref = o.gemv_reference(e, o.bf16_bits_to_f32(xb))
+            assert max_rel_error(y, ref) <= REL_TOL
+        for waves, splits in ((3, 1), (9, 1), (4, 3)):
+            if batch >= 4 and waves > 8:
+                continue
+            grouped = LaunchConfiguration(ThreadsPerBlock(64 * waves), BlockCount(tr_total * splits))
+            ys = multiply_grouped(kerns, x, launch=grouped)
+            ysr = multiply_grouped(raws, x, launch=grouped)
+            for k, r, y, yr, (rows, _) in zip(kerns, raws, ys, ysr, shapes):
+                single = LaunchConfiguration(ThreadsPerBlock(64 * waves), BlockCount(-(-rows // 16) * splits))
+                assert torch.equal(y, k.multiply(x, launch=single)), (batch, waves, splits)
+                assert torch.equal(yr, y), (batch, waves, splits)
+
+
+def test_grouped_launch_rejects_mixed_groups(gpu):
+    from se12_amd import _native as nat
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped
+
+    _, e1 = normal_case(64, 512, seed=3)
+    _, e2 = normal_case(64, 768, seed=4)
+    k1 = Se12MatVecKernel(to_device(e1, gpu))
+    k2 = Se12MatVecKernel(to_device(e2, gpu))
+    r1 = RawBf16MatVecKernel(bf16_tensor(o.decode(e1), gpu))
+    x = torch.zeros((1, 512), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError):
+        multiply_grouped([k1, k2], x)
+    with pytest.raises(ValueError):
+        multiply_grouped([k1, r1], x)
+    with pytest.raises(ValueError):
+        multiply_grouped([k1] * 5, x)
+    hs = (ctypes.c_void_p * 2)(k1.handle.raw.value, k2.handle.raw.value)
+    y = torch.empty((1, 64), dtype=torch.float32, device=gpu)
+    ys = (ctypes.c_void_p * 2)(y.data_ptr(), y.data_ptr())
+    assert nat.lib().se12_gemv_grouped(hs, 2, nat.ptr(x), nat.X_BF16, 1, ys, None, nat.stream_ptr()) == nat.SE12_E_INVALID
+    assert "one K" in nat.last_error()

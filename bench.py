@@ -36,6 +36,10 @@ import torch
 
 METRIC = "BF16-equiv weight GB/s + us per fused SE12 GEMV at batch 1; decode tok/s"
 HBM_PEAK_GBPS = 8000.0
+# HBM bytes per launch of the dominant kernel, measured with two rocprofv3
+# counter runs (FETCH_SIZE, WRITE_SIZE) scaled by the same counters' reading
+# of a 256 MiB device copy; null in the output when the file is absent
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "gemv_fused_b1_down_proj_traffic.json")
 LAYERS = 26
 HIDDEN, INTER, QDIM, KVDIM = 2304, 9216, 2048, 1024
 # (name, rows N, cols K, input vector)
@@ -63,7 +67,41 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-per-shape", action="store_true")
     p.add_argument("--only-fused", action="store_true", help="skip the BF16 and raw-twin comparisons (profiling)")
+    p.add_argument("--profile-down", action="store_true",
+                   help="only the dominant kernel (26 down_proj launches per step) and a 256 MiB device copy of known "
+                        "size, for hardware-counter runs")
     return p.parse_args(argv)
+
+
+def profile_down(args, device) -> int:
+    """The dominant kernel alone: the 26 layers' 2304x9216 down_proj GEMVs
+    (cold: 830 MB of streams), then a 256 MiB device-to-device copy whose byte
+    counts calibrate the FETCH_SIZE / WRITE_SIZE counters."""
+    from se12_amd.hip import Se12MatVecKernel, encode_on_device
+
+    gen = torch.Generator(device=device)
+    n, k = 2304, 9216
+    down = []
+    for layer in range(args.layers):
+        gen.manual_seed(layer * 100 + 6)
+        w = (torch.randn((n, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        gen.manual_seed(1_000_000 + layer * 10 + 2)
+        x = torch.randn((1, k), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+        kern = Se12MatVecKernel(encode_on_device(w), max_batch=1)
+        down.append({"kern": kern, "x": x, "y": torch.empty((1, n), dtype=torch.float32, device=device)})
+        del w
+    g = capture(lambda: [e["kern"].multiply(e["x"], out=e["y"]) for e in down])
+    ms = time_graph(g, args.steps, args.warmup)
+    src = torch.empty(64 << 20, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": "down_proj 2304x9216 fused GEMV", "us_per_launch": round(ms * 1e3 / len(down), 3),
+                      "launches": len(down) * (args.steps + args.warmup + 2), "copy_bytes": src.numel() * 4,
+                      "copies": 3}), flush=True)
+    return 0
 
 
 def build_stack(layers: int, device):
@@ -176,6 +214,8 @@ def main(argv=None) -> int:
     _native.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.profile_down:
+        return profile_down(args, dev)
     props = HipGpuProbe(0).properties()
     log(f"[bench] device {props.name} {props.arch} CUs={props.compute_units}")
     t0 = time.perf_counter()
@@ -255,13 +295,17 @@ def main(argv=None) -> int:
     bytes_launch = down[0]["enc"].byte_size() + down[0]["k"] * 2 + down[0]["n"] * 4
     achieved = bytes_launch / (us_launch * 1e-6) / 1e9
     launch = down[0]["kern"].default_launch(1)
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("traffic_bytes_per_launch")
     result["roofline"] = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBPS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBPS, 4),
-        "traffic": None,
+        "traffic": traffic,
         "kernel": "se12::gemv_kernel (fused SE12 decode + GEMV, batch 1)",
         "shape": [down[0]["n"], down[0]["k"]],
         "launch": {"threads_per_block": launch.threads_per_block.value, "blocks": launch.blocks.value},

@@ -255,25 +255,26 @@ static int max_threads_for(int32_t bl, bool xf32, bool generic) {
 
 // The default launch, re-derived for MI355X (256 CUs in 8 XCDs, wave64) from
 // sweeps of every (waves, splits) pair on cold data at the Gemma-2 2B/9B/27B
-// shapes and the 256000x2304 LM head. A batch-1 GEMV is one pass over the
-// streams. What pays: enough tiles in flight per CU to cover HBM latency but
-// not so many that every wave's data lands at the end of the pass (the
-// decode would then all run after the last byte arrives), and no cross-block
-// K reduction (S > 1 adds a store -> counter -> reload round trip to the end
-// of every block) unless a row is very long:
-//  - fewer tile rows than CUs: one wave per K tile for rows of <= 16 tiles;
-//    8 waves (each streaming its tiles with the next one prefetched) for
-//    longer rows; very long rows on very few tile rows are split so that
-//    every CU gets a block;
-//  - many tile rows: 3 waves for matrices up to ~50 MB of streams, 8 for
-//    larger ones with short rows (6 for very tall matrices such as an LM
-//    head), and 8 waves with splits of ~36 tiles for rows longer than 32
-//    tiles.
+// shapes, the grouped q/k/v and gate/up shapes and the 256000x2304 LM head.
+// A batch-1 GEMV is one pass over the streams. What pays: enough tiles in
+// flight per CU to cover HBM latency but not so many that every wave's data
+// lands at the end of the pass (the decode would then all run after the last
+// byte arrives), and no cross-block K reduction (S > 1 adds a store ->
+// counter -> reload round trip to the end of every block) unless rows are
+// very long. By tiles per CU (T / CUs), for rows of at most 32 tiles:
+//  - fewer tile rows than CUs, or at most 10 tiles per CU: one wave per K
+//    tile (rows longer than 16 tiles: 8 waves streaming with prefetch);
+//  - up to 32 tiles per CU: 3 waves; up to 64: about 2 tiles per wave;
+//    more (very tall matrices such as an LM head): 6 waves;
+// rows longer than 32 tiles on many tile rows: 8 waves and splits of ~36
+// tiles; very long rows on very few tile rows are split so that every CU
+// gets a block.
 static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_cap, int32_t batch, bool xf32,
                            bool generic, int32_t* waves_out, int32_t* splits_out) {
     const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
     const int64_t mw = max_threads_for(bl, xf32, generic) / 64;
     const int64_t cus = std::max<int32_t>(1, cu_count);
+    const int64_t tiles = tr * tc;
     int64_t waves, splits = 1;
     if (tr < cus) {
         waves = tc <= 16 ? tc : 8;
@@ -281,10 +282,14 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     } else if (tc > 32) {
         waves = 8;
         splits = std::max<int64_t>(1, (tc + 18) / 36);
-    } else if (tr * tc <= 8192) {
+    } else if (tiles <= 10 * cus) {
+        waves = std::min<int64_t>(16, tc);
+    } else if (tiles <= 32 * cus) {
         waves = std::min<int64_t>(3, tc);
+    } else if (tiles <= 64 * cus) {
+        waves = std::max<int64_t>(1, std::min<int64_t>(tc, std::max<int64_t>(2, tc / 2)));
     } else {
-        waves = std::min<int64_t>(tr >= 4096 ? 6 : 8, tc);
+        waves = std::min<int64_t>(6, tc);
     }
     waves = std::max<int64_t>(1, std::min(waves, mw));
     *waves_out = (int32_t)waves;

@@ -21,7 +21,11 @@ step through hipBLASLt BF16 (torch.nn.functional.linear) and through the
 raw-BF16 twin kernel; per-shape microseconds; a roofline object for the dominant kernel - the fused GEMV at
 the 2304x9216 down_proj shape, timed live as 26 back-to-back launches over the
 26 layers' (cold) matrices; and the oracle's numpy decode + matmul timed on
-the host as the CPU baseline.
+the host as the CPU baseline. Two more objects: the batch sweep B = 1..32 at
+the Gemma-2-9B gate_proj shape 14336x3584 against hipBLASLt BF16 (the
+crossover from the dot2 kernel to the MFMA kernel), and batch-1 stress shapes
+with heavy-tailed weights (tied LM head 256000x2304, Gemma-2-27B down_proj
+4608x36864).
 """
 
 from __future__ import annotations
@@ -66,6 +70,8 @@ def parse_args(argv=None):
     p.add_argument("--layers", type=int, default=LAYERS, help="layers in the stack (26 = Gemma-2-2B)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-per-shape", action="store_true")
+    p.add_argument("--no-batch-sweep", action="store_true")
+    p.add_argument("--no-stress", action="store_true")
     p.add_argument("--only-fused", action="store_true", help="skip the BF16 and raw-twin comparisons (profiling)")
     p.add_argument("--profile-down", action="store_true",
                    help="only the dominant kernel (26 down_proj launches per step) and a 256 MiB device copy of known "
@@ -168,6 +174,103 @@ def time_graph(g, steps: int, warmup: int, flush=None) -> float:
         end.synchronize()
         total += start.elapsed_time(end)
     return total / steps
+
+
+def cold_rotation(nbytes: int) -> int:
+    """Matrices to rotate through so that a pass streams from HBM (>= 1.1 GB,
+    over 4x the 256 MB Infinity Cache)."""
+    return max(2, -(-int(1.1e9) // nbytes))
+
+
+def batch_sweep(device, batches=(1, 2, 4, 8, 16, 32)) -> dict:
+    """Gemma-2-9B gate_proj 14336x3584, BF16 N(0, 0.02): the fused product at
+    each batch (the dot2 kernel up to 4 rows, the MFMA kernel from 5; one pass
+    over the weights either way) against hipBLASLt BF16 at the same batch,
+    each timed per launch over a rotation of cold matrices."""
+    from se12_amd.hip import Se12MatVecKernel, encode_on_device
+    from se12_amd.launch import uses_mfma
+
+    n, k = 14336, 3584
+    gen = torch.Generator(device=device)
+    ws, kerns = [], []
+    r_se12 = cold_rotation(int(n * k * 1.504))
+    r_bf16 = cold_rotation(2 * n * k)
+    for r in range(max(r_se12, r_bf16)):
+        gen.manual_seed(9_000 + r)
+        w = (torch.randn((n, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        if r < r_se12:
+            kerns.append(Se12MatVecKernel(encode_on_device(w), max_batch=max(batches)))
+        if r < r_bf16:
+            ws.append(w)
+    out = {"shape": [n, k], "rotation": {"se12": r_se12, "bf16": r_bf16}, "points": []}
+    for b in batches:
+        gen.manual_seed(9_999 + b)
+        x = torch.randn((b, k), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+        y = torch.empty((b, n), dtype=torch.float32, device=device)
+        g = capture(lambda x=x, y=y: [kk.multiply(x, out=y) for kk in kerns])
+        us = time_graph(g, 10, 3) * 1e3 / len(kerns)
+        gb = capture(lambda x=x: [torch.nn.functional.linear(x, w) for w in ws])
+        us_b = time_graph(gb, 10, 3) * 1e3 / len(ws)
+        del g, gb
+        lc = kerns[0].default_launch(b)
+        pt = {"batch": b, "kernel": "mfma" if uses_mfma(b) else "dot2", "us": round(us, 3),
+              "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
+              "se12_gbps": round(kerns[0].tensor.byte_size() / (us * 1e-6) / 1e9, 1),
+              "bf16_hipblaslt_us": round(us_b, 3), "speedup_of_se12": round(us_b / us, 4),
+              "launch": [lc.threads_per_block.value, lc.blocks.value]}
+        out["points"].append(pt)
+        log(f"[bench] batch sweep {pt}")
+    return out
+
+
+def heavy_tailed(n: int, k: int, seed: int, device) -> torch.Tensor:
+    """Student-t (df 3) scaled to std 0.02 with 0.1% outliers at +-8 sigma, BF16."""
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    z = torch.randn((n, k), generator=gen, device=device)
+    chi2 = torch.randn((3, n, k), generator=gen, device=device).square().sum(0)
+    w = z / torch.sqrt(chi2 / 3.0) / (3.0 ** 0.5) * 0.02
+    flat = w.view(-1)
+    n_out = max(1, flat.numel() // 1000)
+    idx = torch.randint(0, flat.numel(), (n_out,), generator=gen, device=device)
+    sign = torch.randint(0, 2, (n_out,), generator=gen, device=device).float() * 2 - 1
+    flat[idx] = sign * 0.16
+    return w.to(torch.bfloat16)
+
+
+def stress(device) -> dict:
+    """Batch-1 products at the tied LM head 256000x2304 and the Gemma-2-27B
+    down_proj 4608x36864 with heavy-tailed weights (escape and fallback
+    paths), against hipBLASLt BF16; the cache is flushed before each launch."""
+    from se12_amd.hip import Se12MatVecKernel, encode_on_device
+
+    flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=device)
+    out = {}
+    for name, n, k, seed in (("lm_head", 256000, 2304, 11), ("down_27b", 4608, 36864, 12)):
+        w = heavy_tailed(n, k, seed, device)
+        enc = encode_on_device(w)
+        kern = Se12MatVecKernel(enc, max_batch=1)
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed + 100)
+        x = torch.randn((1, k), generator=gen, device=device).to(torch.bfloat16)
+        y = torch.empty((1, n), dtype=torch.float32, device=device)
+        g = capture(lambda: kern.multiply(x, out=y))
+        us = time_graph(g, 10, 3, flush=lambda: flush_buf.fill_(1.0)) * 1e3
+        gb = capture(lambda: torch.nn.functional.linear(x, w))
+        us_b = time_graph(gb, 10, 3, flush=lambda: flush_buf.fill_(1.0)) * 1e3
+        lc = kern.default_launch(1)
+        out[name] = {"shape": [n, k], "us": round(us, 3), "se12_bytes": enc.byte_size(),
+                     "bytes_per_weight": round(enc.byte_size() / (n * k), 4),
+                     "se12_gbps": round(enc.byte_size() / (us * 1e-6) / 1e9, 1),
+                     "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
+                     "bf16_hipblaslt_us": round(us_b, 3), "speedup_of_se12": round(us_b / us, 4),
+                     "fallback_tiles": enc.fallback_tiles, "tiles": enc.tile_grid[0] * enc.tile_grid[1],
+                     "launch": [lc.threads_per_block.value, lc.blocks.value]}
+        log(f"[bench] stress {name}: {out[name]}")
+        del g, gb, kern, enc, w
+        torch.cuda.empty_cache()
+    del flush_buf
+    return out
 
 
 def cpu_baseline(budget_s: float = 12.0) -> dict:
@@ -379,6 +482,14 @@ def main(argv=None) -> int:
             log(f"[bench] {name} {n}x{k}: {per_shape[name]}")
         result["per_shape"] = per_shape
         del flush_buf
+
+    if not args.no_batch_sweep:
+        del stack, flat
+        torch.cuda.empty_cache()
+        result["batch_sweep"] = batch_sweep(dev)
+        torch.cuda.empty_cache()
+    if not args.no_stress:
+        result["stress"] = stress(dev)
 
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")

@@ -75,6 +75,7 @@ struct se12_handle {
     uint32_t* lut;       // [256] pair table
     int64_t n_fallback;
     float* partial;
+    int64_t partial_elems;
     int32_t* counters;
     int32_t max_batch;
     int32_t s_cap;
@@ -124,10 +125,14 @@ static int bind_common(se12_handle* h, int64_t rows, int64_t cols, int32_t max_b
     SE12_HIP(hipGetDeviceProperties(&p, h->device));
     h->cu_count = p.multiProcessorCount;
     h->lds_per_block = (int64_t)p.sharedMemPerBlock;
-    const int32_t b_launch = std::min<int32_t>(max_batch, kGemvMaxBatchPerLaunch);
+    // split-K workspace: S x (rows per launch) x Np floats, for the dot2
+    // path (up to 4 rows per launch, any split count) and the MFMA path (all
+    // rows in one launch, at most kGemmMaxSplits splits)
     if (h->s_cap > 1) {
-        const size_t pe = (size_t)h->s_cap * b_launch * h->Np;
-        SE12_HIP(hipMalloc(&h->partial, pe * sizeof(float)));
+        int64_t pe = (int64_t)h->s_cap * std::min<int32_t>(max_batch, kGemvMaxBatchPerLaunch);
+        if (max_batch >= kGemmMinBatch) pe = std::max<int64_t>(pe, (int64_t)std::min(h->s_cap, kGemmMaxSplits) * max_batch);
+        h->partial_elems = pe * h->Np;
+        SE12_HIP(hipMalloc(&h->partial, (size_t)h->partial_elems * sizeof(float)));
         SE12_HIP(hipMalloc(&h->counters, (size_t)h->TR * sizeof(int32_t)));
         SE12_HIP(hipMemset(h->counters, 0, (size_t)h->TR * sizeof(int32_t)));
     }
@@ -249,6 +254,11 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
 // Largest block (threads) a launch at batch `bl` may use: the lightest
 // kernel variant (one tile per round, no prefetch) of the fused kernel and of
 // its raw twin must fit its VGPR budget.
+// BF16 activations with kGemmMinBatch or more rows take the MFMA kernel (one
+// launch, one pass over the weights); FP32 activations and smaller batches
+// the dot2 kernel, 4 rows per launch.
+static bool uses_mfma(int32_t batch, bool xf32) { return !xf32 && batch >= kGemmMinBatch; }
+
 static int max_threads_for(int32_t bl, bool xf32, bool generic) {
     return std::min(gemv_max_threads(bl, xf32, false, 1, false, generic), gemv_max_threads(bl, xf32, true, 1, false, generic));
 }
@@ -287,7 +297,9 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     } else if (tiles <= 32 * cus) {
         waves = std::min<int64_t>(3, tc);
     } else if (tiles <= 64 * cus) {
-        waves = std::max<int64_t>(1, std::min<int64_t>(tc, std::max<int64_t>(2, tc / 2)));
+        // 2 rows and more per launch: 2 waves (14336x3584, B = 2..4: 17.8 us
+        // against 19.5 with tc / 2 = 7 waves, 19.8 against 26.9 at B = 4)
+        waves = bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, std::max<int64_t>(2, tc / 2)));
     } else {
         waves = std::min<int64_t>(6, tc);
     }
@@ -296,12 +308,44 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(splits, s_cap));
 }
 
+// Row blocks of the MFMA grid: ceil(tile rows / waves) per matrix.
+static int64_t gemm_row_blocks(se12_handle* const* hs, int32_t count, int32_t waves) {
+    int64_t rb = 0;
+    for (int32_t i = 0; i < count; ++i) rb += ceil_div(hs[i]->TR, waves);
+    return rb;
+}
+
+// Default launch of the MFMA kernel, from sweeps on MI355X over the
+// Gemma-2 2B/9B shapes at B = 8..32: the fewest waves per block the x slab
+// loads allow (batch / 8, rounded up). A wave owns a tile row of one K
+// split, so the launch has tile rows x splits waves; the best shapes kept
+// about 2.5 of them per CU (14336x3584: no split; 2304x9216: 4 splits),
+// with 3 or more K tiles per split for the two-tile prefetch.
+static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
+                                int32_t* splits_out) {
+    const se12_handle* h0 = hs[0];
+    int64_t tr = 0;
+    for (int32_t i = 0; i < count; ++i) tr += hs[i]->TR;
+    const int64_t cus = std::max<int32_t>(1, h0->cu_count);
+    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kGemmMaxSplits, (int64_t)h0->s_cap,
+                                                               ceil_div(h0->TC, 3)}));
+    *waves_out = gemm_min_waves(batch);
+    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, (5 * cus + tr) / (2 * tr)));
+}
+
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
     if (!h || !out) return fail(SE12_E_INVALID, "se12_default_launch: NULL argument");
     if (batch < 1 || batch > SE12_MAX_BATCH) return fail(SE12_E_INVALID, "batch must be in [1, %d]", SE12_MAX_BATCH);
     int32_t waves, splits;
     const bool generic = h->K % SE12_TILE_COLS != 0 ||
                          (h->format == SE12_FORMAT_RAW_BF16 && h->N % SE12_TILE_ROWS != 0);
+    se12_handle* hs[1] = {const_cast<se12_handle*>(h)};
+    if (uses_mfma(batch, false)) {
+        gemm_default_launch(hs, 1, batch, &waves, &splits);
+        out->threads_per_block = waves * 64;
+        out->blocks = (int32_t)(gemm_row_blocks(hs, 1, waves) * splits);
+        return SE12_OK;
+    }
     default_launch(h->TR, h->TC, h->cu_count, h->s_cap, batch, false, generic, &waves, &splits);
     out->threads_per_block = waves * 64;
     out->blocks = h->TR * splits;
@@ -327,8 +371,22 @@ static GemvPlan plan_gemv(int64_t tr, int64_t tc, bool raw, int32_t bl, bool xf3
     return p;
 }
 
-// One GEMV launch (per 4 batch rows) over `count` handles that share x: a
-// single matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped.
+static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool generic, int32_t waves, int32_t splits) {
+    GemvPlan p{};
+    p.batch = batch;
+    p.raw = raw;
+    p.generic = generic;
+    p.waves = waves;
+    p.blocks = (int32_t)(row_blocks * splits);
+    p.lds = gemm_lds_bytes(waves, batch);
+    p.g = 1;
+    p.pf = true;
+    return p;
+}
+
+// The launches of one product over `count` handles that share x (a single
+// matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped): one MFMA
+// launch for all rows, or one dot2 launch per 4 rows.
 static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, const void* x, int32_t x_dtype,
                       int32_t batch, float* const* ys, const se12_launch* launch, void* stream) {
     if (count < 1 || count > kMaxGroup) return fail(SE12_E_INVALID, "%s: %d matrices, expected 1..%d", fn, count, kMaxGroup);
@@ -354,30 +412,46 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     bool generic = xf32 || h0->K % SE12_TILE_COLS != 0 || !aligned16(x);
     for (int32_t i = 0; i < count; ++i)
         generic = generic || (raw && (hs[i]->N % SE12_TILE_ROWS != 0 || !aligned16(hs[i]->wraw)));
-    const int32_t b_first = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
+    const bool mfma = uses_mfma(batch, xf32);
+    const int32_t step = mfma ? batch : kGemvMaxBatchPerLaunch;
+    const int32_t b_first = std::min<int32_t>(batch, step);
     int32_t waves, splits;
+    int64_t grid_rows = tr_total;  // grid rows per split: tile rows, or row blocks (MFMA)
     if (launch) {
-        const int max_threads = max_threads_for(b_first, xf32, generic);
-        if (launch->threads_per_block < 64 || launch->threads_per_block > max_threads ||
+        const int max_threads = mfma ? kGemmMaxThreads : max_threads_for(b_first, xf32, generic);
+        const int min_threads = mfma ? 64 * gemm_min_waves(batch) : 64;
+        if (launch->threads_per_block < min_threads || launch->threads_per_block > max_threads ||
             launch->threads_per_block % 64 != 0)
-            return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d", fn,
-                        launch->threads_per_block, max_threads, batch);
-        if (launch->blocks <= 0 || launch->blocks % tr_total != 0)
-            return fail(SE12_E_INVALID, "%s: blocks %d must be a positive multiple of the %lld tile rows", fn,
-                        launch->blocks, (long long)tr_total);
+            return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [%d, %d] at batch %d", fn,
+                        launch->threads_per_block, min_threads, max_threads, batch);
         waves = launch->threads_per_block / 64;
-        splits = (int32_t)(launch->blocks / tr_total);
-        if (splits > h0->s_cap)
-            return fail(SE12_E_CAPACITY, "%s: %d K splits exceed the handle's limit %d", fn, splits, h0->s_cap);
+        if (mfma) grid_rows = gemm_row_blocks(hs, count, waves);
+        if (launch->blocks <= 0 || launch->blocks % grid_rows != 0)
+            return fail(SE12_E_INVALID, "%s: blocks %d must be a positive multiple of the %lld %s", fn, launch->blocks,
+                        (long long)grid_rows, mfma ? "row blocks (tile rows / waves, rounded up, per matrix)" : "tile rows");
+        splits = (int32_t)(launch->blocks / grid_rows);
+        const int32_t cap = mfma ? std::min(h0->s_cap, kGemmMaxSplits) : h0->s_cap;
+        if (splits > cap)
+            return fail(SE12_E_CAPACITY, "%s: %d K splits exceed the limit %d at batch %d", fn, splits, cap, batch);
     } else {
-        default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, &waves, &splits);
+        if (mfma) {
+            gemm_default_launch(hs, count, batch, &waves, &splits);
+            grid_rows = gemm_row_blocks(hs, count, waves);
+        } else {
+            default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, &waves, &splits);
+        }
     }
-    if (tr_total * splits > INT32_MAX) return fail(SE12_E_INVALID, "%s: grid too large", fn);
+    if (grid_rows * splits > INT32_MAX) return fail(SE12_E_INVALID, "%s: grid too large", fn);
     DeviceScope ds;
     SE12_HIP(ds.enter(h0->device));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    for (int32_t b0 = 0; b0 < batch; b0 += kGemvMaxBatchPerLaunch) {
-        const int32_t bl = std::min<int32_t>(kGemvMaxBatchPerLaunch, batch - b0);
+    if (splits > 1)
+        for (int32_t i = 0; i < count; ++i)
+            if ((int64_t)splits * b_first * hs[i]->Np > hs[i]->partial_elems)
+                return fail(SE12_E_CAPACITY, "%s: %d K splits at batch %d exceed handle %d's split-K workspace", fn,
+                            splits, batch, i);
+    for (int32_t b0 = 0; b0 < batch; b0 += step) {
+        const int32_t bl = std::min<int32_t>(step, batch - b0);
         GemvGroupArgs g{};
         g.count = count;
         int32_t start = 0;
@@ -402,15 +476,16 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.TC = h->TC;
             a.S = splits;
             g.tr_start[i] = start;
-            start += h->TR;
+            start += mfma ? (int32_t)ceil_div(h->TR, waves) : h->TR;
         }
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);
-        const GemvPlan p = plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
+        const GemvPlan p = mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
+                                : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
         if ((int64_t)(p.lds + kLutBytes) > h0->lds_per_block)
             return fail(SE12_E_CAPACITY, "%s: launch needs %zu bytes of LDS, the device allows %lld", fn, p.lds,
                         (long long)h0->lds_per_block);
-        hipError_t e = launch_gemv(g, p, st);
+        hipError_t e = mfma ? launch_gemm(g, bl, p, st) : launch_gemv(g, p, st);
         if (e != hipSuccess) return fail(SE12_E_HIP, "%s launch: %s", fn, hipGetErrorString(e));
     }
     return SE12_OK;

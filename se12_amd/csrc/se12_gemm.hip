@@ -1,0 +1,379 @@
+// Batched fused SE12 decode + matrix product for gfx950: Y[b, n] =
+// sum_k W[n, k] X[b, k] for up to 32 BF16 batch rows in ONE pass over the
+// weights (the dot2 kernel in se12_gemv.hip takes 4 rows per launch and so
+// re-reads W once per 4 rows). Same semantics as the reference kernel
+// lws/adapters/cuda/kernels/gemv_se12.cu:50-142 at batch B, which runs one
+// warp per (row, batch) element and reads W B times.
+//
+// Grid: block = W wave64s over W consecutive tile rows (wave w owns tile row
+// W * row_block + w), blockIdx.y = K split s covering the K tiles
+// [s*TC/S, (s+1)*TC/S). A grouped launch serves up to 4 matrices with the
+// same K: their row blocks follow one another along blockIdx.x.
+//
+// Per K tile the block's waves share one copy of the x slab (batch rows x 256
+// columns, BF16) in LDS, double-buffered: every thread requests up to 4
+// pieces of 16 bytes of slab i + 2 while its wave decodes tile i and writes
+// those of slab i + 1 to the other buffer after its MFMAs; the block meets
+// once per K tile. Each wave requests its tile streams two tiles ahead of
+// the decode (the edge-handling variants load and use in turn).
+//
+// A wave decodes its 16x256 tile exactly as the dot2 kernel does (same lane
+// mapping, escapes, fallback tiles), stores the BF16 tile in its own LDS
+// buffer and reads it back in the A-operand layout of
+// v_mfma_f32_16x16x32_bf16 (lane l: weight row l % 16, columns
+// 32 s + 8 (l / 16) .. + 7 of slab s); the B operand is the x slab (lane l:
+// batch row 16 g + l % 16, the same columns). 8 MFMAs per tile and group of
+// 16 batch rows, FP32 accumulate. Rows of both LDS buffers are padded to 528
+// bytes so that the 16-byte reads of 8 lanes per cycle hit distinct banks.
+// Batch rows past the batch in a 16-row group read stale LDS: MFMA output
+// column n depends on B column n only, and those columns are not stored.
+//
+// A wave owns whole tile rows, so there is no cross-wave reduction: it adds
+// its K tiles in ascending order, and for S > 1 the last wave of a tile row to
+// finish (device-scope arrival counter, reset by that wave) adds the S
+// partials in ascending split order. The launch shape (W, S) fixes every sum:
+// the raw-BF16 twin (same kernel, RAW) is bit-identical under one shape.
+//
+// FAST variants need K % 256 == 0 and 16-byte aligned x rows (and, for the
+// raw twin, N % 16 == 0 and an aligned W); GENERIC variants guard loads by
+// the matrix edges and zero weights and x past K (padding can decode to
+// +inf when codebook[0] = 255).
+#include "se12_device.hpp"
+#include "se12_internal.hpp"
+
+namespace se12 {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kRowBytes = 528;                    // 512 B of BF16 + 16 B of padding
+constexpr int kWaveTileBytes = kTileRows * kRowBytes;
+
+template <int BG>
+constexpr int x_slab_bytes() {
+    return 16 * BG * kRowBytes;
+}
+
+// the 16-byte pieces p = tid + k * threads (k < kGemmXPieces) of an x slab:
+// batch row p / 32, columns 8 (p % 32) .. + 7
+struct XPieces {
+    uint4 v[kGemmXPieces];
+};
+
+// Every load here and below is issued unconditionally (indexes clamped into
+// the matrix): a load skipped on some path leaves the compiler unable to
+// count the loads in flight, and it then waits for all of them - the
+// prefetched tiles included - before the next decode.
+template <bool GENERIC>
+__device__ __forceinline__ XPieces load_x_slab(const GemvArgs& a, int batch, int kt, int tid, int threads) {
+    XPieces xr;
+#pragma unroll
+    for (int k = 0; k < kGemmXPieces; ++k) {
+        const int p = min(tid + k * threads, batch * 32 - 1);
+        const uint16_t* row = static_cast<const uint16_t*>(a.x) + (int64_t)(p >> 5) * a.K;
+        const int64_t col = (int64_t)kt * kTileCols + 8 * (p & 31);
+        if constexpr (!GENERIC) {
+            xr.v[k] = *reinterpret_cast<const uint4*>(row + col);
+        } else {
+            uint32_t e[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t lo = row[min(col + 2 * t, a.K - 1)];
+                const uint32_t hi = row[min(col + 2 * t + 1, a.K - 1)];
+                e[t] = (col + 2 * t < a.K ? lo : 0u) | (col + 2 * t + 1 < a.K ? hi << 16 : 0u);
+            }
+            xr.v[k] = make_uint4(e[0], e[1], e[2], e[3]);
+        }
+    }
+    return xr;
+}
+
+// pieces past the slab repeat the last piece: the same bytes to the same
+// address as the thread that owns it
+__device__ __forceinline__ void store_x_slab(char* xb, const XPieces& xr, int batch, int tid, int threads) {
+#pragma unroll
+    for (int k = 0; k < kGemmXPieces; ++k) {
+        const int p = min(tid + k * threads, batch * 32 - 1);
+        *reinterpret_cast<uint4*>(xb + (p >> 5) * kRowBytes + 16 * (p & 31)) = xr.v[k];
+    }
+}
+
+template <bool GENERIC>
+__device__ __forceinline__ void load_raw_rows(uint4 r[4][2], const GemvArgs& a, int tr, int kt, uint32_t lane) {
+    const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int64_t row = (int64_t)tr * kTileRows + 4 * j + (lane >> 4);
+        if constexpr (!GENERIC) {
+            const uint16_t* p = a.wraw + row * a.K + col;
+            r[j][0] = reinterpret_cast<const uint4*>(p)[0];
+            r[j][1] = reinterpret_cast<const uint4*>(p)[1];
+        } else {
+            const uint16_t* p = a.wraw + min(row, a.N - 1) * a.K;
+            uint32_t h[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int64_t c = col + 2 * q;
+                const uint32_t lo = p[min(c, a.K - 1)];
+                const uint32_t hi = p[min(c + 1, a.K - 1)];
+                h[q] = row < a.N ? ((c < a.K ? lo : 0u) | (c + 1 < a.K ? hi << 16 : 0u)) : 0u;
+            }
+            r[j][0] = make_uint4(h[0], h[1], h[2], h[3]);
+            r[j][1] = make_uint4(h[4], h[5], h[6], h[7]);
+        }
+    }
+}
+
+// chunk j of the lane's decoded weights (row 4j + lane/16, 16 columns) into
+// the wave's LDS tile buffer
+__device__ __forceinline__ void stage_chunk(char* buf, int j, uint32_t lane, const uint32_t w[8]) {
+    char* p = buf + (4 * j + (int)(lane >> 4)) * kRowBytes + 32 * (int)(lane & 15u);
+    reinterpret_cast<uint4*>(p)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(p)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
+// weights at columns >= lim of the tile are zeroed
+__device__ __forceinline__ void zero_past_k(uint32_t w[8], int c0, int lim) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+        const int c = c0 + 2 * q;
+        w[q] = (c >= lim) ? 0u : ((c + 1 >= lim) ? (w[q] & 0xFFFFu) : w[q]);
+    }
+}
+
+template <int BG>
+__device__ __forceinline__ void mfma_tile(const char* wb, const char* xb, uint32_t lane, floatx4_t acc[BG]) {
+    const int off = (int)(lane & 15u) * kRowBytes + 16 * (int)(lane >> 4);
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(wb + off + 64 * s));
+#pragma unroll
+        for (int g = 0; g < BG; ++g) {
+            const uint4 bv = *reinterpret_cast<const uint4*>(xb + g * 16 * kRowBytes + off + 64 * s);
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv), acc[g], 0, 0, 0);
+        }
+    }
+}
+
+// orders a wave's own LDS stores before its later loads of the same bytes
+// (and those loads before the next stores): LDS executes one wave's
+// instructions in order, so only the compiler has to be held back
+__device__ __forceinline__ void wave_lds_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <bool RAW>
+struct GemmTile {
+    TileSide side;
+    TileLoads t;
+    uint4 r[RAW ? 4 : 1][2];
+};
+
+template <int BG, bool RAW, bool GENERIC>
+__global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga, int batch) {
+    SE12_DECLARE_LUT(lut);
+    extern __shared__ __attribute__((aligned(16))) char gsm[];
+    int mi = 0;
+#pragma unroll
+    for (int i = 1; i < kMaxGroup; ++i) mi += (i < ga.count && (int)blockIdx.x >= ga.tr_start[i]) ? 1 : 0;
+    const GemvArgs& a = ga.m[mi];
+    const int threads = blockDim.x;
+    const int W = threads >> 6;
+    const int tid = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63u;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int tr = ((int)blockIdx.x - ga.tr_start[mi]) * W + w;
+    const bool active = tr < a.TR;
+    const int trl = active ? tr : a.TR - 1;  // row the loads of an idle wave use
+    const int S = a.S;
+    const int s = blockIdx.y;
+    const int kb = (int)(((uint32_t)s * (uint32_t)a.TC) / (uint32_t)S);
+    const int ke = (int)(((uint32_t)(s + 1) * (uint32_t)a.TC) / (uint32_t)S);
+    const int n = ke - kb;
+    const int64_t row_tiles = (int64_t)trl * a.TC;
+    char* xbuf = gsm;
+    char* wbuf = gsm + 2 * x_slab_bytes<BG>() + w * kWaveTileBytes;
+
+    floatx4_t acc[BG];
+#pragma unroll
+    for (int g = 0; g < BG; ++g) acc[g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    auto load_tile_i = [&](GemmTile<RAW>& t, int i) {
+        const int kt = kb + (i < n ? i : n - 1);
+        if constexpr (RAW) {
+            load_raw_rows<GENERIC>(t.r, a, trl, kt, lane);
+        } else {
+            const int kt2 = kb + (i + (int)(lane & 1u) < n ? i + (int)(lane & 1u) : n - 1);
+            load_side(t.side, a.esc, a.info, row_tiles + kt2);
+            load_tile(t.t, a.sm, a.ec, row_tiles + kt, lane);
+        }
+    };
+    auto use_tile = [&](const GemmTile<RAW>& t, int i) {
+        const int kt = kb + i;
+        const int c0 = 16 * (int)(lane & 15u);
+        const int lim = GENERIC ? (int)(a.K - (int64_t)kt * kTileCols) : kTileCols;
+        if constexpr (RAW) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t wv[8] = {t.r[j][0].x, t.r[j][0].y, t.r[j][0].z, t.r[j][0].w,
+                                  t.r[j][1].x, t.r[j][1].y, t.r[j][1].z, t.r[j][1].w};
+                if constexpr (GENERIC) zero_past_k(wv, c0, lim);
+                stage_chunk(wbuf, j, lane, wv);
+            }
+        } else {
+            const uint32_t info = side_info(t.side, 0);
+            if (info_is_fallback(info)) {
+                const int16_t* raw = a.fb_raw + (int64_t)info_rank(info) * kTile;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t wv[8];
+                    load_raw_chunk(raw, j, lane, wv);
+                    if constexpr (GENERIC) zero_past_k(wv, c0, lim);
+                    stage_chunk(wbuf, j, lane, wv);
+                }
+            } else {
+                uint32_t pat[4][8];
+                lookup_tile(lut, t.t, pat);
+                if (info & 0xFu) resolve_tile_escapes(pat, t.t, info, side_esc(t.side, 0));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t wv[8];
+                    merge_chunk(pat[j], t.t.sm[j], wv);
+                    if constexpr (GENERIC) zero_past_k(wv, c0, lim);
+                    stage_chunk(wbuf, j, lane, wv);
+                }
+            }
+        }
+        wave_lds_fence();
+        mfma_tile<BG>(wbuf, xbuf + (i & 1) * x_slab_bytes<BG>(), lane, acc);
+        wave_lds_fence();  // the next tile's stores follow these reads
+    };
+
+    uint4 lutv;
+    if constexpr (!RAW) lutv = reinterpret_cast<const uint4*>(a.lut)[lane];
+    __builtin_amdgcn_sched_barrier(0);
+    // rings of three: tile i's streams are requested two steps before its
+    // decode, x slab i's pieces two steps before they are stored to LDS
+    // Tile streams and x pieces are requested D - 1 steps ahead of their
+    // use (D = 3; the GENERIC variants, whose element-wise loads are packed
+    // as they arrive, load and use in turn): under a full-bandwidth stream
+    // even the L2 hits of x take about a step to return. Steps run in groups
+    // of D so that every step's loads are issued on every path (steps past
+    // the last tile reload it and skip the decode): a load skipped on some
+    // path would make the compiler wait for all loads in flight. Slab i + 1
+    // is stored to LDS at the end of step i.
+    constexpr int D = GENERIC ? 1 : 3;
+    auto slab = [&](int i) { return kb + (i < n ? i : n - 1); };
+    if constexpr (D == 3) {
+        GemmTile<RAW> t0, t1, t2;
+        load_tile_i(t0, 0);
+        XPieces x0 = load_x_slab<GENERIC>(a, batch, slab(0), tid, threads);
+        load_tile_i(t1, 1);
+        XPieces x1 = load_x_slab<GENERIC>(a, batch, slab(1), tid, threads);
+        XPieces x2;
+        if constexpr (!RAW) store_block_lut(lut, lutv, lane);
+        store_x_slab(xbuf, x0, batch, tid, threads);
+        lds_barrier();
+        auto step = [&](const GemmTile<RAW>& cur, GemmTile<RAW>& ahead, const XPieces& x_next, XPieces& x_ahead,
+                        int i) {
+            x_ahead = load_x_slab<GENERIC>(a, batch, slab(i + 2), tid, threads);
+            load_tile_i(ahead, i + 2);
+            if (i < n) use_tile(cur, i);  // an idle wave decodes row trl; its sums are dropped
+            store_x_slab(xbuf + ((i + 1) & 1) * x_slab_bytes<BG>(), x_next, batch, tid, threads);
+            lds_barrier();
+        };
+        for (int i = 0; i < n; i += 3) {
+            step(t0, t2, x1, x2, i);
+            step(t1, t0, x2, x0, i + 1);
+            step(t2, t1, x0, x1, i + 2);
+        }
+    } else {
+        GemmTile<RAW> t0;
+        XPieces xr = load_x_slab<GENERIC>(a, batch, slab(0), tid, threads);
+        if constexpr (!RAW) store_block_lut(lut, lutv, lane);
+        store_x_slab(xbuf, xr, batch, tid, threads);
+        lds_barrier();
+        for (int i = 0; i < n; ++i) {
+            xr = load_x_slab<GENERIC>(a, batch, slab(i + 1), tid, threads);
+            load_tile_i(t0, i);
+            use_tile(t0, i);
+            store_x_slab(xbuf + ((i + 1) & 1) * x_slab_bytes<BG>(), xr, batch, tid, threads);
+            lds_barrier();
+        }
+    }
+    if (!active) return;
+
+    // accumulator layout: lane l holds D[4 * (l / 16) + e][l % 16] of each
+    // batch group: tile row 4 * (l / 16) + e, batch row 16 * g + l % 16
+    const int64_t n0 = (int64_t)tr * kTileRows + 4 * (int)(lane >> 4);
+    if (S == 1) {
+#pragma unroll
+        for (int g = 0; g < BG; ++g) {
+            const int b = 16 * g + (int)(lane & 15u);
+            if (b < batch)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (n0 + e < a.N) a.y[(int64_t)b * a.N + n0 + e] = acc[g][e];
+        }
+        return;
+    }
+    // split-K: device-scope partial stores, then the wave's arrival on the
+    // tile row's counter; the last of the S waves adds the partials in order
+#pragma unroll
+    for (int g = 0; g < BG; ++g) {
+        const int b = 16 * g + (int)(lane & 15u);
+        if (b < batch)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                __hip_atomic_store(&a.partial[((int64_t)s * batch + b) * a.Np + n0 + e], acc[g][e], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(&a.counters[tr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old != S - 1) return;
+#pragma unroll
+    for (int g = 0; g < BG; ++g) {
+        const int b = 16 * g + (int)(lane & 15u);
+        if (b < batch)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float sum = 0.0f;
+                for (int ss = 0; ss < S; ++ss)
+                    sum += __hip_atomic_load(&a.partial[((int64_t)ss * batch + b) * a.Np + n0 + e], __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+                if (n0 + e < a.N) a.y[(int64_t)b * a.N + n0 + e] = sum;
+            }
+    }
+    if (lane == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+namespace {
+
+template <int BG, bool RAW>
+hipError_t gemm_b(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
+    const dim3 grid(a.tr_start[a.count], a.m[0].S), block(p.waves * 64);
+    if (p.generic)
+        hipLaunchKernelGGL((gemm_kernel<BG, RAW, true>), grid, block, p.lds, stream, a, batch);
+    else
+        hipLaunchKernelGGL((gemm_kernel<BG, RAW, false>), grid, block, p.lds, stream, a, batch);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t gemm_lds_bytes(int waves, int batch) {
+    const int bg = batch > 16 ? 2 : 1;
+    return (size_t)2 * 16 * bg * kRowBytes + (size_t)waves * kWaveTileBytes;
+}
+
+hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
+    if (batch < 1 || batch > 32 || p.waves * 64 * kGemmXPieces < batch * 32) return hipErrorInvalidValue;
+    if (batch > 16) return p.raw ? gemm_b<2, true>(a, batch, p, stream) : gemm_b<2, false>(a, batch, p, stream);
+    return p.raw ? gemm_b<1, true>(a, batch, p, stream) : gemm_b<1, false>(a, batch, p, stream);
+}
+
+}  // namespace se12

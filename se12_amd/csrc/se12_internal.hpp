@@ -116,6 +116,21 @@ constexpr int gemv_waves_per_simd(int batch, bool raw, int g, bool pf, bool gene
 inline size_t gemv_lds_bytes(int waves, int batch) { return (size_t)waves * batch * 16 * sizeof(float); }
 
 hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream);
+
+// Batched path (se12_gemm.hip): BF16 x with kGemmMinBatch..32 rows runs one
+// MFMA launch over all rows (one pass over the weights) instead of one
+// dot2 launch per 4 rows. A block is 1..8 waves, one tile row each, and
+// loads each x slab (batch x 256 BF16) with at most kGemmXPieces 16-byte
+// pieces per thread, so it needs at least batch / 8 waves; at most
+// kGemmMaxSplits K splits. The grid's x dimension counts row blocks
+// (ceil(tile rows / waves) per matrix), and tr_start is in those units.
+constexpr int kGemmMinBatch = 5;
+constexpr int kGemmMaxThreads = 512;
+constexpr int kGemmMaxSplits = 16;
+constexpr int kGemmXPieces = 4;
+constexpr int gemm_min_waves(int batch) { return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces); }
+size_t gemm_lds_bytes(int waves, int batch);
+hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream);
 // Bind-time sidecar: one word per tile (fallback rank, or the chunks holding
 // escape codes) and the fallback tile count.

@@ -6,10 +6,14 @@ threads_per_block + blocks) and lws/domain/launch/search_space.py:14-75
 for this kernel's grid: a block is 1..16 wave64s working on one 16-row tile
 row, and `blocks` = tile_rows x k_splits, where the K tiles of a tile row are
 cut into `k_splits` contiguous ranges (the last block of a tile row to finish
-adds the splits in order). The launch shape fixes the order of every sum, so
-the fused kernel and its raw twin agree bit for bit under one configuration.
-The default configuration itself is computed by the library
-(se12_default_launch) from the device's CU count.
+adds the splits in order). BF16 batches of MFMA_MIN_BATCH or more rows run
+the batched MFMA kernel instead, whose block is 1..8 wave64s each owning one
+tile row: there `blocks` = ceil(tile_rows / waves) x k_splits, and a block
+needs at least batch / 8 waves (each thread loads at most 4 x pieces per K
+tile). The launch shape fixes the order of every sum, so the fused kernel and
+its raw twin agree bit for bit under one configuration. The default
+configuration itself is computed by the library (se12_default_launch) from
+the device's CU count.
 """
 
 from __future__ import annotations
@@ -20,6 +24,11 @@ WAVE_SIZE = 64
 WAVES_PER_BLOCK_CANDIDATES = (1, 2, 3, 4, 6, 8, 9, 12, 16)
 K_SPLIT_CANDIDATES = (1, 2, 3, 4, 6, 8, 9, 12, 16, 18, 24, 32, 36, 48, 64)
 MAX_K_SPLITS = 64
+# BF16 activations with this many rows or more take the batched MFMA kernel:
+# one launch over all rows, at most 8 waves per block and 16 K splits
+MFMA_MIN_BATCH = 5
+MFMA_MAX_K_SPLITS = 16
+MFMA_MAX_WAVES = 8
 
 
 @dataclasses.dataclass(frozen=True)
@@ -52,9 +61,25 @@ def k_tiles(k: int) -> int:
     return -(-k // 256)
 
 
-def configuration(waves: int, k_splits: int, output_rows: int) -> LaunchConfiguration:
+def uses_mfma(batch: int, float32_activations: bool = False) -> bool:
+    return not float32_activations and batch >= MFMA_MIN_BATCH
+
+
+def mfma_min_waves(batch: int) -> int:
+    return -(-batch // 8)
+
+
+def grid_rows(output_rows: int, waves: int, batch: int = 1, float32_activations: bool = False) -> int:
+    """Blocks per K split: one per tile row, or per `waves` tile rows (MFMA)."""
+    tr = tile_rows(output_rows)
+    return -(-tr // waves) if uses_mfma(batch, float32_activations) else tr
+
+
+def configuration(waves: int, k_splits: int, output_rows: int, batch: int = 1,
+                  float32_activations: bool = False) -> LaunchConfiguration:
     return LaunchConfiguration(
-        threads_per_block=ThreadsPerBlock(waves * WAVE_SIZE), blocks=BlockCount(tile_rows(output_rows) * k_splits)
+        threads_per_block=ThreadsPerBlock(waves * WAVE_SIZE),
+        blocks=BlockCount(grid_rows(output_rows, waves, batch, float32_activations) * k_splits),
     )
 
 
@@ -65,9 +90,16 @@ def runs_generic(output_rows: int, k: int, float32_activations: bool = False) ->
     return float32_activations or k % 256 != 0 or output_rows % 16 != 0
 
 
+def max_k_splits(batch: int, float32_activations: bool = False) -> int:
+    return MFMA_MAX_K_SPLITS if uses_mfma(batch, float32_activations) else MAX_K_SPLITS
+
+
 def max_waves_per_block(batch: int, float32_activations: bool = False, generic: bool = False) -> int:
     """16 wave64s (1024 threads), or 8 where a launch needs more registers per
-    lane: 4 batch rows per launch, or 2-4 rows in the edge-handling variants."""
+    lane: 4 batch rows per launch, 2-4 rows in the edge-handling variants, or
+    the batched MFMA kernel."""
+    if uses_mfma(batch, float32_activations):
+        return MFMA_MAX_WAVES
     b = min(batch, 4)
     if generic or float32_activations:
         return 8 if b >= 2 else 16
@@ -77,33 +109,36 @@ def max_waves_per_block(batch: int, float32_activations: bool = False, generic: 
 def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int = 1, k: int | None = None,
                      float32_activations: bool = False) -> tuple[int, int]:
     """(waves per block, K splits) of a configuration for a matrix with `output_rows` rows."""
-    tr = tile_rows(output_rows)
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
     generic = runs_generic(output_rows, k, float32_activations) if k is not None else float32_activations
     hi = WAVE_SIZE * max_waves_per_block(batch, float32_activations, generic)
-    if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= hi:
-        raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {hi}]")
-    if blocks <= 0 or blocks % tr:
-        raise ValueError(f"blocks {blocks} must be a positive multiple of the {tr} tile rows")
-    return tpb // WAVE_SIZE, blocks // tr
+    lo = WAVE_SIZE * (mfma_min_waves(batch) if uses_mfma(batch, float32_activations) else 1)
+    if tpb % WAVE_SIZE or not lo <= tpb <= hi:
+        raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [{lo}, {hi}]")
+    rows = grid_rows(output_rows, tpb // WAVE_SIZE, batch, float32_activations)
+    if blocks <= 0 or blocks % rows:
+        raise ValueError(f"blocks {blocks} must be a positive multiple of {rows}")
+    return tpb // WAVE_SIZE, blocks // rows
 
 
 def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_activations: bool = False) -> tuple[LaunchConfiguration, ...]:
     """Every (waves, splits) worth timing: waves per block up to the batch's
     limit (valid for the fused kernel and its raw twin alike), K splits up to
-    the K tiles, never more waves than tiles per split (search_space.py:17-19
-    enumerates threads per block the same way)."""
+    the K tiles; for the dot2 kernel never more waves than tiles per split
+    (search_space.py:17-19 enumerates threads per block the same way)."""
     tc = k_tiles(k)
+    mfma = uses_mfma(batch, float32_activations)
     mw = max_waves_per_block(batch, float32_activations, runs_generic(output_rows, k, float32_activations))
-    splits = [s for s in K_SPLIT_CANDIDATES if s <= min(tc, MAX_K_SPLITS)]
+    lo = mfma_min_waves(batch) if mfma else 1
+    splits = [s for s in K_SPLIT_CANDIDATES if s <= min(tc, max_k_splits(batch, float32_activations))]
     out = []
     for waves in WAVES_PER_BLOCK_CANDIDATES:
-        if waves > mw:
+        if not lo <= waves <= mw:
             continue
         for s in splits:
-            if waves <= -(-tc // s):
-                out.append(configuration(waves, s, output_rows))
+            if mfma or waves <= -(-tc // s):
+                out.append(configuration(waves, s, output_rows, batch, float32_activations))
     return tuple(out)
 
 

@@ -37,7 +37,7 @@ def _check(kernel, enc, xbits, device, launch=None, f32=False):
 
 
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
-@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("batch", [1, 3, 8])
 def test_gemv_golden_vectors(gpu, name, batch):
     from se12_amd.hip import Se12MatVecKernel
 
@@ -102,7 +102,21 @@ def test_gemv_ragged_and_escape_heavy(gpu, rows, cols):
     _check(k, enc, _x(2, cols, seed=rows), gpu)
 
 
-def test_gemv_fallback_tiles(gpu):
+@pytest.mark.parametrize("batch", [5, 17])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (17, 257), (33, 300), (2048, 2304), (64, 9216)])
+def test_batched_ragged_and_escape_heavy(gpu, rows, cols, batch):
+    """The batched MFMA kernel (BF16 x, 5..32 rows) on ragged and escape-heavy
+    matrices, padding rows of the 16-row batch groups included."""
+    from se12_amd.hip import Se12MatVecKernel
+
+    bits = heavy_tailed_bf16(rows, cols, seed=rows * 5 + cols)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    _check(k, enc, _x(batch, cols, seed=rows + batch), gpu)
+
+
+@pytest.mark.parametrize("batch", [3, 9])
+def test_gemv_fallback_tiles(gpu, batch):
     from se12_amd.hip import Se12MatVecKernel
 
     # concentrated exponents with random escapes; a third of the tiles overflow
@@ -119,10 +133,11 @@ def test_gemv_fallback_tiles(gpu):
     enc = o.encode(bits.reshape(-1), 64, 1024)
     assert o.fallback_tile_count(enc) == 6
     k = Se12MatVecKernel(to_device(enc, gpu))
-    _check(k, enc, _x(3, 1024, seed=5), gpu)
+    _check(k, enc, _x(batch, 1024, seed=5), gpu)
 
 
-def test_gemv_padding_of_an_infinite_codebook0_is_masked(gpu):
+@pytest.mark.parametrize("batch", [1, 6])
+def test_gemv_padding_of_an_infinite_codebook0_is_masked(gpu, batch):
     """codebook[0] = 255: padding columns decode to +inf; rows whose real
     weights are finite must still give finite, correct outputs."""
     from se12_amd.hip import Se12MatVecKernel
@@ -134,7 +149,7 @@ def test_gemv_padding_of_an_infinite_codebook0_is_masked(gpu):
     enc = o.encode(bits.reshape(-1), rows, cols)
     assert enc["codebook"][0] == 255
     k = Se12MatVecKernel(to_device(enc, gpu))
-    xb = _x(1, cols, seed=int(rng.integers(100)))
+    xb = _x(batch, cols, seed=int(rng.integers(100)))
     y = k.multiply(bf16_tensor(xb, gpu)).cpu().numpy()
     ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
     assert np.all(np.isfinite(y[:, 16:]))
@@ -148,16 +163,17 @@ def _configs(rows, cols, batch=1):
     return candidate_configurations(rows, cols, batch=batch)
 
 
-def test_every_launch_configuration_is_correct_and_deterministic(gpu):
+@pytest.mark.parametrize("rows,cols,batch", [(272, 2800, 2), (272, 2800, 6), (272, 2800, 20), (448, 3584, 32)])
+def test_every_launch_configuration_is_correct_and_deterministic(gpu, rows, cols, batch):
     from se12_amd.hip import Se12MatVecKernel
 
-    bits = heavy_tailed_bf16(272, 2800, seed=31)
-    enc = o.encode(bits.reshape(-1), 272, 2800)
+    bits = heavy_tailed_bf16(rows, cols, seed=31)
+    enc = o.encode(bits.reshape(-1), rows, cols)
     k = Se12MatVecKernel(to_device(enc, gpu))
-    xb = _x(2, 2800, seed=32)
+    xb = _x(batch, cols, seed=32)
     x = bf16_tensor(xb, gpu)
     ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
-    for cfg in _configs(272, 2800, batch=2):
+    for cfg in _configs(rows, cols, batch=batch):
         y1 = k.multiply(x, launch=cfg).clone()
         y2 = k.multiply(x, launch=cfg)
         torch.cuda.synchronize()
@@ -194,7 +210,7 @@ def test_raw_twin_is_bit_identical_under_one_launch(gpu, shape):
         enc = o.encode(bits.reshape(-1), rows, cols)
     fused = Se12MatVecKernel(to_device(enc, gpu))
     raw = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
-    for batch in (1, 4, 6):
+    for batch in (1, 4, 6, 17, 32):
         x = bf16_tensor(_x(batch, cols, seed=batch), gpu)
         all_cfgs = list(_configs(rows, cols, batch=batch))
         cfgs = [None] + all_cfgs[:: max(1, len(all_cfgs) // 6)] + all_cfgs[-2:]
@@ -202,13 +218,14 @@ def test_raw_twin_is_bit_identical_under_one_launch(gpu, shape):
             assert torch.equal(fused.multiply(x, launch=cfg), raw.multiply(x, launch=cfg)), (batch, cfg)
 
 
-def test_graph_replay_matches_eager(gpu):
+@pytest.mark.parametrize("batch", [1, 8])
+def test_graph_replay_matches_eager(gpu, batch):
     from se12_amd.hip import Se12MatVecKernel
 
     bits, enc = normal_case(2304, 9216, seed=0)
     k = Se12MatVecKernel(to_device(enc, gpu))
-    x = bf16_tensor(_x(1, 9216, seed=1), gpu)
-    out = torch.empty((1, 2304), dtype=torch.float32, device=gpu)
+    x = bf16_tensor(_x(batch, 9216, seed=1), gpu)
+    out = torch.empty((batch, 2304), dtype=torch.float32, device=gpu)
     eager = k.multiply(x).clone()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -251,16 +268,15 @@ def test_grouped_launch_equals_separate_launches(gpu):
     launches under the same waves per block and K splits, and within the
     tolerance of the oracle under the default launch."""
     from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped
-    from se12_amd.launch import BlockCount, LaunchConfiguration, ThreadsPerBlock
+    from se12_amd.launch import BlockCount, LaunchConfiguration, ThreadsPerBlock, configuration, grid_rows
 
     cols = 2304
     shapes = [(272, cols), (128, cols), (48, cols)]
     bits = [heavy_tailed_bf16(r, c, seed=40 + i) for i, (r, c) in enumerate(shapes)]
     encs = [o.encode(b.reshape(-1), r, c) for b, (r, c) in zip(bits, shapes)]
-    kerns = [Se12MatVecKernel(to_device(e, gpu), max_batch=8) for e in encs]
-    raws = [RawBf16MatVecKernel(bf16_tensor(b, gpu), max_batch=8) for b in bits]
-    tr_total = sum(-(-r // 16) for r, _ in shapes)
-    for batch in (1, 3, 6):
+    kerns = [Se12MatVecKernel(to_device(e, gpu), max_batch=20) for e in encs]
+    raws = [RawBf16MatVecKernel(bf16_tensor(b, gpu), max_batch=20) for b in bits]
+    for batch in (1, 3, 6, 20):
         xb = _x(batch, cols, seed=50 + batch)
         x = bf16_tensor(xb, gpu)
         ys = multiply_grouped(kerns, x)
@@ -270,11 +286,12 @@ def test_grouped_launch_equals_separate_launches(gpu):
         for waves, splits in ((3, 1), (9, 1), (4, 3)):
             if batch >= 4 and waves > 8:
                 continue
-            grouped = LaunchConfiguration(ThreadsPerBlock(64 * waves), BlockCount(tr_total * splits))
+            rows_total = sum(grid_rows(r, waves, batch) for r, _ in shapes)
+            grouped = LaunchConfiguration(ThreadsPerBlock(64 * waves), BlockCount(rows_total * splits))
             ys = multiply_grouped(kerns, x, launch=grouped)
             ysr = multiply_grouped(raws, x, launch=grouped)
             for k, r, y, yr, (rows, _) in zip(kerns, raws, ys, ysr, shapes):
-                single = LaunchConfiguration(ThreadsPerBlock(64 * waves), BlockCount(-(-rows // 16) * splits))
+                single = configuration(waves, splits, rows, batch)
                 assert torch.equal(y, k.multiply(x, launch=single)), (batch, waves, splits)
                 assert torch.equal(yr, y), (batch, waves, splits)
 

@@ -23,9 +23,10 @@ the 2304x9216 down_proj shape, timed live as 26 back-to-back launches over the
 26 layers' (cold) matrices; and the oracle's numpy decode + matmul timed on
 the host as the CPU baseline. Two more objects: the batch sweep B = 1..32 at
 the Gemma-2-9B gate_proj shape 14336x3584 against hipBLASLt BF16 (the
-crossover from the dot2 kernel to the MFMA kernel), and batch-1 stress shapes
+crossover from the dot2 kernel to the MFMA kernel), batch-1 stress shapes
 with heavy-tailed weights (tied LM head 256000x2304, Gemma-2-27B down_proj
-4608x36864).
+4608x36864), and a random-init Gemma-2-2B greedy decode (prompt 512, 128
+tokens) whose decode tokens/s is the `decode_tok_s` field.
 """
 
 from __future__ import annotations
@@ -72,6 +73,7 @@ def parse_args(argv=None):
     p.add_argument("--no-per-shape", action="store_true")
     p.add_argument("--no-batch-sweep", action="store_true")
     p.add_argument("--no-stress", action="store_true")
+    p.add_argument("--no-e2e", action="store_true", help="skip the Gemma-2-2B greedy decode")
     p.add_argument("--only-fused", action="store_true", help="skip the BF16 and raw-twin comparisons (profiling)")
     p.add_argument("--profile-down", action="store_true",
                    help="only the dominant kernel (26 down_proj launches per step) and a 256 MiB device copy of known "
@@ -147,6 +149,14 @@ def capture(fn):
         fn()
     torch.cuda.synchronize()
     return g
+
+
+def evict_caches(buf: torch.Tensor) -> None:
+    """Reads `buf` (1 GiB, over 4x L2 + Infinity Cache) so that the next
+    launch finds its weights in HBM only. A read, not a fill: a fill leaves
+    the caches full of dirty lines whose write-back would compete with the
+    timed launch's reads."""
+    torch.sum(buf)
 
 
 def time_graph(g, steps: int, warmup: int, flush=None) -> float:
@@ -244,7 +254,7 @@ def stress(device) -> dict:
     paths), against hipBLASLt BF16; the cache is flushed before each launch."""
     from se12_amd.hip import Se12MatVecKernel, encode_on_device
 
-    flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=device)
+    flush_buf = torch.zeros(1 << 28, dtype=torch.float32, device=device)
     out = {}
     for name, n, k, seed in (("lm_head", 256000, 2304, 11), ("down_27b", 4608, 36864, 12)):
         w = heavy_tailed(n, k, seed, device)
@@ -255,9 +265,9 @@ def stress(device) -> dict:
         x = torch.randn((1, k), generator=gen, device=device).to(torch.bfloat16)
         y = torch.empty((1, n), dtype=torch.float32, device=device)
         g = capture(lambda: kern.multiply(x, out=y))
-        us = time_graph(g, 10, 3, flush=lambda: flush_buf.fill_(1.0)) * 1e3
+        us = time_graph(g, 10, 3, flush=lambda: evict_caches(flush_buf)) * 1e3
         gb = capture(lambda: torch.nn.functional.linear(x, w))
-        us_b = time_graph(gb, 10, 3, flush=lambda: flush_buf.fill_(1.0)) * 1e3
+        us_b = time_graph(gb, 10, 3, flush=lambda: evict_caches(flush_buf)) * 1e3
         lc = kern.default_launch(1)
         out[name] = {"shape": [n, k], "us": round(us, 3), "se12_bytes": enc.byte_size(),
                      "bytes_per_weight": round(enc.byte_size() / (n * k), 4),
@@ -270,6 +280,61 @@ def stress(device) -> dict:
         del g, gb, kern, enc, w
         torch.cuda.empty_cache()
     del flush_buf
+    return out
+
+
+def e2e_decode(device, prompt_len: int = 512, new_tokens: int = 128) -> dict:
+    """Random-init Gemma-2-2B (26 layers, hidden 2304, 8 query / 4 KV heads of
+    256, intermediate 9216, vocab 256000; BF16 N(0, 0.02)) greedy decode at
+    batch 1: a random prompt of `prompt_len` tokens, `new_tokens` generated.
+    Every linear goes through the SE12 kernels (prefill decodes each layer and
+    runs F.linear, exact); the same model through the order-matched raw-BF16
+    twin and through hipBLASLt BF16 gives the comparison. Each decode step is
+    one HIP graph replay; tokens/s counts the decode steps after prefill."""
+    from se12_amd.gemma2 import GEMMA2_2B, PROJECTIONS, Gemma2Decoder, Gemma2Weights
+    from se12_amd.hip import encode_on_device
+
+    shape = GEMMA2_2B
+    w = Gemma2Weights.random(shape, device)
+    encoded = {(li, n): encode_on_device(lw[n]) for li, lw in enumerate(w.layers) for n in PROJECTIONS}
+    encoded["embed"] = encode_on_device(w.embed)
+    se12_bytes = sum(e.byte_size() for e in encoded.values())
+    bf16_bytes = 2 * sum(lw[n].numel() for lw in w.layers for n in PROJECTIONS) + 2 * w.embed.numel()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4242)
+    prompt = torch.randint(0, shape.vocab, (1, prompt_len), generator=gen, device=device)
+    out = {"workload": f"gemma-2-2b random init, batch 1, prompt {prompt_len}, {new_tokens} greedy tokens",
+           "se12_weight_bytes": se12_bytes, "bf16_weight_bytes": bf16_bytes}
+    tokens = {}
+    for name, backend in (("se12", "se12"), ("raw_bf16_twin", "raw"), ("bf16_hipblaslt", "bf16")):
+        dec = Gemma2Decoder(w, backend, batch=1, max_len=prompt_len + new_tokens, encoded=encoded)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        dec.prefill(prompt)
+        torch.cuda.synchronize()
+        prefill_ms = (time.perf_counter() - t0) * 1e3
+        dec.capture()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        dec.decode(new_tokens - 1)
+        end.record()
+        end.synchronize()
+        decode_ms = start.elapsed_time(end)
+        tokens[name] = dec.tokens[0, :new_tokens].cpu()
+        out[name] = {"prefill_ms": round(prefill_ms, 3), "decode_ms": round(decode_ms, 3),
+                     "ms_per_token": round(decode_ms / (new_tokens - 1), 4),
+                     "decode_tok_s": round((new_tokens - 1) / (decode_ms * 1e-3), 2),
+                     "e2e_tok_s": round(new_tokens / ((prefill_ms + decode_ms) * 1e-3), 2)}
+        log(f"[bench] e2e {name}: {out[name]}")
+        del dec
+        torch.cuda.empty_cache()
+    same = tokens["se12"] == tokens["bf16_hipblaslt"]
+    out["tokens_identical_se12_vs_raw_twin"] = bool(torch.equal(tokens["se12"], tokens["raw_bf16_twin"]))
+    out["tokens_matching_se12_vs_bf16"] = int(same.sum())
+    out["first_divergence_se12_vs_bf16"] = None if bool(same.all()) else int((~same).nonzero()[0, 0])
+    out["decode_speedup_vs_bf16"] = round(out["se12"]["decode_tok_s"] / out["bf16_hipblaslt"]["decode_tok_s"], 4)
+    del w, encoded
+    torch.cuda.empty_cache()
     return out
 
 
@@ -460,10 +525,10 @@ def main(argv=None) -> int:
         del g_raw, raw
 
     if not args.no_per_shape:
-        flush_buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB > 2 x (L2 + MALL)
+        flush_buf = torch.zeros(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB > 4 x (L2 + MALL)
 
         def flush():
-            flush_buf.fill_(1.0)
+            evict_caches(flush_buf)
 
         per_shape = {}
         for pi, (name, n, k, _) in enumerate(PROJECTIONS):
@@ -490,6 +555,9 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
     if not args.no_stress:
         result["stress"] = stress(dev)
+    if not args.no_e2e:
+        result["e2e"] = e2e_decode(dev)
+        result["decode_tok_s"] = result["e2e"]["se12"]["decode_tok_s"]
 
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")

@@ -117,18 +117,15 @@ __device__ __forceinline__ uint32_t esc_byte(uint4 e, uint32_t r) {
     return (d >> ((r & 3u) * 8u)) & 0xFFu;
 }
 
-// write exponent e into the pattern of weight p (0..15) of the chunk; every
-// element is rewritten through a mask so the array stays in registers
+// write exponent e into the pattern of weight p (0..15) of the chunk. The
+// pair table gives the escape code no exponent, so the field is 0 and an OR
+// suffices; the word is chosen by a one-hot mask (two instructions per word)
+// so the array stays in registers.
 __device__ __forceinline__ void patch_exponent(uint32_t pat[8], uint32_t p, uint32_t e) {
-    const uint32_t q = p >> 1;
-    const bool hi = (p & 1u) != 0u;
-    const uint32_t m = hi ? 0x7F800000u : 0x00007F80u;
-    const uint32_t v = hi ? (e << 23) : (e << 7);
+    const uint32_t v = e << ((p & 1u) ? 23u : 7u);
+    const uint32_t onehot = 1u << (p >> 1);
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) {
-        const uint32_t sel = 0u - (uint32_t)(i == q);
-        pat[i] = (pat[i] & ~(m & sel)) | (v & sel);
-    }
+    for (uint32_t i = 0; i < 8; ++i) pat[i] |= v & (uint32_t)((int32_t)(onehot << (31u - i)) >> 31);
 }
 
 __device__ __forceinline__ void resolve_escapes(uint32_t pat[8], uint2 ec, uint4 esc, uint32_t& run) {
@@ -146,16 +143,18 @@ __device__ __forceinline__ void resolve_escapes(uint32_t pat[8], uint2 ec, uint4
         below = incl - cnt;
         total = __builtin_amdgcn_readlane(incl, kWave - 1);
     }
+    // the lane's escapes in weight order, both halves in one loop (one
+    // iteration when no lane holds two)
     uint32_t r = run + below;
-    while (t0) {
-        const uint32_t p = (uint32_t)__builtin_ctz(t0) >> 2;
-        t0 &= t0 - 1u;
-        patch_exponent(pat, p, esc_byte(esc, r < 15u ? r : 15u));
-        ++r;
-    }
-    while (t1) {
-        const uint32_t p = 8u + ((uint32_t)__builtin_ctz(t1) >> 2);
-        t1 &= t1 - 1u;
+    while (t0 | t1) {
+        uint32_t p;
+        if (t0) {
+            p = (uint32_t)__builtin_ctz(t0) >> 2;
+            t0 &= t0 - 1u;
+        } else {
+            p = 8u + ((uint32_t)__builtin_ctz(t1) >> 2);
+            t1 &= t1 - 1u;
+        }
         patch_exponent(pat, p, esc_byte(esc, r < 15u ? r : 15u));
         ++r;
     }
@@ -247,8 +246,9 @@ __device__ __forceinline__ void lookup_tile(const uint32_t* lut, const TileLoads
 __device__ __forceinline__ void resolve_tile_escapes(uint32_t pat[4][8], const TileLoads& t, uint32_t info, uint4 esc) {
     uint32_t run = 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
         if (info & (1u << j)) resolve_escapes(pat[j], t.ec[j], esc, run);
+    }
 }
 
 // Raw BF16 pairs of chunk j of a fallback tile (tile-local order, like sm).

@@ -155,6 +155,29 @@ class Se12MatVecKernel(_GemvBase):
         self.device = self.tensor.sm.device
         self.handle = bind_se12(self.tensor, max_batch)
 
+    def decode_into(self, out: torch.Tensor) -> torch.Tensor:
+        """Decodes the whole matrix into `out` (row-major BF16 [rows, cols],
+        e.g. a view of a scratch buffer shared by many layers)."""
+        if out.dtype != torch.bfloat16 or tuple(out.shape) != (self.rows, self.cols) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous bfloat16 [{self.rows}, {self.cols}] tensor")
+        if out.device != self.device:
+            raise ValueError(f"out on {out.device}, weights on {self.device}")
+        nat.check(nat.lib().se12_decode(self.handle.raw, nat.ptr(out), nat.stream_ptr()))
+        return out
+
+    def decode_rows_into(self, rows: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        """Decodes the rows of a device int64 index tensor, in order, into `out`
+        ([len(rows), cols] BF16); only the tiles of those rows are read. An
+        index outside [0, rows) gives a row of zeros (the kernel checks each
+        index before reading)."""
+        idx = rows.reshape(-1)
+        if idx.dtype != torch.int64 or idx.device != self.device or not idx.is_contiguous():
+            raise ValueError("rows must be a contiguous int64 tensor on the weights' device")
+        if out.dtype != torch.bfloat16 or tuple(out.shape) != (idx.numel(), self.cols) or not out.is_contiguous():
+            raise ValueError(f"out must be a contiguous bfloat16 [{idx.numel()}, {self.cols}] tensor")
+        nat.check(nat.lib().se12_decode_rows(self.handle.raw, nat.ptr(idx), idx.numel(), nat.ptr(out), nat.stream_ptr()))
+        return out
+
 
 class RawBf16MatVecKernel(_GemvBase):
     """The same-skeleton raw-BF16 twin bound to a [N, K] BF16 matrix (gemv.py:143-172)."""

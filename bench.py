@@ -308,6 +308,7 @@ def e2e_decode(device, prompt_len: int = 512, new_tokens: int = 128) -> dict:
     tokens = {}
     for name, backend in (("se12", "se12"), ("raw_bf16_twin", "raw"), ("bf16_hipblaslt", "bf16")):
         dec = Gemma2Decoder(w, backend, batch=1, max_len=prompt_len + new_tokens, encoded=encoded)
+        dec.prefill(prompt)          # warm-up (library and GEMM selection), untimed
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         dec.prefill(prompt)

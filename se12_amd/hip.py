@@ -410,10 +410,12 @@ class HipBenchmarkTimer:
         if l2_bytes is None:
             l2_bytes = HipGpuProbe(self.device).properties().l2_bytes
         flush = 2 * (int(l2_bytes) + INFINITY_CACHE_BYTES)
-        self.flush_buffer = torch.empty(flush // 4, dtype=torch.float32, device=f"cuda:{self.device}")
+        self.flush_buffer = torch.zeros(flush // 4, dtype=torch.float32, device=f"cuda:{self.device}")
 
     def flush(self) -> None:
-        self.flush_buffer.fill_(1.0)
+        """Evicts by reading the buffer: a fill would leave the caches full of
+        dirty lines whose write-back competes with the timed operation."""
+        torch.sum(self.flush_buffer)
 
     def time_operation(self, operation: Callable[[], Any], warmup: int = 25, timed: int = 100, flush: bool = True) -> LatencyStats:
         for _ in range(warmup):

@@ -392,12 +392,15 @@ def load_packed(packed: Any, mode: str = "auto", order: str | None = None, devic
                 policy: FusedPolicy | None = None, verdict_dir=None, launch_lookup: LaunchLookup | None = None,
                 max_batch: int = nat.MAX_BATCH, log: Callable[[str], None] | None = print,
                 kernel_factory: Callable[[str, Any, torch.device, int], Any] | None = None,
-                attn_implementation: str | None = None) -> nn.Module:
+                attn_implementation: str | None = None, tuning_dir=None) -> nn.Module:
     """A Hugging Face causal LM whose eligible Linear and Embedding layers are
     SE12-backed (AC-015): `packed` is a packed directory/file or a
     `PackedModel`; `config` defaults to the directory's config.json.
     `order="matched"` launches every fused step with the configuration the
-    reference runtime uses (the library default, or `launch_lookup`)."""
+    reference runtime uses. Launch configurations come from `launch_lookup`,
+    else this GPU's tuning file (`tune-<gpu-slug>.json` in `tuning_dir`,
+    $LWS_TUNING_DIR or reports/: its order-matched entries with
+    order="matched", its fused entries otherwise), else the library default."""
     from transformers import AutoConfig, AutoModelForCausalLM
 
     if mode not in MODES:
@@ -412,6 +415,8 @@ def load_packed(packed: Any, mode: str = "auto", order: str | None = None, devic
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     if policy is None:
         policy = load_policy(current_gpu_slug(dev), verdict_dir) if mode == "auto" else FusedPolicy()
+    if launch_lookup is None and mode != "exact" and kernel_factory is None:
+        launch_lookup = tuned_lookup(dev, "order_matched" if order == "matched" else "fused", tuning_dir)
     make_kernel = kernel_factory or _default_kernel
     if attn_implementation == CONTIGUOUS_EAGER:
         register_attention()
@@ -439,7 +444,7 @@ def load_packed(packed: Any, mode: str = "auto", order: str | None = None, devic
             # tensor after the model is materialised
             bias = torch.empty(mod.out_features, dtype=torch.bfloat16, device="meta") if mod.bias is not None else None
             new = CompressedLinear(kernel_for(src), bias, mode=mode, policy=policy, scratch=scratch,
-                                   launch_lookup=launch_lookup if order == "matched" else None)
+                                   launch_lookup=launch_lookup)
         elif isinstance(mod, nn.Embedding):
             # a scaled embedding keeps its scale in a non-persistent buffer that
             # no checkpoint holds; Gemma models set it to sqrt(hidden_size)
@@ -475,14 +480,26 @@ def load_packed(packed: Any, mode: str = "auto", order: str | None = None, devic
     return model
 
 
+def tuned_lookup(device, kind: str, tuning_dir=None) -> LaunchLookup | None:
+    """The launch lookup of this GPU's tuning file, or None without one."""
+    from .tune import load_tuning
+
+    tf = load_tuning(current_gpu_slug(device), tuning_dir)
+    return tf.lookup(kind) if tf is not None else None
+
+
 def load_reference(model_dir, device=None, order: str | None = "matched",
                    launch_lookup: LaunchLookup | None = None, model: nn.Module | None = None,
-                   attn_implementation: str | None = None) -> nn.Module:
+                   attn_implementation: str | None = None, tuning_dir=None) -> nn.Module:
     """The reference runtime (AC-033): original BF16 weights, every eligible
-    Linear through the raw-BF16 twin for decode steps."""
+    Linear through the raw-BF16 twin for decode steps, launched with the
+    tuning file's order-matched (order="matched") or raw entries when this GPU
+    has one."""
     from transformers import AutoModelForCausalLM
 
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    if launch_lookup is None:
+        launch_lookup = tuned_lookup(dev, "order_matched" if order == "matched" else "raw", tuning_dir)
     if attn_implementation == CONTIGUOUS_EAGER:
         register_attention()
     if model is None:
@@ -493,7 +510,7 @@ def load_reference(model_dir, device=None, order: str | None = "matched",
         if isinstance(mod, nn.Linear) and is_eligible(mod.weight):
             parent, attr = _module_and_attr(model, name)
             setattr(parent, attr, ReferenceLinear(mod.weight.data, mod.bias.data if mod.bias is not None else None,
-                                                  launch_lookup=launch_lookup if order == "matched" else None))
+                                                  launch_lookup=launch_lookup))
     model.eval()
     return model
 

@@ -90,7 +90,8 @@ class DeviceInfo(ctypes.Structure):
     ]
 
 
-# name -> (restype, argtypes): every symbol include/se12_gfx950.h declares
+# name -> (restype, argtypes): every symbol include/se12_gfx950.h and
+# include/se12_step.h declare
 SIGNATURES = {
     "se12_last_error": (ctypes.c_char_p, []),
     "se12_version": (ctypes.c_char_p, []),
@@ -116,7 +117,31 @@ SIGNATURES = {
         c_i32,
         [c_void_p, c_i64, c_i64, c_i64, c_u8p, ctypes.POINTER(StreamsOut), ctypes.POINTER(c_i64), c_void_p],
     ),
+    # decode-step kernels (include/se12_step.h)
+    "se12_step_last_error": (ctypes.c_char_p, []),
+    "se12_step_rmsnorm": (
+        c_i32,
+        [c_void_p, c_i32, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32, ctypes.c_float, ctypes.c_float,
+         c_i32, c_void_p],
+    ),
+    "se12_step_attention_workspace": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "se12_step_attention": (
+        c_i32,
+        [c_void_p, c_void_p, c_void_p, c_i32, c_i64, c_i64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i32, c_i32,
+         c_i32, c_i32, c_i32, ctypes.c_float, ctypes.c_float, c_i32, c_void_p, c_i64, c_void_p],
+    ),
+    "se12_step_gelu_mul": (c_i32, [c_void_p, c_void_p, c_i32, c_i64, c_void_p, c_i32, c_i32, c_void_p]),
+    "se12_step_logits_workspace": (c_i64, [c_i32, c_i32]),
+    "se12_step_logits_argmax": (
+        c_i32,
+        [c_void_p, c_i32, c_i64, c_i32, c_i32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_i64, c_void_p, c_void_p,
+         c_i64, c_void_p],
+    ),
+    "se12_step_advance": (c_i32, [c_void_p, c_void_p, c_void_p]),
 }
+
+STEP_BF16 = 0
+STEP_F32 = 1
 
 _lib: ctypes.CDLL | None = None
 
@@ -142,6 +167,12 @@ def lib() -> ctypes.CDLL:
 def last_error() -> str:
     msg = lib().se12_last_error()
     return msg.decode() if msg else ""
+
+
+def step_check(rc: int) -> None:
+    """Raises the step kernels' last error for a non-zero status."""
+    if rc != 0:
+        raise Se12Error(rc, (lib().se12_step_last_error() or b"").decode())
 
 
 def check(rc: int) -> None:

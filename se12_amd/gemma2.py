@@ -20,6 +20,12 @@ pattern (q/k/v and gate/up issued as one grouped product each):
            gate/up weights).
 Batched products whose right operand is a transposed view are avoided (the
 K cache is kept transposed and contiguous): they have faulted MI355X GPUs.
+
+A decode step runs either through the library's step kernels (include/
+se12_step.h: fused norms, attention, activation, logits; the default, ~8
+launches per layer) or through framework ops (`fused_step=False`, ~80 small
+kernels per layer; kept as the reference the step kernels are tested
+against).
 """
 
 from __future__ import annotations
@@ -177,6 +183,37 @@ class _Backend:
             return F.linear(x, self.w.embed)
         return self.lm_head.multiply(x).to(torch.bfloat16)
 
+    # -- fused decode steps: raw products (FP32 for the library kernels, BF16
+    # for hipBLASLt), consumed by the step kernels ---------------------------
+    def grouped_raw(self, li: int, names: tuple[str, ...], x: torch.Tensor, outs: list[torch.Tensor] | None):
+        """[(tensor, column offset, row stride)] per name."""
+        if self.kind == "bf16":
+            y = F.linear(x, self.layers[li]["qkv" if names[0] == "q" else "gate_up"])
+            offs, res = 0, []
+            for n in names:
+                res.append((y, offs, y.shape[1]))
+                offs += self.w.layers[li][n].shape[0]
+            return res
+        from .hip import multiply_grouped
+
+        ys = multiply_grouped([self.layers[li][n] for n in names], x, outs=outs)
+        return [(y, 0, y.shape[1]) for y in ys]
+
+    def single_raw(self, li: int, name: str, x: torch.Tensor, out: torch.Tensor | None) -> torch.Tensor:
+        if self.kind == "bf16":
+            return F.linear(x, self.w.layers[li][name])
+        return self.layers[li][name].multiply(x, out=out)
+
+    def logits_raw(self, x: torch.Tensor, out: torch.Tensor | None) -> torch.Tensor:
+        if self.kind == "bf16":
+            return F.linear(x, self.w.embed)
+        return self.lm_head.multiply(x, out=out)
+
+    def embed_into(self, ids: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+        if self.kind == "se12":
+            return self.lm_head.decode_rows_into(ids.reshape(-1), out)
+        return torch.index_select(self.w.embed, 0, ids.reshape(-1), out=out)
+
     def embed_rows(self, ids: torch.Tensor) -> torch.Tensor:
         if self.kind == "se12":
             out = torch.empty((ids.numel(), self.w.shape.hidden), dtype=torch.bfloat16, device=ids.device)
@@ -188,8 +225,10 @@ class Gemma2Decoder:
     """Prefill + graph-captured greedy decode over one backend."""
 
     def __init__(self, weights: Gemma2Weights, backend: str, batch: int, max_len: int,
-                 encoded: dict | None = None, max_batch: int = nat.MAX_BATCH, scratch: torch.Tensor | None = None):
+                 encoded: dict | None = None, max_batch: int = nat.MAX_BATCH, scratch: torch.Tensor | None = None,
+                 fused_step: bool = True):
         s = weights.shape
+        max_len = -(-max_len // 8) * 8          # the step kernels read the caches 8 positions at a time
         self.s, self.w, self.batch, self.max_len = s, weights, batch, max_len
         dev = weights.embed.device
         self.dev = dev
@@ -207,6 +246,33 @@ class Gemma2Decoder:
         self.tokens = torch.zeros((batch, max_len), dtype=torch.int64, device=dev)
         self.last_logits = torch.zeros((batch, s.vocab), dtype=torch.bfloat16, device=dev)
         self.graph = None
+        self.fused_step = fused_step
+        if fused_step:
+            f32 = backend != "bf16"
+            shapes = projection_shapes(s)
+
+            def buf(n, dtype=torch.float32):
+                return torch.empty((batch, n), dtype=dtype, device=dev)
+
+            self.x = buf(s.hidden, torch.bfloat16)          # residual stream
+            self.h = buf(s.hidden, torch.bfloat16)          # normalised input of the next product
+            self.emb = buf(s.hidden, torch.bfloat16)
+            self.attn = buf(s.heads * s.head_dim, torch.bfloat16)
+            self.m = buf(s.intermediate, torch.bfloat16)
+            self.qkv = [buf(shapes[n][0]) for n in ("q", "k", "v")] if f32 else None
+            self.gu = [buf(s.intermediate), buf(s.intermediate)] if f32 else None
+            self.o_out = buf(s.hidden) if f32 else None
+            self.down_out = buf(s.hidden) if f32 else None
+            self.logits_out = buf(s.vocab) if f32 else None
+            self.embed_scale_value = float(self.embed_scale.float().item())
+            n = nat.lib().se12_step_attention_workspace(batch, s.heads, s.kv_heads, s.head_dim, max_len)
+            if n < 0:
+                nat.step_check(n)
+            self.attn_ws = torch.zeros(n, dtype=torch.uint8, device=dev)   # counters start at zero
+            n = nat.lib().se12_step_logits_workspace(batch, s.vocab)
+            if n < 0:
+                nat.step_check(n)
+            self.logits_ws = torch.zeros(n, dtype=torch.uint8, device=dev)
 
     def _rope(self, positions: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         freqs = positions.float()[..., None] * self.inv_freq
@@ -300,6 +366,52 @@ class Gemma2Decoder:
         self.pos.add_(1)
         self.step_index.add_(1)
 
+    # -- one decode step through the step kernels (captured) ------------------
+    def _step_fused(self) -> None:
+        s, B = self.s, self.batch
+        lib = nat.lib()
+        st = nat.stream_ptr()
+        BF16, F32 = nat.STEP_BF16, nat.STEP_F32
+        ck = nat.step_check
+
+        def dt(t: torch.Tensor) -> int:
+            return F32 if t.dtype == torch.float32 else BF16
+
+        def at(t: torch.Tensor, col: int) -> int:
+            return t.data_ptr() + col * t.element_size()
+
+        self.be.embed_into(self.ids, self.emb)
+        ck(lib.se12_step_rmsnorm(nat.ptr(self.emb), BF16, s.hidden, nat.ptr(self.w.layers[0]["input_norm"]),
+                                 nat.ptr(self.x), None, nat.ptr(self.h), B, s.hidden, s.eps, self.embed_scale_value, 0, st))
+        for li, lw in enumerate(self.w.layers):
+            (q, qo, qs), (k, ko, ks), (v, vo, _) = self.be.grouped_raw(li, ("q", "k", "v"), self.h, self.qkv)
+            ck(lib.se12_step_attention(at(q, qo), at(k, ko), at(v, vo), dt(q), qs, ks, nat.ptr(self.kt[li]),
+                                       nat.ptr(self.v[li]), nat.ptr(self.inv_freq), nat.ptr(self.pos), nat.ptr(self.attn),
+                                       B, s.heads, s.kv_heads, s.head_dim, self.max_len, self.scaling, s.attn_softcap,
+                                       0 if li % 2 else s.sliding_window, nat.ptr(self.attn_ws), self.attn_ws.numel(),
+                                       st))
+            o = self.be.single_raw(li, "o", self.attn, self.o_out)
+            ck(lib.se12_step_rmsnorm(nat.ptr(o), dt(o), o.shape[1], nat.ptr(lw["post_attn_norm"]), nat.ptr(self.x),
+                                     nat.ptr(lw["pre_ffw_norm"]), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
+            (g, go, gs), (u, uo, _) = self.be.grouped_raw(li, ("gate", "up"), self.h, self.gu)
+            ck(lib.se12_step_gelu_mul(at(g, go), at(u, uo), dt(g), gs, nat.ptr(self.m), B, s.intermediate, st))
+            dn = self.be.single_raw(li, "down", self.m, self.down_out)
+            nxt = self.w.layers[li + 1]["input_norm"] if li + 1 < s.layers else self.w.final_norm
+            ck(lib.se12_step_rmsnorm(nat.ptr(dn), dt(dn), dn.shape[1], nat.ptr(lw["post_ffw_norm"]), nat.ptr(self.x),
+                                     nat.ptr(nxt), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
+        lg = self.be.logits_raw(self.h, self.logits_out)
+        ck(lib.se12_step_logits_argmax(nat.ptr(lg), dt(lg), lg.shape[1], B, s.vocab, s.final_softcap,
+                                       nat.ptr(self.last_logits), nat.ptr(self.ids), nat.ptr(self.tokens), self.max_len,
+                                       nat.ptr(self.step_index), nat.ptr(self.logits_ws), self.logits_ws.numel(), st))
+        ck(lib.se12_step_advance(nat.ptr(self.pos), nat.ptr(self.step_index), st))
+
+    def step(self) -> None:
+        """One decode step, eagerly (fused step kernels, or framework ops)."""
+        if self.fused_step:
+            self._step_fused()
+        else:
+            self._step()
+
     @torch.no_grad()
     def capture(self) -> None:
         """Captures one decode step; the KV cache and counters are restored
@@ -309,11 +421,11 @@ class Gemma2Decoder:
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
-            self._step()
+            self.step()
         torch.cuda.current_stream().wait_stream(s)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            self._step()
+            self.step()
         torch.cuda.synchronize()
         self.ids.copy_(saved[0]); self.pos.copy_(saved[1]); self.step_index.copy_(saved[2]); self.tokens.copy_(saved[3])
         for t, c in zip(self.kt, saved[4]):
@@ -331,4 +443,4 @@ class Gemma2Decoder:
             if graph:
                 self.graph.replay()
             else:
-                self._step()
+                self.step()

@@ -1,7 +1,11 @@
 """The graph-captured Gemma-2 decode stack (se12_amd.gemma2) on a small shape:
 - the SE12 backend and the order-matched raw-BF16 twin give bit-identical
-  logits and the same greedy tokens over graph-replayed decode steps;
+  logits and the same greedy tokens over graph-replayed decode steps, with
+  the step kernels and with framework ops around the products;
 - graph replays give exactly what eager steps give;
+- a step through the step kernels agrees with the framework-op step from the
+  same state (logits and the KV-cache slot within BF16 rounding, for every
+  backend);
 - prefill and a decode step agree with transformers' Gemma2ForCausalLM on the
   same weights (attention with a contiguous key operand) within BF16
   rounding."""
@@ -32,14 +36,14 @@ def _prompt(gpu, batch, length, seed=3):
     return torch.randint(0, TINY.vocab, (batch, length), generator=g, device=gpu)
 
 
-@pytest.mark.parametrize("batch", [1, 3])
-def test_se12_and_raw_twin_decode_bit_identically(gpu, batch):
+@pytest.mark.parametrize("batch,fused", [(1, True), (3, True), (3, False)])
+def test_se12_and_raw_twin_decode_bit_identically(gpu, batch, fused):
     w = Gemma2Weights.random(TINY, gpu, seed=1)
     enc = _encoded(w)
     prompt = _prompt(gpu, batch, 12)
     out = {}
     for backend in ("se12", "raw"):
-        d = Gemma2Decoder(w, backend, batch, max_len=32, encoded=enc)
+        d = Gemma2Decoder(w, backend, batch, max_len=32, encoded=enc, fused_step=fused)
         d.prefill(prompt)
         d.capture()
         d.decode(10)
@@ -49,20 +53,59 @@ def test_se12_and_raw_twin_decode_bit_identically(gpu, batch):
     assert torch.equal(out["se12"][1], out["raw"][1])
 
 
-def test_graph_replays_equal_eager_steps(gpu):
+@pytest.mark.parametrize("backend,fused", [("se12", True), ("se12", False), ("bf16", True)])
+def test_graph_replays_equal_eager_steps(gpu, backend, fused):
     w = Gemma2Weights.random(TINY, gpu, seed=2)
     enc = _encoded(w)
     prompt = _prompt(gpu, 2, 9)
-    a = Gemma2Decoder(w, "se12", 2, max_len=24, encoded=enc)
+    a = Gemma2Decoder(w, backend, 2, max_len=24, encoded=enc, fused_step=fused)
     a.prefill(prompt)
     a.capture()
     a.decode(6)
-    b = Gemma2Decoder(w, "se12", 2, max_len=24, encoded=enc)
+    b = Gemma2Decoder(w, backend, 2, max_len=24, encoded=enc, fused_step=fused)
     b.prefill(prompt)
     b.decode(6, graph=False)
     torch.cuda.synchronize()
     assert torch.equal(a.tokens, b.tokens) and torch.equal(a.last_logits, b.last_logits)
     assert int(a.pos.item()) == 9 + 6
+
+
+def _close(a: torch.Tensor, b: torch.Tensor, rel: float = 0.02) -> bool:
+    a, b = a.float(), b.float()
+    return (a - b).abs().max().item() <= rel * max(b.abs().max().item(), 1e-3)
+
+
+@pytest.mark.parametrize("backend", ["se12", "raw", "bf16"])
+def test_step_kernels_agree_with_the_framework_step(gpu, backend):
+    """From one prefilled state, one step through the step kernels and one
+    through framework ops: the same KV-cache slot and logits up to BF16
+    rounding differences (FP32 sums in another order), propagated through
+    the layers."""
+    w = Gemma2Weights.random(TINY, gpu, seed=6)
+    for lw in w.layers:
+        for nm in ("input_norm", "post_attn_norm", "pre_ffw_norm", "post_ffw_norm"):
+            lw[nm].normal_(0.0, 0.1)
+    enc = _encoded(w) if backend == "se12" else None
+    prompt = _prompt(gpu, 2, 11, seed=8)
+    dec = {}
+    for fused in (True, False):
+        d = Gemma2Decoder(w, backend, 2, max_len=16, encoded=enc, fused_step=fused)
+        d.prefill(prompt)
+        d.decode(1, graph=False)
+        torch.cuda.synchronize()
+        dec[fused] = d
+    a, b = dec[True], dec[False]
+    assert int(a.pos.item()) == int(b.pos.item()) == 12 and int(a.step_index.item()) == 2
+    for li in range(TINY.layers):
+        # the prompt's slots are untouched; slot 11 is the new token's
+        assert torch.equal(a.kt[li][..., :11], b.kt[li][..., :11]) and torch.equal(a.v[li][:, :, :11], b.v[li][:, :, :11])
+        assert torch.equal(a.kt[li][..., 12:], b.kt[li][..., 12:])
+        assert _close(a.kt[li][..., 11], b.kt[li][..., 11]) and _close(a.v[li][:, :, 11], b.v[li][:, :, 11])
+    assert _close(a.last_logits, b.last_logits)
+    # the argmax is the first maximum of each decoder's own logits
+    for d in (a, b):
+        mx = d.last_logits.float().max(dim=1, keepdim=True).values
+        assert torch.equal(d.tokens[:, 1], (d.last_logits.float() == mx).float().argmax(dim=1))
 
 
 def test_agrees_with_transformers_gemma2(gpu):

@@ -1,0 +1,252 @@
+"""The decode-step kernels (include/se12_step.h) against the framework op
+sequences they replace (the eager Gemma-2 step in se12_amd/gemma2.py), on
+random inputs. Each framework BF16 op rounds its FP32 result to BF16; the
+kernels do the same op by op, so results agree to the last BF16 bit except
+where an FP32 sum runs in another order or a transcendental differs in its
+last FP32 bit: the bar is at most one BF16 ulp on any element and at least
+99% of elements bit-identical. Index work (argmax ids, the token slot, the
+KV-cache slot, the counters) is exact."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from se12_amd import _native as nat
+from se12_amd.gemma2 import rms_norm, rotate_half
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(gpu, seed):
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    return g
+
+
+def _ulp_close(got: torch.Tensor, want: torch.Tensor, min_exact: float = 0.99) -> None:
+    """At most one BF16 ulp apart everywhere, bit-identical on `min_exact` of
+    the elements."""
+    assert got.dtype == torch.bfloat16 and want.dtype == torch.bfloat16 and got.shape == want.shape
+    a = got.view(torch.int16).to(torch.int32)
+    b = want.view(torch.int16).to(torch.int32)
+    same = a == b
+    # adjacent BF16 values of one sign differ by 1 in their bit pattern
+    near = ((a - b).abs() <= 1) & ((a < 0) == (b < 0))
+    assert bool((same | near).all()), f"{int((~(same | near)).sum())} elements more than one ulp apart"
+    assert same.float().mean().item() >= min_exact
+
+
+def _rmsnorm(x, w1, residual, w2, out, hidden, eps, in_scale, mode, in_stride=None):
+    dtype = nat.STEP_F32 if x.dtype == torch.float32 else nat.STEP_BF16
+    nat.step_check(nat.lib().se12_step_rmsnorm(
+        nat.ptr(x), dtype, in_stride or x.shape[1], nat.ptr(w1), nat.ptr(residual), nat.ptr(w2), nat.ptr(out),
+        out.shape[0], hidden, eps, in_scale, mode, nat.stream_ptr()))
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 2304), (5, 256), (3, 100)])
+def test_rmsnorm_mode0_scaled_embedding(gpu, rows, hidden):
+    g = _gen(gpu, rows * 1000 + hidden)
+    emb = (torch.randn((rows, hidden), generator=g, device=gpu) * 0.02).to(torch.bfloat16)
+    w = (torch.randn(hidden, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    scale = torch.tensor(math.sqrt(hidden), dtype=torch.bfloat16, device=gpu)
+    x = torch.empty_like(emb)
+    h = torch.empty_like(emb)
+    _rmsnorm(emb, w, x, None, h, hidden, 1e-6, float(scale.float().item()), 0)
+    x_ref = emb * scale
+    assert torch.equal(x, x_ref)
+    _ulp_close(h, rms_norm(x_ref, w, 1e-6))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rmsnorm_mode1_residual_and_next_norm(gpu, dtype):
+    rows, hidden = 4, 2304
+    g = _gen(gpu, 7)
+    y = torch.randn((rows, hidden + 64), generator=g, device=gpu).to(dtype)[:, :hidden]   # strided input
+    x0 = torch.randn((rows, hidden), generator=g, device=gpu).to(torch.bfloat16)
+    w1 = (torch.randn(hidden, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(hidden, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    x = x0.clone()
+    h = torch.empty_like(x0)
+    _rmsnorm(y, w1, x, w2, h, hidden, 1e-6, 0.0, 1, in_stride=hidden + 64)
+    x_ref = x0 + rms_norm(y.to(torch.bfloat16), w1, 1e-6)
+    _ulp_close(x, x_ref)
+    _ulp_close(h, rms_norm(x, w2, 1e-6))     # the second norm of the kernel's own residual
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gelu_mul(gpu, dtype):
+    rows, cols, stride = 3, 9216, 2 * 9216
+    g = _gen(gpu, 11)
+    gu = (torch.randn((rows, stride), generator=g, device=gpu) * 2).to(dtype)
+    out = torch.empty((rows, cols), dtype=torch.bfloat16, device=gpu)
+    gate, up = gu[:, :cols], gu[:, cols:]
+    d = nat.STEP_F32 if dtype == torch.float32 else nat.STEP_BF16
+    nat.step_check(nat.lib().se12_step_gelu_mul(nat.ptr(gate), nat.ptr(up), d, stride, nat.ptr(out), rows, cols,
+                                                nat.stream_ptr()))
+    ref = F.gelu(gate.to(torch.bfloat16), approximate="tanh") * up.to(torch.bfloat16)
+    _ulp_close(out, ref)
+
+
+def _attention_ref(q, k, v, kt, vc, inv_freq, pos, heads, kvh, d, scaling, softcap, window):
+    """The eager step's attention at one position (gemma2.Gemma2Decoder._step)."""
+    B = q.shape[0]
+    freqs = torch.tensor([float(pos)], device=q.device)[..., None] * inv_freq
+    emb = torch.cat((freqs, freqs), dim=-1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    q = q.to(torch.bfloat16).view(B, heads, d)
+    k = k.to(torch.bfloat16).view(B, kvh, d)
+    v = v.to(torch.bfloat16)
+    q = q * cos + rotate_half(q) * sin
+    k = k * cos + rotate_half(k) * sin
+    L = kt.shape[-1]
+    kt = kt.clone()
+    vc = vc.clone()
+    kt[:, :, :, pos] = k
+    vc[:, :, pos, :] = v.view(B, kvh, d)
+    j = torch.arange(L, device=q.device)
+    allowed = j <= pos
+    if window:
+        allowed = allowed & (pos - j < window)
+    g = heads // kvh
+    sc = torch.matmul(q.view(B, kvh, g, d), kt) * scaling
+    sc = torch.tanh(sc / softcap) * softcap
+    sc = sc.masked_fill(~allowed, float("-inf"))
+    p = F.softmax(sc.float(), dim=-1).to(torch.bfloat16)
+    return torch.matmul(p, vc).reshape(B, heads * d), kt, vc
+
+
+def _workspace(gpu, batch, heads, kvh, d, L):
+    n = nat.lib().se12_step_attention_workspace(batch, heads, kvh, d, L)
+    assert n > 0
+    return torch.zeros(n, dtype=torch.uint8, device=gpu)
+
+
+def _attention(q, k, v, dtype, q_stride, kv_stride, kt, vc, inv_freq, pos_t, out, batch, heads, kvh, d, L, scaling,
+               softcap, window, ws):
+    dd = nat.STEP_F32 if dtype == torch.float32 else nat.STEP_BF16
+    nat.step_check(nat.lib().se12_step_attention(
+        nat.ptr(q), nat.ptr(k), nat.ptr(v), dd, q_stride, kv_stride, nat.ptr(kt), nat.ptr(vc), nat.ptr(inv_freq),
+        nat.ptr(pos_t), nat.ptr(out), batch, heads, kvh, d, L, scaling, softcap, window, nat.ptr(ws), ws.numel(),
+        nat.stream_ptr()))
+
+
+# (batch, heads, kv heads, head dim, cache length, position, window, input dtype): one chunk of 64 positions,
+# several chunks, a window starting inside a chunk, a cache length off the chunk size, every query-group size
+ATTN_CASES = [
+    (1, 8, 4, 256, 64, 0, 0, torch.float32),
+    (2, 8, 4, 256, 64, 37, 0, torch.float32),
+    (3, 8, 4, 256, 128, 90, 16, torch.float32),
+    (2, 8, 4, 256, 64, 63, 0, torch.bfloat16),
+    (1, 8, 4, 256, 640, 575, 0, torch.float32),
+    (2, 8, 4, 256, 160, 150, 100, torch.float32),
+    (1, 8, 4, 256, 304, 128, 0, torch.bfloat16),
+    (2, 4, 4, 128, 200, 199, 0, torch.float32),
+    (1, 8, 2, 64, 256, 130, 0, torch.float32),
+    (2, 16, 2, 128, 96, 70, 0, torch.float32),
+]
+
+
+@pytest.mark.parametrize("batch,heads,kvh,d,L,pos,window,dtype", ATTN_CASES)
+def test_attention_step(gpu, batch, heads, kvh, d, L, pos, window, dtype):
+    g = _gen(gpu, 100 + pos + L)
+    q = torch.randn((batch, heads * d), generator=g, device=gpu).to(dtype)
+    kv = torch.randn((batch, 2 * kvh * d), generator=g, device=gpu).to(dtype)   # k and v side by side
+    k, v = kv[:, : kvh * d], kv[:, kvh * d:]
+    kt = (torch.randn((batch, kvh, d, L), generator=g, device=gpu)).to(torch.bfloat16)
+    vc = (torch.randn((batch, kvh, L, d), generator=g, device=gpu)).to(torch.bfloat16)
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(0, d, 2, dtype=torch.int64, device=gpu).float() / d))
+    scaling, softcap = 256.0 ** -0.5, 50.0
+    want, kt_ref, vc_ref = _attention_ref(q, k, v, kt, vc, inv_freq, pos, heads, kvh, d, scaling, softcap, window)
+    out = torch.empty((batch, heads * d), dtype=torch.bfloat16, device=gpu)
+    pos_t = torch.tensor(pos, dtype=torch.int64, device=gpu)
+    ws = _workspace(gpu, batch, heads, kvh, d, L)
+    _attention(q, k, v, dtype, heads * d, 2 * kvh * d, kt, vc, inv_freq, pos_t, out, batch, heads, kvh, d, L, scaling,
+               softcap, window, ws)
+    torch.cuda.synchronize()
+    # the caches change only at `pos`, the value slot exactly
+    assert torch.equal(vc, vc_ref)
+    mask = torch.ones(L, dtype=torch.bool, device=gpu)
+    mask[pos] = False
+    assert torch.equal(kt[..., mask], kt_ref[..., mask])
+    _ulp_close(kt[..., pos].contiguous(), kt_ref[..., pos].contiguous(), min_exact=0.98)
+    diff = (out.float() - want.float()).abs()
+    assert diff.max().item() <= 2 ** -7 * want.float().abs().max().item() + 1e-3
+    assert (out == want).float().mean().item() >= 0.9
+    # the arrival counters are back at zero: a second call on the same workspace gives the same result
+    out2 = torch.empty_like(out)
+    _attention(q, k, v, dtype, heads * d, 2 * kvh * d, kt, vc, inv_freq, pos_t, out2, batch, heads, kvh, d, L,
+               scaling, softcap, window, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
+
+
+def test_attention_position_outside_the_cache_touches_nothing(gpu):
+    batch, heads, kvh, d, L = 1, 4, 2, 64, 80
+    q = torch.ones((batch, heads * d), device=gpu)
+    k = torch.ones((batch, kvh * d), device=gpu)
+    kt = torch.full((batch, kvh, d, L), 3.0, device=gpu).to(torch.bfloat16)
+    vc = torch.full((batch, kvh, L, d), 5.0, device=gpu).to(torch.bfloat16)
+    inv_freq = torch.ones(d // 2, device=gpu)
+    out = torch.full((batch, heads * d), 7.0, device=gpu).to(torch.bfloat16)
+    ws = _workspace(gpu, batch, heads, kvh, d, L)
+    for p in (L, -1):
+        pos_t = torch.tensor(p, dtype=torch.int64, device=gpu)
+        _attention(q, k, k, torch.float32, heads * d, kvh * d, kt, vc, inv_freq, pos_t, out, batch, heads, kvh, d, L,
+                   1.0, 0.0, 0, ws)
+        torch.cuda.synchronize()
+        assert bool((out == 0).all()) and bool((kt == 3).all()) and bool((vc == 5).all())
+    assert bool((ws[:8] == 0).all())
+
+
+def _argmax(logits, dtype, stride, rows, vocab, softcap, out, ids, tokens, max_len, step, ws):
+    d = nat.STEP_F32 if dtype == torch.float32 else nat.STEP_BF16
+    nat.step_check(nat.lib().se12_step_logits_argmax(nat.ptr(logits), d, stride, rows, vocab, softcap, nat.ptr(out),
+                                                     nat.ptr(ids), nat.ptr(tokens), max_len, nat.ptr(step),
+                                                     nat.ptr(ws), ws.numel(), nat.stream_ptr()))
+
+
+@pytest.mark.parametrize("dtype,vocab", [(torch.float32, 256000), (torch.bfloat16, 256000), (torch.float32, 3000)])
+def test_logits_argmax_and_token_slot(gpu, dtype, vocab):
+    rows, max_len = 3, 40
+    stride = vocab + 32
+    g = _gen(gpu, 17)
+    z = (torch.randn((rows, stride), generator=g, device=gpu) * 5).to(dtype)
+    z[1, vocab - 7] = 1000.0             # soft-capped to 30: ties with nothing else
+    z[2, 7] = z[2, vocab // 2 + 1] = 2000.0   # an exact tie across vocabulary slices: the first index wins
+    logits = z[:, :vocab]
+    out = torch.empty((rows, vocab), dtype=torch.bfloat16, device=gpu)
+    ids = torch.full((rows,), -1, dtype=torch.int64, device=gpu)
+    tokens = torch.full((rows, max_len), -1, dtype=torch.int64, device=gpu)
+    step = torch.tensor(5, dtype=torch.int64, device=gpu)
+    ws = torch.zeros(nat.lib().se12_step_logits_workspace(rows, vocab), dtype=torch.uint8, device=gpu)
+    _argmax(logits, dtype, stride, rows, vocab, 30.0, out, ids, tokens, max_len, step, ws)
+    torch.cuda.synchronize()
+    lb = logits.to(torch.bfloat16)
+    _ulp_close(out, torch.tanh(lb / 30.0) * 30.0)
+    # ids are the first maximum of the kernel's own capped logits
+    mx = out.float().max(dim=1, keepdim=True).values
+    first = (out.float() == mx).float().argmax(dim=1)
+    assert torch.equal(ids, first)
+    assert int(ids[1]) == vocab - 7 and int(ids[2]) == 7
+    assert torch.equal(tokens[:, 5], ids) and int((tokens != -1).sum()) == rows
+    # a step outside the token buffer writes ids only; the workspace's counters were left at zero
+    step.fill_(max_len)
+    tokens.fill_(-1)
+    ids.fill_(-1)
+    _argmax(logits, dtype, stride, rows, vocab, 30.0, None, ids, tokens, max_len, step, ws)
+    torch.cuda.synchronize()
+    assert bool((tokens == -1).all()) and torch.equal(ids, first)
+    assert bool((ws[: 4 * rows] == 0).all())
+
+
+def test_advance(gpu):
+    pos = torch.tensor(41, dtype=torch.int64, device=gpu)
+    step = torch.tensor(2, dtype=torch.int64, device=gpu)
+    for _ in range(3):
+        nat.step_check(nat.lib().se12_step_advance(nat.ptr(pos), nat.ptr(step), nat.stream_ptr()))
+    torch.cuda.synchronize()
+    assert int(pos) == 44 and int(step) == 5

@@ -19,7 +19,7 @@ HEADER = ROOT / "include" / "se12_gfx950.h"
 
 
 def header_functions() -> set[str]:
-    text = HEADER.read_text()
+    text = "\n".join(h.read_text() for h in sorted(HEADER.parent.glob("*.h")))
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return set(re.findall(r"\b(se12_[a-z0-9_]+)\s*\(", text))
 
@@ -109,3 +109,62 @@ def test_launch_candidates_respect_each_kernels_limits():
         pairs = [waves_and_splits(c, 2304, batch=batch, k=9216, float32_activations=f32) for c in cfgs]
         assert max(s for _, s in pairs) == max_s
         assert max(w for w, _ in pairs) == max_waves_per_block(batch, f32)
+
+
+def test_step_kernels_reject_invalid_arguments():
+    """Argument checks run before any HIP call, so this runs without a GPU
+    (host pointers are never dereferenced)."""
+    import torch
+
+    x = torch.zeros((2, 8), dtype=torch.bfloat16)
+    lib = nat.lib()
+    s = ctypes.c_void_p(None)
+    with pytest.raises(nat.Se12Error, match="mode 1"):
+        nat.step_check(lib.se12_step_rmsnorm(nat.ptr(x), nat.STEP_BF16, 8, nat.ptr(x[0]), None, None, nat.ptr(x),
+                                             2, 8, 1e-6, 0.0, 1, s))
+    with pytest.raises(nat.Se12Error, match="mode must be"):
+        nat.step_check(lib.se12_step_rmsnorm(nat.ptr(x), nat.STEP_BF16, 8, nat.ptr(x[0]), nat.ptr(x), nat.ptr(x[0]),
+                                             nat.ptr(x), 2, 8, 1e-6, 0.0, 2, s))
+    with pytest.raises(nat.Se12Error, match="bad argument"):
+        nat.step_check(lib.se12_step_gelu_mul(nat.ptr(x), nat.ptr(x), 7, 8, nat.ptr(x), 2, 8, s))
+    def attention(heads, kvh, d, L, ws, ws_bytes):
+        return lib.se12_step_attention(nat.ptr(x), nat.ptr(x), nat.ptr(x), nat.STEP_BF16, heads * d, kvh * d,
+                                       nat.ptr(x), nat.ptr(x), nat.ptr(x), nat.ptr(x), nat.ptr(x), 1, heads, kvh, d,
+                                       L, 1.0, 0.0, 0, ws, ws_bytes, s)
+
+    need = lib.se12_step_attention_workspace(1, 8, 4, 256, 640)
+    # counters, scores, chunk statistics and partial sums, each section 256-byte aligned
+    assert need == 256 + 8 * 10 * 64 * 4 + 768 + 8 * 10 * 256 * 4        # 640 B of statistics padded to 768
+    assert lib.se12_step_attention_workspace(1, 6, 4, 256, 640) < 0      # 6 query heads over 4 KV heads
+    assert lib.se12_step_attention_workspace(1, 24, 2, 64, 640) < 0      # groups of 12
+    assert lib.se12_step_attention_workspace(1, 8, 4, 512, 640) < 0      # head_dim above 256
+    assert lib.se12_step_attention_workspace(1, 8, 4, 100, 640) < 0      # head_dim not a multiple of 8
+    assert lib.se12_step_attention_workspace(1, 8, 4, 256, 644) < 0      # cache length not a multiple of 8
+    aligned = ctypes.c_void_p(1 << 20)                                     # never dereferenced
+    with pytest.raises(nat.Se12Error, match="bad shape"):
+        nat.step_check(attention(3, 2, 4, 4, aligned, 1 << 20))
+    with pytest.raises(nat.Se12Error, match="workspace too small"):
+        nat.step_check(attention(8, 4, 256, 640, aligned, need - 1))
+    with pytest.raises(nat.Se12Error, match="aligned"):
+        nat.step_check(attention(8, 4, 256, 640, ctypes.c_void_p((1 << 20) + 4), need))
+    with pytest.raises(nat.Se12Error, match="NULL"):
+        nat.step_check(attention(8, 4, 256, 640, None, need))
+    ws = lib.se12_step_logits_workspace(2, 256000)
+    assert ws == 256 + 512 + 512            # counters; 2 rows x 63 slices of 4,096 logits: values, indices
+    assert lib.se12_step_logits_workspace(0, 10) < 0
+
+    def argmax(rows, vocab, stride, wsp, ws_bytes):
+        return lib.se12_step_logits_argmax(nat.ptr(x), nat.STEP_BF16, stride, rows, vocab, 0.0, None, nat.ptr(x),
+                                           nat.ptr(x), 4, nat.ptr(x), wsp, ws_bytes, s)
+
+    with pytest.raises(nat.Se12Error, match="bad argument"):
+        nat.step_check(argmax(2, 8, 4, aligned, 1 << 20))                  # stride below vocab
+    with pytest.raises(nat.Se12Error, match="workspace too small"):
+        nat.step_check(argmax(2, 256000, 256000, aligned, ws - 1))
+    with pytest.raises(nat.Se12Error, match="aligned"):
+        nat.step_check(argmax(2, 256000, 256000, ctypes.c_void_p((1 << 20) + 16), ws))
+    with pytest.raises(nat.Se12Error, match="hidden above 8192"):
+        nat.step_check(lib.se12_step_rmsnorm(nat.ptr(x), nat.STEP_BF16, 9000, nat.ptr(x[0]), None, None, nat.ptr(x),
+                                             2, 9000, 1e-6, 0.0, 0, s))
+    with pytest.raises(nat.Se12Error, match="NULL"):
+        nat.step_check(lib.se12_step_advance(None, nat.ptr(x), s))

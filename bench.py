@@ -78,7 +78,41 @@ def parse_args(argv=None):
     p.add_argument("--profile-down", action="store_true",
                    help="only the dominant kernel (26 down_proj launches per step) and a 256 MiB device copy of known "
                         "size, for hardware-counter runs")
+    p.add_argument("--profile-e2e", choices=("se12", "raw", "bf16"), default=None,
+                   help="only the Gemma-2-2B decode of one backend: prefill 512, capture, a 0.5 s pause, 32 graph-"
+                        "replayed steps (kernel traces of the decode step)")
     return p.parse_args(argv)
+
+
+def profile_e2e(backend: str, device, steps: int = 32) -> int:
+    """The Gemma-2-2B greedy decode of `e2e_decode` for one backend, with a
+    0.5 s pause between capture and the timed steps so that a kernel trace
+    can cut the decode steps from prefill and capture."""
+    from se12_amd.gemma2 import GEMMA2_2B, PROJECTIONS, Gemma2Decoder, Gemma2Weights
+    from se12_amd.hip import encode_on_device
+
+    w = Gemma2Weights.random(GEMMA2_2B, device)
+    enc = None
+    if backend == "se12":
+        enc = {(li, n): encode_on_device(lw[n]) for li, lw in enumerate(w.layers) for n in PROJECTIONS}
+        enc["embed"] = encode_on_device(w.embed)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(4242)
+    prompt = torch.randint(0, GEMMA2_2B.vocab, (1, 512), generator=gen, device=device)
+    dec = Gemma2Decoder(w, backend, batch=1, max_len=512 + 128, encoded=enc)
+    dec.prefill(prompt)
+    dec.capture()
+    torch.cuda.synchronize()
+    time.sleep(0.5)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    dec.decode(steps)
+    end.record()
+    end.synchronize()
+    ms = start.elapsed_time(end)
+    print(json.dumps({"profile": f"gemma-2-2b decode, {backend}", "steps": steps, "ms_per_step": round(ms / steps, 4)}),
+          flush=True)
+    return 0
 
 
 def profile_down(args, device) -> int:
@@ -385,6 +419,8 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     if args.profile_down:
         return profile_down(args, dev)
+    if args.profile_e2e:
+        return profile_e2e(args.profile_e2e, dev)
     props = HipGpuProbe(0).properties()
     log(f"[bench] device {props.name} {props.arch} CUs={props.compute_units}")
     t0 = time.perf_counter()

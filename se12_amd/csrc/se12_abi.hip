@@ -61,6 +61,7 @@ struct DeviceScope {
 };
 
 constexpr int32_t kMaxSplits = 64;
+constexpr size_t kSideBytes = 64;  // one side record per tile (16 dwords)
 
 }  // namespace
 
@@ -71,7 +72,11 @@ struct se12_handle {
     int32_t TR, TC;
     se12_streams s;
     const uint16_t* wraw;
-    uint32_t* info;      // [T] per-tile sidecar word
+    uint32_t* info;      // [T] per-tile sidecar word (bind time only)
+    uint4* escpos;       // [T] listed escape positions (bind time only)
+    uint32_t* side;      // [T, 16] per-tile side records read by the kernels
+    int16_t* ovf_raw;    // tiles with more than the listed escapes, decoded at bind
+    int64_t n_overflow;
     uint32_t* lut;       // [256] pair table
     int64_t n_fallback;
     float* partial;
@@ -142,6 +147,9 @@ static int bind_common(se12_handle* h, int64_t rows, int64_t cols, int32_t max_b
 static void free_handle(se12_handle* h) {
     if (!h) return;
     if (h->info) (void)hipFree(h->info);
+    if (h->escpos) (void)hipFree(h->escpos);
+    if (h->side) (void)hipFree(h->side);
+    if (h->ovf_raw) (void)hipFree(h->ovf_raw);
     if (h->lut) (void)hipFree(h->lut);
     if (h->partial) (void)hipFree(h->partial);
     if (h->counters) (void)hipFree(h->counters);
@@ -158,6 +166,8 @@ static int check_shape(int64_t rows, int64_t cols, int32_t max_batch) {
         return fail(SE12_E_INVALID, "max_batch must be in [1, %d], got %d", SE12_MAX_BATCH, max_batch);
     return SE12_OK;
 }
+
+static DecodeArgs decode_args(const se12_handle* h, uint16_t* out);
 
 int se12_bind(const se12_streams* s, int64_t rows, int64_t cols, int32_t max_batch, void* stream,
               se12_handle** out) {
@@ -184,32 +194,51 @@ int se12_bind(const se12_streams* s, int64_t rows, int64_t cols, int32_t max_bat
     }
     hipStream_t st = static_cast<hipStream_t>(stream);
     int64_t* total_dev = nullptr;
-    int64_t total = 0;
+    int64_t totals[2] = {0, 0};  // fallback tiles, tiles with more than the listed escapes
     uint8_t cb[SE12_CODEBOOK_SIZE] = {0};
     uint32_t lut[256];
     hipError_t e = hipMalloc(&h->info, (size_t)h->T * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc(&h->escpos, (size_t)h->T * sizeof(uint4));
+    if (e == hipSuccess) e = hipMemsetAsync(h->escpos, 0, (size_t)h->T * sizeof(uint4), st);
+    if (e == hipSuccess) e = hipMalloc(&h->side, (size_t)h->T * kSideBytes);
     if (e == hipSuccess) e = hipMalloc(&h->lut, sizeof lut);
-    if (e == hipSuccess) e = hipMalloc(&total_dev, sizeof(int64_t));
-    if (e == hipSuccess) e = launch_tile_info(s->fallback_bitmap_dev, s->ec_dev, h->T, h->info, total_dev, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(&total, total_dev, sizeof total, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMalloc(&total_dev, sizeof totals);
+    if (e == hipSuccess) e = hipMemsetAsync(total_dev, 0, sizeof totals, st);
+    if (e == hipSuccess) e = launch_tile_info(s->fallback_bitmap_dev, s->ec_dev, h->T, h->info, h->escpos, total_dev, st);
+    if (e == hipSuccess) e = launch_side_records(h->info, s->esc_dev, h->escpos, h->T, h->side, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(totals, total_dev, sizeof totals, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipMemcpyAsync(cb, s->codebook_dev, sizeof cb, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e == hipSuccess) {
         for (uint32_t b = 0; b < 256; ++b) lut[b] = pair_lut_entry(cb, b);
         e = hipMemcpyAsync(h->lut, lut, sizeof lut, hipMemcpyHostToDevice, st);
     }
+    // tiles with more escapes than the sidecar lists are decoded once here and
+    // read as raw tiles by every kernel
+    if (e == hipSuccess && totals[1] > 0) {
+        e = hipMalloc(&h->ovf_raw, (size_t)totals[1] * SE12_TILE_SIZE * sizeof(int16_t));
+        if (e == hipSuccess) e = launch_overflow_decode(decode_args(h, nullptr), h->ovf_raw, st);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (total_dev) (void)hipFree(total_dev);
+    // the side records hold everything the kernels read
+    if (e == hipSuccess) {
+        (void)hipFree(h->info);
+        (void)hipFree(h->escpos);
+        h->info = nullptr;
+        h->escpos = nullptr;
+    }
     if (e != hipSuccess) {
         free_handle(h);
         return fail(SE12_E_HIP, "se12_bind: %s", hipGetErrorString(e));
     }
-    if (total * SE12_TILE_SIZE != s->fallback_raw_elems) {
+    if (totals[0] * SE12_TILE_SIZE != s->fallback_raw_elems) {
         free_handle(h);
         return fail(SE12_E_INVALID, "se12_bind: bitmap marks %lld fallback tiles but fallback_raw holds %lld elements",
-                    (long long)total, (long long)s->fallback_raw_elems);
+                    (long long)totals[0], (long long)s->fallback_raw_elems);
     }
-    h->n_fallback = total;
+    h->n_fallback = totals[0];
+    h->n_overflow = totals[1];
     *out = h;
     return SE12_OK;
 }
@@ -260,7 +289,7 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
 static bool uses_mfma(int32_t batch, bool xf32) { return !xf32 && batch >= kGemmMinBatch; }
 
 static int max_threads_for(int32_t bl, bool xf32, bool generic) {
-    return std::min(gemv_max_threads(bl, xf32, false, 1, false, generic), gemv_max_threads(bl, xf32, true, 1, false, generic));
+    return std::min(gemv_max_threads(bl, xf32, false, 1, 0, generic), gemv_max_threads(bl, xf32, true, 1, 0, generic));
 }
 
 // The default launch, re-derived for MI355X (256 CUs in 8 XCDs, wave64) from
@@ -367,7 +396,7 @@ static GemvPlan plan_gemv(int64_t tr, int64_t tc, bool raw, int32_t bl, bool xf3
     p.lds = gemv_lds_bytes(waves, bl);
     p.g = 1;
     const int64_t per_wave = ceil_div(ceil_div(tc, splits), waves);
-    p.pf = !generic && per_wave >= 4 && waves * 64 <= gemv_max_threads(bl, xf32, p.raw, 1, true, false);
+    p.pf = (!generic && per_wave >= 4 && waves * 64 <= gemv_max_threads(bl, xf32, p.raw, 1, 1, false)) ? 1 : 0;
     return p;
 }
 
@@ -380,7 +409,7 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
     p.blocks = (int32_t)(row_blocks * splits);
     p.lds = gemm_lds_bytes(waves, batch);
     p.g = 1;
-    p.pf = true;
+    p.pf = 1;
     return p;
 }
 
@@ -460,10 +489,10 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             GemvArgs& a = g.m[i];
             a.sm = h->s.sm_dev;
             a.ec = h->s.ec_dev;
-            a.esc = h->s.esc_dev;
             a.lut = h->lut;
-            a.info = h->info;
+            a.side = h->side;
             a.fb_raw = h->s.fallback_raw_dev;
+            a.ovf_raw = h->ovf_raw;
             a.wraw = h->wraw;
             a.x = static_cast<const char*>(x) + (size_t)b0 * h->K * esize;
             a.y = ys[i] + (size_t)b0 * h->N;
@@ -515,7 +544,10 @@ static DecodeArgs decode_args(const se12_handle* h, uint16_t* out) {
     a.bitmap = h->s.fallback_bitmap_dev;
     a.lut = h->lut;
     a.info = h->info;
+    a.escpos = h->escpos;
+    a.side = h->side;
     a.fb_raw = h->s.fallback_raw_dev;
+    a.ovf_raw = h->ovf_raw;
     a.out = out;
     a.N = h->N;
     a.K = h->K;

@@ -35,13 +35,11 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
                                             Sink&& sink) {
     TileSide side;
     TileLoads t;
-    // lane 0: this tile's side data; other lanes: the next tile (clamped),
-    // which keeps the addresses lane-dependent (vector loads)
-    load_side(side, a.esc, a.info, (lane & 1u) && tile + 1 < a.T ? tile + 1 : tile);
+    load_side(side, a.side, tile, lane);
     load_tile(t, a.sm, a.ec, tile, lane);
     const uint32_t info = side_info(side, 0);
     if (info_is_fallback(info)) {
-        const int16_t* raw = a.fb_raw + (int64_t)info_rank(info) * kTile;
+        const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
@@ -51,7 +49,7 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
     } else {
         uint32_t pat[4][8];
         lookup_tile(lut, t, pat);
-        if (info & 0xFu) resolve_tile_escapes(pat, t, info, side_esc(side, 0));
+        patch_tile_escapes(pat, info, side, 0, lane);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
@@ -155,31 +153,141 @@ __global__ __launch_bounds__(kScanThreads) void fallback_info_kernel(const uint8
     if (tid == 0) *total_out = total;
 }
 
-// escape chunk bits of every non-fallback tile: one wave per tile
+// escape chunk bits, escape count and listed escape positions of every
+// non-fallback tile: one wave per tile. Escapes are ranked in row-major
+// order (chunk, then lane, then weight within the lane), the order in which
+// they take the tile's esc slots.
 constexpr int kInfoWaves = 4;
 
-__global__ __launch_bounds__(kInfoWaves * kWave) void escape_info_kernel(const uint8_t* ec, int64_t T, uint32_t* info) {
+__global__ __launch_bounds__(kInfoWaves * kWave) void escape_info_kernel(const uint8_t* ec, int64_t T, uint32_t* info,
+                                                                          uint4* escpos) {
     const uint32_t lane = threadIdx.x & 63u;
     const int64_t tile = (int64_t)blockIdx.x * kInfoWaves + (threadIdx.x >> 6);
     if (tile >= T) return;
     const uint8_t* ect = ec + tile * (kTile / 2) + 8u * lane;
-    uint32_t mask = 0;
+    uint16_t* pos = reinterpret_cast<uint16_t*>(escpos + tile);
+    uint32_t mask = 0, run = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint2 e = *reinterpret_cast<const uint2*>(ect + 512 * j);
-        const bool any = (escape_nibbles(e.x) | escape_nibbles(e.y)) != 0u;
-        if (wave_any(any)) mask |= 1u << j;
+        uint32_t t0 = escape_nibbles(e.x), t1 = escape_nibbles(e.y);
+        const uint32_t cnt = __popc(t0) + __popc(t1);
+        const uint32_t incl = wave_incl_scan(cnt);
+        const uint32_t total = __builtin_amdgcn_readlane(incl, kWave - 1);
+        if (total) mask |= 1u << j;
+        uint32_t r = run + incl - cnt;
+        const uint32_t base = (4u * j + (lane >> 4)) * kTileCols + 16u * (lane & 15u);
+        while (t0 | t1) {
+            uint32_t p;
+            if (t0) {
+                p = (uint32_t)__builtin_ctz(t0) >> 2;
+                t0 &= t0 - 1u;
+            } else {
+                p = 8u + ((uint32_t)__builtin_ctz(t1) >> 2);
+                t1 &= t1 - 1u;
+            }
+            if (r < kListedEscapes) pos[r] = (uint16_t)(base + p);
+            ++r;
+        }
+        run += total;
     }
-    if (lane == 0 && !info_is_fallback(info[tile])) info[tile] = mask;
+    if (lane == 0 && !info_is_fallback(info[tile]))
+        info[tile] = mask | ((run < kInfoCountMax ? run : kInfoCountMax) << kInfoCountShift);
 }
 
-hipError_t launch_tile_info(const uint8_t* bitmap, const uint8_t* ec, int64_t T, uint32_t* info, int64_t* total,
-                            hipStream_t stream) {
+// Tiles with more than kListedEscapes escapes become raw tiles: rank them
+// (kInfoFallback | kInfoOverflow | rank) and count them.
+__global__ __launch_bounds__(kScanThreads) void overflow_info_kernel(int64_t T, uint32_t* info, int64_t* total_out) {
+    __shared__ int64_t tmp[kScanThreads];
+    const int tid = threadIdx.x;
+    const int64_t chunk = (T + kScanThreads - 1) / kScanThreads;
+    const int64_t t0 = (int64_t)tid * chunk;
+    const int64_t t1 = t0 + chunk < T ? t0 + chunk : T;
+    auto over = [&](int64_t t) {
+        const uint32_t v = info[t];
+        return !info_is_fallback(v) && info_escapes(v) > kListedEscapes;
+    };
+    int64_t count = 0;
+    for (int64_t t = t0; t < t1; ++t) count += over(t) ? 1 : 0;
+    int64_t total;
+    int64_t base = block_exclusive_scan(count, tmp, &total);
+    for (int64_t t = t0; t < t1; ++t)
+        if (over(t)) info[t] = kInfoFallback | kInfoOverflow | (uint32_t)base++;
+    if (tid == 0) *total_out = total;
+}
+
+// Decodes every overflow tile into raw[rank] (tile-local order, the layout of
+// the format's fallback tiles), ranking its escapes per chunk (lanes, then
+// weights within a lane): one wave per tile.
+__global__ __launch_bounds__(kInfoWaves * kWave) void overflow_decode_kernel(DecodeArgs a, int16_t* raw) {
+    SE12_DECLARE_LUT(lut);
+    const uint32_t lane = threadIdx.x & 63u;
+    store_block_lut(lut, reinterpret_cast<const uint4*>(a.lut)[lane], lane);
+    lds_barrier();
+    const int64_t tile = (int64_t)blockIdx.x * kInfoWaves + (threadIdx.x >> 6);
+    if (tile >= a.T) return;
+    const uint32_t info = a.info[tile];
+    if (!info_is_overflow(info)) return;
+    TileLoads t;
+    load_tile(t, a.sm, a.ec, tile, lane);
+    const uint4 esc = *reinterpret_cast<const uint4*>(a.esc + tile * kEscBudget);
+    uint32_t pat[4][8];
+    lookup_tile(lut, t, pat);
+    resolve_tile_escapes(pat, t, 0xFu, esc);
+    int16_t* out = raw + (int64_t)info_rank(info) * kTile;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        uint32_t w[8];
+        merge_chunk(pat[j], t.sm[j], w);
+        uint4* p = reinterpret_cast<uint4*>(out + 1024 * j + 16 * lane);
+        p[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
+}
+
+// The side record of every tile (one thread per record word).
+__global__ void side_record_kernel(const uint32_t* info, const uint8_t* esc, const uint4* escpos, int64_t T,
+                                   uint32_t* side) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= T * kSideWords) return;
+    const int64_t t = i / kSideWords;
+    const int k = (int)(i % kSideWords);
+    uint32_t v = 0;
+    if (k == 0)
+        v = info[t];
+    else if (k <= 4)
+        v = reinterpret_cast<const uint32_t*>(esc + t * kEscBudget)[k - 1];
+    else if (k <= 8)
+        v = reinterpret_cast<const uint32_t*>(escpos + t)[k - 5];
+    side[i] = v;
+}
+
+hipError_t launch_side_records(const uint32_t* info, const uint8_t* esc, const uint4* escpos, int64_t T, uint32_t* side,
+                               hipStream_t stream) {
+    if (T == 0) return hipSuccess;
+    const int64_t n = T * kSideWords;
+    hipLaunchKernelGGL(side_record_kernel, dim3((uint32_t)((n + 255) / 256)), dim3(256), 0, stream, info, esc, escpos, T,
+                       side);
+    return hipGetLastError();
+}
+
+hipError_t launch_overflow_decode(const DecodeArgs& a, int16_t* raw, hipStream_t stream) {
+    const int64_t blocks = (a.T + kInfoWaves - 1) / kInfoWaves;
+    hipLaunchKernelGGL(overflow_decode_kernel, dim3((uint32_t)blocks), dim3(kInfoWaves * kWave), 0, stream, a, raw);
+    return hipGetLastError();
+}
+
+hipError_t launch_tile_info(const uint8_t* bitmap, const uint8_t* ec, int64_t T, uint32_t* info, uint4* escpos,
+                            int64_t* total, hipStream_t stream) {
     hipLaunchKernelGGL(fallback_info_kernel, dim3(1), dim3(kScanThreads), 0, stream, bitmap, T, info, total);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || T == 0) return e;
     const int64_t blocks = (T + kInfoWaves - 1) / kInfoWaves;
-    hipLaunchKernelGGL(escape_info_kernel, dim3((uint32_t)blocks), dim3(kInfoWaves * kWave), 0, stream, ec, T, info);
+    hipLaunchKernelGGL(escape_info_kernel, dim3((uint32_t)blocks), dim3(kInfoWaves * kWave), 0, stream, ec, T, info,
+                       escpos);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(overflow_info_kernel, dim3(1), dim3(kScanThreads), 0, stream, T, info, total + 1);
     return hipGetLastError();
 }
 

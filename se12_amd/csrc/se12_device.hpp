@@ -186,13 +186,26 @@ __device__ __forceinline__ void merge_chunk(const uint32_t pat[8], uint4 sm, uin
 }
 
 // Per-tile word built at bind time (one per tile):
-//   bit 31 set   -> fallback tile, bits 0..30 = its rank among fallback tiles
+//   bit 31 set   -> a tile read as raw BF16: bits 0..29 = its rank among the
+//                   format's fallback tiles, or, with bit 30 set, among the
+//                   tiles holding more than kListedEscapes escapes, which
+//                   bind decodes once into a raw buffer of its own
 //   bit 31 clear -> bit j (j = 0..3) set iff chunk j (tile rows 4j..4j+3)
-//                   holds at least one escape code
+//                   holds at least one escape code; bits 8..12 = the tile's
+//                   escape count (at most kListedEscapes on this path)
+// and, per tile, the positions (row * 256 + column, row-major order: the
+// order escapes take their esc slots) of its kListedEscapes first escapes,
+// 16 bits each in one 16-byte word.
 constexpr uint32_t kInfoFallback = 0x80000000u;
+constexpr uint32_t kInfoOverflow = 0x40000000u;
+constexpr uint32_t kInfoCountShift = 8;
+constexpr uint32_t kInfoCountMax = 31;
+constexpr uint32_t kListedEscapes = 8;
 
 __device__ __forceinline__ bool info_is_fallback(uint32_t info) { return (info & kInfoFallback) != 0u; }
-__device__ __forceinline__ uint32_t info_rank(uint32_t info) { return info & ~kInfoFallback; }
+__device__ __forceinline__ bool info_is_overflow(uint32_t info) { return (info & kInfoOverflow) != 0u; }
+__device__ __forceinline__ uint32_t info_rank(uint32_t info) { return info & ~(kInfoFallback | kInfoOverflow); }
+__device__ __forceinline__ uint32_t info_escapes(uint32_t info) { return (info >> kInfoCountShift) & kInfoCountMax; }
 
 // One tile's `sm` and `ec` loads for one lane.
 struct TileLoads {
@@ -211,28 +224,37 @@ __device__ __forceinline__ void load_tile(TileLoads& t, const uint8_t* sm, const
     }
 }
 
-// The wave-uniform side data of up to 64 tiles, one tile per lane (lane g
-// holds tile g of the caller's list): the sidecar word and the 16 escape
-// slots. The per-lane addresses differ, so these stay vector loads (a scalar
-// load would share its wait counter with the LDS lookups and be waited for
-// at the first lookup). Read back with readlane.
+// The per-tile side record built at bind time: 16 dwords (64 bytes) per
+// tile, word 0 the sidecar word, words 1..4 the tile's 16 esc slots, words
+// 5..8 the listed escape positions, 9..15 zero. A wave reads records with one
+// dword load, lanes 16 s .. 16 s + 15 holding the record of its tile slot s
+// (up to 4 tiles per load): 256 bytes reach the registers instead of the
+// 64 x 36 a per-lane copy of each field would move. The per-lane addresses
+// differ, so this stays a vector load (a scalar load would share its wait
+// counter with the LDS lookups). Read back with readlane.
+constexpr int kSideWords = 16;
+
 struct TileSide {
-    uint32_t info;
-    uint4 esc;
+    uint32_t rec;
 };
 
-__device__ __forceinline__ void load_side(TileSide& s, const uint8_t* esc, const uint32_t* info, int64_t tile) {
-    s.info = info[tile];
-    s.esc = *reinterpret_cast<const uint4*>(esc + tile * kEscBudget);
+// `tile` is the tile of this lane's slot (lane / 16).
+__device__ __forceinline__ void load_side(TileSide& s, const uint32_t* side, int64_t tile, uint32_t lane) {
+    s.rec = side[tile * kSideWords + (lane & 15u)];
 }
 
-__device__ __forceinline__ uint32_t side_info(const TileSide& s, int g) {
-    return (uint32_t)__builtin_amdgcn_readlane((int)s.info, g);
+__device__ __forceinline__ uint32_t side_word(const TileSide& s, int g, int k) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)s.rec, 16 * g + k);
 }
+
+__device__ __forceinline__ uint32_t side_info(const TileSide& s, int g) { return side_word(s, g, 0); }
 
 __device__ __forceinline__ uint4 side_esc(const TileSide& s, int g) {
-    return make_uint4((uint32_t)__builtin_amdgcn_readlane((int)s.esc.x, g), (uint32_t)__builtin_amdgcn_readlane((int)s.esc.y, g),
-                      (uint32_t)__builtin_amdgcn_readlane((int)s.esc.z, g), (uint32_t)__builtin_amdgcn_readlane((int)s.esc.w, g));
+    return make_uint4(side_word(s, g, 1), side_word(s, g, 2), side_word(s, g, 3), side_word(s, g, 4));
+}
+
+__device__ __forceinline__ uint4 side_pos(const TileSide& s, int g) {
+    return make_uint4(side_word(s, g, 5), side_word(s, g, 6), side_word(s, g, 7), side_word(s, g, 8));
 }
 
 // All 32 pattern lookups of a tile (issued back to back).
@@ -249,6 +271,50 @@ __device__ __forceinline__ void resolve_tile_escapes(uint32_t pat[4][8], const T
     for (int j = 0; j < 4; ++j) {
         if (info & (1u << j)) resolve_escapes(pat[j], t.ec[j], esc, run);
     }
+}
+
+// pat[word / 8][word % 8] |= v for a wave-uniform word: the 32 words as
+// one vector value, so the uniform index becomes a register-indexed move
+// (on an array the computed index would move it to scratch memory).
+typedef uint32_t PatternVector __attribute__((ext_vector_type(32)));
+
+__device__ __forceinline__ void or_pattern_word(uint32_t pat[4][8], uint32_t word, uint32_t v) {
+    PatternVector t;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) t[i] = pat[i >> 3][i & 7];
+    t[word & 31u] |= v;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) pat[i >> 3][i & 7] = t[i];
+}
+
+// Patches the n (1..kListedEscapes) listed escapes of a tile: escape k sits
+// at pos_k = row * 256 + col and takes esc slot k. Everything but the final
+// OR is wave-uniform (scalar), so an escape costs a few instructions.
+__device__ __forceinline__ void patch_listed_escapes(uint32_t pat[4][8], uint4 pos, uint4 esc, uint32_t n,
+                                                     uint32_t lane) {
+    for (uint32_t k = 0; k < n; ++k) {
+        const uint32_t w = k < 4u ? (k < 2u ? pos.x : pos.y) : (k < 6u ? pos.z : pos.w);
+        const uint32_t p = (k & 1u) ? (w >> 16) : (w & 0xFFFFu);
+        const uint32_t row = (p >> 8) & 15u, col = p & 255u;
+        const uint32_t owner = ((row & 3u) << 4) | (col >> 4);         // lane of chunk row >> 2
+        const uint32_t word = ((row >> 2) << 3) | ((col & 15u) >> 1);  // pattern word of that lane
+        const uint32_t v = esc_byte(esc, k) << ((col & 1u) ? 23u : 7u);
+        or_pattern_word(pat, word, lane == owner ? v : 0u);
+    }
+}
+
+// The escapes of a tile read through the pair table (at most
+// kListedEscapes: bind turns tiles with more into raw tiles).
+__device__ __forceinline__ void patch_tile_escapes(uint32_t pat[4][8], uint32_t info, const TileSide& side, int g,
+                                                   uint32_t lane) {
+    const uint32_t n = info_escapes(info);
+    if (n != 0u) patch_listed_escapes(pat, side_pos(side, g), side_esc(side, g), n, lane);
+}
+
+// The raw BF16 of a tile that bind marked raw: the format's fallback tiles,
+// or the tiles bind decoded because they hold too many escapes.
+__device__ __forceinline__ const int16_t* raw_tile_ptr(uint32_t info, const int16_t* fb_raw, const int16_t* ovf_raw) {
+    return (info_is_overflow(info) ? ovf_raw : fb_raw) + (int64_t)info_rank(info) * kTile;
 }
 
 // Raw BF16 pairs of chunk j of a fallback tile (tile-local order, like sm).

@@ -205,8 +205,7 @@ __global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
         if constexpr (RAW) {
             load_raw_rows<GENERIC>(t.r, a, trl, kt, lane);
         } else {
-            const int kt2 = kb + (i + (int)(lane & 1u) < n ? i + (int)(lane & 1u) : n - 1);
-            load_side(t.side, a.esc, a.info, row_tiles + kt2);
+            load_side(t.side, a.side, row_tiles + kt, lane);
             load_tile(t.t, a.sm, a.ec, row_tiles + kt, lane);
         }
     };
@@ -225,7 +224,7 @@ __global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
         } else {
             const uint32_t info = side_info(t.side, 0);
             if (info_is_fallback(info)) {
-                const int16_t* raw = a.fb_raw + (int64_t)info_rank(info) * kTile;
+                const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t wv[8];
@@ -236,7 +235,7 @@ __global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
             } else {
                 uint32_t pat[4][8];
                 lookup_tile(lut, t.t, pat);
-                if (info & 0xFu) resolve_tile_escapes(pat, t.t, info, side_esc(t.side, 0));
+                patch_tile_escapes(pat, info, t.side, 0, lane);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t wv[8];

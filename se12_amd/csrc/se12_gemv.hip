@@ -136,7 +136,7 @@ __device__ __forceinline__ void se12_tile(const GemvArgs& a, const TileLoads& t,
     const int c0 = 16 * (int)(lane & 15u);
     const int lim = GENERIC ? (int)(a.K - (int64_t)kt * kTileCols) : kTileCols;
     if (info_is_fallback(info)) {
-        const int16_t* raw = a.fb_raw + (int64_t)info_rank(info) * kTile;
+        const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
@@ -148,7 +148,7 @@ __device__ __forceinline__ void se12_tile(const GemvArgs& a, const TileLoads& t,
     } else {
         uint32_t pat[4][8];
         lookup_tile(lut, t, pat);
-        if (info & 0xFu) resolve_tile_escapes(pat, t, info, side_esc(side, g));
+        patch_tile_escapes(pat, info, side, g, lane);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             uint32_t w[8];
@@ -219,7 +219,9 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         if constexpr (!RAW) {
             // lane g: side data of tile g (lanes past G read the next round's
             // tiles, clamped, which keeps the addresses lane-dependent)
-            load_side(rd.side, a.esc, a.info, row_tiles + tile_at(r * G + (int)(lane & 63u) % (G < 2 ? 2 : G)));
+            // slot s = lane / 16 reads round tile s (clamped: slots past G
+            // re-read the last one)
+            load_side(rd.side, a.side, row_tiles + tile_at(r * G + ((int)(lane >> 4) < G ? (int)(lane >> 4) : G - 1)), lane);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) load_x<B, XF32, GENERIC>(rd.x[g], a, tile_at(r * G + g), lane);

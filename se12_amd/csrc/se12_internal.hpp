@@ -10,10 +10,10 @@ namespace se12 {
 struct GemvArgs {
     const uint8_t* sm;
     const uint8_t* ec;
-    const uint8_t* esc;
     const uint32_t* lut;      // [256] pair table built at bind time
-    const uint32_t* info;     // [T] per-tile sidecar word (fallback rank / escape chunks)
+    const uint32_t* side;     // [T, 16] per-tile side records
     const int16_t* fb_raw;
+    const int16_t* ovf_raw;   // tiles with too many escapes, decoded at bind
     const uint16_t* wraw;     // raw twin: row-major [N, K] BF16 bits
     const void* x;            // [B, K] BF16 or FP32
     float* y;                 // [B, N]
@@ -44,7 +44,7 @@ struct GemvPlan {
     bool raw;
     bool generic;
     int g;
-    bool pf;
+    int pf;  // rounds in flight ahead of the decoded one (0 or 1)
     int waves;
     int blocks;
     size_t lds;
@@ -58,7 +58,10 @@ struct DecodeArgs {
     const uint8_t* bitmap;
     const uint32_t* lut;      // [256] pair table built at bind time
     const uint32_t* info;     // [T] per-tile sidecar word
+    const uint4* escpos;      // [T] listed escape positions
+    const uint32_t* side;     // [T, 16] per-tile side records
     const int16_t* fb_raw;
+    const int16_t* ovf_raw;
     const int64_t* rows;      // decode_rows only
     uint16_t* out;
     int64_t N, K, T, nrows, items;
@@ -93,11 +96,12 @@ constexpr int kLutBytes = 1024;
 // allocation (per round: a tile's streams + its x slice, 37 VGPRs at batch 1,
 // 40 for the raw twin; 8 more per extra batch row); the GENERIC variants run
 // one tile per round without prefetch. The build fails if any variant spills.
-constexpr int gemv_vgpr_estimate(int batch, bool raw, int g, bool pf) {
-    return raw ? 24 + 4 * (batch - 1) + (pf ? 2 : 1) * g * (40 + 8 * (batch - 1))
-               : 57 + 4 * (batch - 1) + (pf ? 2 : 1) * g * (37 + 8 * (batch - 1));
+// `pf` = rounds kept in flight ahead of the one being decoded (0 or 1).
+constexpr int gemv_vgpr_estimate(int batch, bool raw, int g, int pf) {
+    return raw ? 24 + 4 * (batch - 1) + (pf + 1) * g * (40 + 8 * (batch - 1))
+               : 57 + 4 * (batch - 1) + (pf + 1) * g * (37 + 8 * (batch - 1));
 }
-constexpr int gemv_max_threads(int batch, bool xf32, bool raw, int g, bool pf, bool generic) {
+constexpr int gemv_max_threads(int batch, bool xf32, bool raw, int g, int pf, bool generic) {
     return generic ? (batch >= 2 ? 512 : 1024)
                    : gemv_vgpr_estimate(batch, raw, g, pf) <= 128 ? 1024
                    : gemv_vgpr_estimate(batch, raw, g, pf) <= 256 ? 512 : 256;
@@ -107,7 +111,7 @@ constexpr int gemv_max_threads(int batch, bool xf32, bool raw, int g, bool pf, b
 // allocation target) for the variants whose occupancy sits on a VGPR
 // granule boundary: the batch-1 single-tile rounds at 5 waves (96 VGPRs),
 // two tiles per round at 4 (128). 1 = no target.
-constexpr int gemv_waves_per_simd(int batch, bool raw, int g, bool pf, bool generic) {
+constexpr int gemv_waves_per_simd(int batch, bool raw, int g, int pf, bool generic) {
     return (raw || generic || batch != 1 || pf) ? 1 : g == 1 ? 5 : g == 2 ? 4 : 1;
 }
 
@@ -134,8 +138,12 @@ hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hip
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream);
 // Bind-time sidecar: one word per tile (fallback rank, or the chunks holding
 // escape codes) and the fallback tile count.
-hipError_t launch_tile_info(const uint8_t* bitmap, const uint8_t* ec, int64_t T, uint32_t* info, int64_t* total,
+// total[0] = fallback tiles, total[1] = tiles with more than the listed escapes
+hipError_t launch_tile_info(const uint8_t* bitmap, const uint8_t* ec, int64_t T, uint32_t* info, uint4* escpos, int64_t* total,
                             hipStream_t stream);
+hipError_t launch_overflow_decode(const DecodeArgs& a, int16_t* raw, hipStream_t stream);
+hipError_t launch_side_records(const uint32_t* info, const uint8_t* esc, const uint4* escpos, int64_t T, uint32_t* side,
+                               hipStream_t stream);
 hipError_t launch_encode_histogram(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_count(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_scan(const EncodeArgs& a, hipStream_t stream);

@@ -51,3 +51,29 @@ def heavy_tailed_bf16(rows: int, cols: int, seed: int) -> np.ndarray:
 def uniform_bits(rows: int, cols: int, seed: int) -> np.ndarray:
     rng = np.random.default_rng(seed)
     return rng.integers(0, 65536, size=(rows, cols), dtype=np.uint32).astype(np.uint16).view(np.int16)
+
+
+# escape count of each tile of escape_count_bf16's matrix, tile-major
+ESCAPE_COUNTS = (0, 1, 2, 7, 8, 9, 12, 16, 17, 3, 8, 9, 1, 16, 0, 5)
+
+
+def escape_count_bf16(seed: int) -> tuple[np.ndarray, list[int]]:
+    """A 64 x 1024 matrix (4 x 4 tiles) whose tiles hold exactly ESCAPE_COUNTS
+    escapes: bulk exponents 111..125 fill the 15 codebook entries, each escape
+    takes an exponent in 90..109. Positions include a tile's first and last
+    weight, two escapes in one lane (16 weights) and every chunk. A tile with
+    17 escapes exceeds the escape budget and is a fallback tile."""
+    rng = np.random.default_rng(seed)
+    e = rng.integers(111, 126, size=(64, 1024)).astype(np.uint16)
+    for t, n in enumerate(ESCAPE_COUNTS):
+        tr, tc = divmod(t, 4)
+        if n == 0:
+            continue
+        fixed = [0, 4095, 17, 18][: min(n, 4)]        # first, last, two in lane 1 of chunk 0
+        rest = rng.choice(np.setdiff1d(np.arange(4096), fixed), size=n - len(fixed), replace=False)
+        pos = np.concatenate([np.array(fixed, dtype=np.int64), rest])
+        e[tr * 16 + pos // 256, tc * 256 + pos % 256] = rng.integers(90, 110, size=n)
+    sign = rng.integers(0, 2, size=e.shape).astype(np.uint16)
+    mant = rng.integers(0, 0x80, size=e.shape).astype(np.uint16)
+    return ((sign << 15) | (e << 7) | mant).view(np.int16), list(ESCAPE_COUNTS)
+

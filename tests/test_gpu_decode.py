@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from conftest import GOLDEN_NAMES, golden_as_encoding, load_golden
-from gpu_helpers import heavy_tailed_bf16, normal_case, to_device, uniform_bits
+from gpu_helpers import escape_count_bf16, heavy_tailed_bf16, normal_case, to_device, uniform_bits
 from oracle import se12_codec as o
 
 pytestmark = pytest.mark.gpu
@@ -89,3 +89,22 @@ def test_decode_rows_ragged_and_fallback(gpu):
     rows = tuple(range(47, -1, -5))
     got = HipSe12WeightDecoder().decode_rows(to_device(enc, gpu), RowIndices(values=rows))
     assert np.array_equal(got.bit_pattern, bits[list(rows)].reshape(-1))
+
+
+def test_decode_every_escape_count(gpu):
+    """Tiles with 0..16 escapes (listed in the bind-time sidecar up to 8, more
+    decoded to raw tiles at bind) and a fallback tile: bit-exact, whole matrix
+    and row subsets."""
+    from se12_amd.hip import HipSe12WeightDecoder, RowIndices
+
+    bits, counts = escape_count_bf16(seed=11)
+    enc = o.encode(bits.reshape(-1), 64, 1024)
+    codes = o.unpack_codes(enc["ec"]).reshape(16, 4096)
+    assert (codes == 15).sum(axis=1).tolist() == counts
+    assert o.fallback_tile_count(enc) == sum(1 for n in counts if n > 16)
+    assert np.array_equal(_decode(enc, gpu), bits)
+    dt = to_device(enc, gpu)
+    rows = [63, 0, 17, 31, 40, 15, 48]
+    got = HipSe12WeightDecoder().decode_rows(dt, RowIndices(tuple(rows)))
+    assert np.array_equal(got.bit_pattern, bits[rows].reshape(-1))
+

@@ -14,7 +14,8 @@ import pytest
 import torch
 
 from conftest import GOLDEN_NAMES, golden_as_encoding, load_golden
-from gpu_helpers import REL_TOL, bf16_tensor, heavy_tailed_bf16, max_rel_error, normal_case, to_device, uniform_bits
+from gpu_helpers import (REL_TOL, bf16_tensor, escape_count_bf16, heavy_tailed_bf16, max_rel_error, normal_case, to_device,
+                         uniform_bits)
 from oracle import se12_codec as o
 
 pytestmark = pytest.mark.gpu
@@ -317,3 +318,23 @@ def test_grouped_launch_rejects_mixed_groups(gpu):
     ys = (ctypes.c_void_p * 2)(y.data_ptr(), y.data_ptr())
     assert nat.lib().se12_gemv_grouped(hs, 2, nat.ptr(x), nat.X_BF16, 1, ys, None, nat.stream_ptr()) == nat.SE12_E_INVALID
     assert "one K" in nat.last_error()
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 6, 17])
+def test_every_escape_count_matches_oracle_and_raw_twin(gpu, batch):
+    """Tiles with 0..16 escapes (listed escapes up to 8, raw tiles decoded at
+    bind beyond) and a fallback tile, through the dot2 (B <= 4) and MFMA
+    kernels: within REL_TOL of the oracle, and bit-identical to the raw-BF16
+    twin under each launch shape."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+
+    bits, _ = escape_count_bf16(seed=12)
+    enc = o.encode(bits.reshape(-1), 64, 1024)
+    fused = Se12MatVecKernel(to_device(enc, gpu))
+    raw = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
+    xb = _x(batch, 1024, seed=batch)
+    _check(fused, enc, xb, gpu)
+    x = bf16_tensor(xb, gpu)
+    for cfg in [None] + list(_configs(64, 1024, batch=batch))[::3]:
+        assert torch.equal(fused.multiply(x, launch=cfg), raw.multiply(x, launch=cfg)), cfg
+

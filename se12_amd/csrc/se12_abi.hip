@@ -447,7 +447,8 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     int32_t waves, splits;
     int64_t grid_rows = tr_total;  // grid rows per split: tile rows, or row blocks (MFMA)
     if (launch) {
-        const int max_threads = mfma ? kGemmMaxThreads : max_threads_for(b_first, xf32, generic);
+        const int max_threads = mfma ? (generic ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
+                                     : max_threads_for(b_first, xf32, generic);
         const int min_threads = mfma ? 64 * gemm_min_waves(batch) : 64;
         if (launch->threads_per_block < min_threads || launch->threads_per_block > max_threads ||
             launch->threads_per_block % 64 != 0)

@@ -17,16 +17,19 @@
 // once per K tile. Each wave requests its tile streams two tiles ahead of
 // the decode (the edge-handling variants load and use in turn).
 //
-// A wave decodes its 16x256 tile exactly as the dot2 kernel does (same lane
-// mapping, escapes, fallback tiles), stores the BF16 tile in its own LDS
-// buffer and reads it back in the A-operand layout of
-// v_mfma_f32_16x16x32_bf16 (lane l: weight row l % 16, columns
-// 32 s + 8 (l / 16) .. + 7 of slab s); the B operand is the x slab (lane l:
-// batch row 16 g + l % 16, the same columns). 8 MFMAs per tile and group of
-// 16 batch rows, FP32 accumulate. Rows of both LDS buffers are padded to 528
-// bytes so that the 16-byte reads of 8 lanes per cycle hit distinct banks.
-// Batch rows past the batch in a 16-row group read stale LDS: MFMA output
-// column n depends on B column n only, and those columns are not stored.
+// A wave decodes its 16x256 tile in four parts of 64 columns, lane l taking
+// row l % 16 and the 16 columns 64 p + 16 (l / 16) .. + 15 of part p (the
+// same per-weight decode as the dot2 kernel: pair table, listed escapes, raw
+// tiles). Two lane-row swaps (v_permlane16_swap, v_permlane32_swap) then
+// leave each lane holding exactly its A operands of v_mfma_f32_16x16x32_bf16
+// for the part's two 32-column slices s (lane l: weight row l % 16, columns
+// 32 s + 8 (l / 16) .. + 7), so the decoded tile never goes through memory.
+// The B operand is the x slab (lane l: batch row 16 g + l % 16, the same
+// columns). 8 MFMAs per tile and group of 16 batch rows, FP32 accumulate, in
+// ascending slice order. Rows of the LDS x slabs are padded to 528 bytes so
+// that the 16-byte reads of 8 lanes per cycle hit distinct banks. Batch rows
+// past the batch in a 16-row group read stale LDS: MFMA output column n
+// depends on B column n only, and those columns are not stored.
 //
 // A wave owns whole tile rows, so there is no cross-wave reduction: it adds
 // its K tiles in ascending order, and for S > 1 the last wave of a tile row to
@@ -47,7 +50,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kRowBytes = 528;                    // 512 B of BF16 + 16 B of padding
-constexpr int kWaveTileBytes = kTileRows * kRowBytes;
 
 template <int BG>
 constexpr int x_slab_bytes() {
@@ -98,12 +100,56 @@ __device__ __forceinline__ void store_x_slab(char* xb, const XPieces& xr, int ba
     }
 }
 
+// The row layout: lane l holds row l % 16 and, in part p, the 16 columns
+// 64 p + 16 (l / 16) .. + 15 of the tile.
+__device__ __forceinline__ int row_layout_col(int p, uint32_t lane) { return 64 * p + 16 * (int)(lane >> 4); }
+
+// One tile's sm and ec bytes in the row layout (per part: 16 sm bytes, 8 ec
+// bytes of the lane's row).
+__device__ __forceinline__ void load_tile_rows(TileLoads& t, const uint8_t* sm, const uint8_t* ec, int64_t tile,
+                                               uint32_t lane) {
+    const uint8_t* smt = sm + tile * kTile + (lane & 15u) * kTileCols + 16u * (lane >> 4);
+    const uint8_t* ect = ec + tile * (kTile / 2) + (lane & 15u) * (kTileCols / 2) + 8u * (lane >> 4);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        t.sm[p] = *reinterpret_cast<const uint4*>(smt + 64 * p);
+        t.ec[p] = *reinterpret_cast<const uint2*>(ect + 32 * p);
+    }
+}
+
+// Raw BF16 of part p of a raw tile (tile-local row-major) in the row layout.
+__device__ __forceinline__ void load_raw_part(const int16_t* tile_raw, int p, uint32_t lane, uint32_t w[8]) {
+    const uint4* q = reinterpret_cast<const uint4*>(tile_raw + (lane & 15u) * kTileCols + row_layout_col(p, lane));
+    const uint4 a = q[0], b = q[1];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+// The lane's 16 decoded weights of a part (8 BF16 pairs: w[0..3] columns
+// c..c+7, w[4..7] columns c+8..c+15) become the A operands of the part's two
+// slices: a v_permlane16_swap (odd rows of the first register with even rows
+// of the second) and a v_permlane32_swap (upper half of the first with lower
+// half of the second) per register pair.
+__device__ __forceinline__ void rows_to_operands(const uint32_t w[8], bf16x8_t& a0, bf16x8_t& a1) {
+    uint32_t u[4], v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const auto s16 = __builtin_amdgcn_permlane16_swap(w[i], w[4 + i], false, false);
+        const auto s32 = __builtin_amdgcn_permlane32_swap(s16[0], s16[1], false, false);
+        u[i] = s32[0];
+        v[i] = s32[1];
+    }
+    a0 = __builtin_bit_cast(bf16x8_t, make_uint4(u[0], u[1], u[2], u[3]));
+    a1 = __builtin_bit_cast(bf16x8_t, make_uint4(v[0], v[1], v[2], v[3]));
+}
+
+// Raw-twin rows in the row layout (per part: the lane's 16 columns).
 template <bool GENERIC>
 __device__ __forceinline__ void load_raw_rows(uint4 r[4][2], const GemvArgs& a, int tr, int kt, uint32_t lane) {
-    const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
+    const int64_t row = (int64_t)tr * kTileRows + (lane & 15u);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int64_t row = (int64_t)tr * kTileRows + 4 * j + (lane >> 4);
+        const int64_t col = (int64_t)kt * kTileCols + row_layout_col(j, lane);
         if constexpr (!GENERIC) {
             const uint16_t* p = a.wraw + row * a.K + col;
             r[j][0] = reinterpret_cast<const uint4*>(p)[0];
@@ -124,14 +170,6 @@ __device__ __forceinline__ void load_raw_rows(uint4 r[4][2], const GemvArgs& a, 
     }
 }
 
-// chunk j of the lane's decoded weights (row 4j + lane/16, 16 columns) into
-// the wave's LDS tile buffer
-__device__ __forceinline__ void stage_chunk(char* buf, int j, uint32_t lane, const uint32_t w[8]) {
-    char* p = buf + (4 * j + (int)(lane >> 4)) * kRowBytes + 32 * (int)(lane & 15u);
-    reinterpret_cast<uint4*>(p)[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    reinterpret_cast<uint4*>(p)[1] = make_uint4(w[4], w[5], w[6], w[7]);
-}
-
 // weights at columns >= lim of the tile are zeroed
 __device__ __forceinline__ void zero_past_k(uint32_t w[8], int c0, int lim) {
 #pragma unroll
@@ -141,27 +179,22 @@ __device__ __forceinline__ void zero_past_k(uint32_t w[8], int c0, int lim) {
     }
 }
 
+// The MFMAs of part p (slices 2p and 2p + 1) for every batch group, the x
+// slab (B operands) read from LDS.
 template <int BG>
-__device__ __forceinline__ void mfma_tile(const char* wb, const char* xb, uint32_t lane, floatx4_t acc[BG]) {
+__device__ __forceinline__ void mfma_part(const bf16x8_t& a0, const bf16x8_t& a1, const char* xb, int p, uint32_t lane,
+                                          floatx4_t acc[BG]) {
     const int off = (int)(lane & 15u) * kRowBytes + 16 * (int)(lane >> 4);
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-        const bf16x8_t a = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(wb + off + 64 * s));
+    for (int h = 0; h < 2; ++h) {
+        const int s = 2 * p + h;
 #pragma unroll
         for (int g = 0; g < BG; ++g) {
             const uint4 bv = *reinterpret_cast<const uint4*>(xb + g * 16 * kRowBytes + off + 64 * s);
-            acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, __builtin_bit_cast(bf16x8_t, bv), acc[g], 0, 0, 0);
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h ? a1 : a0, __builtin_bit_cast(bf16x8_t, bv), acc[g], 0, 0,
+                                                              0);
         }
     }
-}
-
-// orders a wave's own LDS stores before its later loads of the same bytes
-// (and those loads before the next stores): LDS executes one wave's
-// instructions in order, so only the compiler has to be held back
-__device__ __forceinline__ void wave_lds_fence() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 template <bool RAW>
@@ -172,7 +205,8 @@ struct GemmTile {
 };
 
 template <int BG, bool RAW, bool GENERIC>
-__global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga, int batch) {
+__global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
+                                                                                                  int batch) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) char gsm[];
     int mi = 0;
@@ -194,7 +228,6 @@ __global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
     const int n = ke - kb;
     const int64_t row_tiles = (int64_t)trl * a.TC;
     char* xbuf = gsm;
-    char* wbuf = gsm + 2 * x_slab_bytes<BG>() + w * kWaveTileBytes;
 
     floatx4_t acc[BG];
 #pragma unroll
@@ -206,48 +239,49 @@ __global__ __launch_bounds__(kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
             load_raw_rows<GENERIC>(t.r, a, trl, kt, lane);
         } else {
             load_side(t.side, a.side, row_tiles + kt, lane);
-            load_tile(t.t, a.sm, a.ec, row_tiles + kt, lane);
+            load_tile_rows(t.t, a.sm, a.ec, row_tiles + kt, lane);
         }
     };
     auto use_tile = [&](const GemmTile<RAW>& t, int i) {
         const int kt = kb + i;
-        const int c0 = 16 * (int)(lane & 15u);
         const int lim = GENERIC ? (int)(a.K - (int64_t)kt * kTileCols) : kTileCols;
+        const char* xb = xbuf + (i & 1) * x_slab_bytes<BG>();
+        // one part: weights (row layout) -> A operands -> the part's MFMAs
+        auto part = [&](int p, uint32_t wv[8]) {
+            if constexpr (GENERIC) zero_past_k(wv, row_layout_col(p, lane), lim);
+            bf16x8_t a0, a1;
+            rows_to_operands(wv, a0, a1);
+            mfma_part<BG>(a0, a1, xb, p, lane, acc);
+        };
         if constexpr (RAW) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t wv[8] = {t.r[j][0].x, t.r[j][0].y, t.r[j][0].z, t.r[j][0].w,
-                                  t.r[j][1].x, t.r[j][1].y, t.r[j][1].z, t.r[j][1].w};
-                if constexpr (GENERIC) zero_past_k(wv, c0, lim);
-                stage_chunk(wbuf, j, lane, wv);
+            for (int p = 0; p < 4; ++p) {
+                uint32_t wv[8] = {t.r[p][0].x, t.r[p][0].y, t.r[p][0].z, t.r[p][0].w,
+                                  t.r[p][1].x, t.r[p][1].y, t.r[p][1].z, t.r[p][1].w};
+                part(p, wv);
             }
         } else {
             const uint32_t info = side_info(t.side, 0);
             if (info_is_fallback(info)) {
                 const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int p = 0; p < 4; ++p) {
                     uint32_t wv[8];
-                    load_raw_chunk(raw, j, lane, wv);
-                    if constexpr (GENERIC) zero_past_k(wv, c0, lim);
-                    stage_chunk(wbuf, j, lane, wv);
+                    load_raw_part(raw, p, lane, wv);
+                    part(p, wv);
                 }
             } else {
                 uint32_t pat[4][8];
                 lookup_tile(lut, t.t, pat);
-                patch_tile_escapes(pat, info, t.side, 0, lane);
+                patch_tile_escapes<true>(pat, info, t.side, 0, lane);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
+                for (int p = 0; p < 4; ++p) {
                     uint32_t wv[8];
-                    merge_chunk(pat[j], t.t.sm[j], wv);
-                    if constexpr (GENERIC) zero_past_k(wv, c0, lim);
-                    stage_chunk(wbuf, j, lane, wv);
+                    merge_chunk(pat[p], t.t.sm[p], wv);
+                    part(p, wv);
                 }
             }
         }
-        wave_lds_fence();
-        mfma_tile<BG>(wbuf, xbuf + (i & 1) * x_slab_bytes<BG>(), lane, acc);
-        wave_lds_fence();  // the next tile's stores follow these reads
     };
 
     uint4 lutv;
@@ -365,8 +399,9 @@ hipError_t gemm_b(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStrea
 }  // namespace
 
 size_t gemm_lds_bytes(int waves, int batch) {
+    (void)waves;
     const int bg = batch > 16 ? 2 : 1;
-    return (size_t)2 * 16 * bg * kRowBytes + (size_t)waves * kWaveTileBytes;
+    return (size_t)2 * 16 * bg * kRowBytes;
 }
 
 hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {

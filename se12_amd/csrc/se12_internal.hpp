@@ -130,6 +130,9 @@ hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t st
 // (ceil(tile rows / waves) per matrix), and tr_start is in those units.
 constexpr int kGemmMinBatch = 5;
 constexpr int kGemmMaxThreads = 512;
+// the edge-handling (GENERIC) MFMA variants, whose element-wise loads need
+// more registers, take at most 4 waves per block (enough for 32 batch rows)
+constexpr int kGemmMaxThreadsGeneric = 256;
 constexpr int kGemmMaxSplits = 16;
 constexpr int kGemmXPieces = 4;
 constexpr int gemm_min_waves(int batch) { return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces); }

@@ -29,6 +29,7 @@ MAX_K_SPLITS = 64
 MFMA_MIN_BATCH = 5
 MFMA_MAX_K_SPLITS = 16
 MFMA_MAX_WAVES = 8
+MFMA_MAX_WAVES_GENERIC = 4   # the edge-handling MFMA variants (K % 256 != 0 or unaligned x)
 
 
 @dataclasses.dataclass(frozen=True)
@@ -99,7 +100,7 @@ def max_waves_per_block(batch: int, float32_activations: bool = False, generic: 
     lane: 4 batch rows per launch, 2-4 rows in the edge-handling variants, or
     the batched MFMA kernel."""
     if uses_mfma(batch, float32_activations):
-        return MFMA_MAX_WAVES
+        return MFMA_MAX_WAVES_GENERIC if generic else MFMA_MAX_WAVES
     b = min(batch, 4)
     if generic or float32_activations:
         return 8 if b >= 2 else 16

@@ -337,29 +337,32 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(splits, s_cap));
 }
 
-// Row blocks of the MFMA grid: ceil(tile rows / waves) per matrix.
-static int64_t gemm_row_blocks(se12_handle* const* hs, int32_t count, int32_t waves) {
+// Row blocks of the MFMA grid: ceil(tile rows / rows per block) per matrix.
+static int64_t gemm_row_blocks(se12_handle* const* hs, int32_t count, int32_t rows) {
     int64_t rb = 0;
-    for (int32_t i = 0; i < count; ++i) rb += ceil_div(hs[i]->TR, waves);
+    for (int32_t i = 0; i < count; ++i) rb += ceil_div(hs[i]->TR, rows);
     return rb;
 }
 
-// Default launch of the MFMA kernel, from sweeps on MI355X over the
-// Gemma-2 2B/9B shapes at B = 8..32: the fewest waves per block the x slab
-// loads allow (batch / 8, rounded up). A wave owns a tile row of one K
-// split, so the launch has tile rows x splits waves; the best shapes kept
-// about 2.5 of them per CU (14336x3584: no split; 2304x9216: 4 splits),
-// with 3 or more K tiles per split for the two-tile prefetch.
-static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
+// Default launch of the MFMA kernel: rows per block fixed by the batch (the
+// fewest waves whose threads load an x slab, batch / 8 rounded up), then K
+// groups and K splits for about kGemmWavesPerCu waves per CU, each wave
+// keeping 3 or more K tiles for the two-tile prefetch.
+static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, bool generic, int32_t* waves_out,
                                 int32_t* splits_out) {
     const se12_handle* h0 = hs[0];
     int64_t tr = 0;
     for (int32_t i = 0; i < count; ++i) tr += hs[i]->TR;
     const int64_t cus = std::max<int32_t>(1, h0->cu_count);
+    const int64_t rows = gemm_min_waves(batch);
+    const int64_t target = kGemmWavesPerCu * cus;  // waves = tile rows x K groups x splits
+    const int64_t max_waves = (generic ? kGemmMaxThreadsGeneric : kGemmMaxThreads) / 64;
+    const int64_t kg_max = std::max<int64_t>(1, std::min<int64_t>(max_waves / rows, h0->TC / 3));
+    const int64_t kg = std::max<int64_t>(1, std::min<int64_t>(kg_max, ceil_div(target, tr)));
     const int64_t cap = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kGemmMaxSplits, (int64_t)h0->s_cap,
-                                                               ceil_div(h0->TC, 3)}));
-    *waves_out = gemm_min_waves(batch);
-    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, (5 * cus + tr) / (2 * tr)));
+                                                               h0->TC / (3 * kg)}));
+    *waves_out = (int32_t)(rows * kg);
+    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, target / (tr * kg)));
 }
 
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
@@ -370,9 +373,9 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
                          (h->format == SE12_FORMAT_RAW_BF16 && h->N % SE12_TILE_ROWS != 0);
     se12_handle* hs[1] = {const_cast<se12_handle*>(h)};
     if (uses_mfma(batch, false)) {
-        gemm_default_launch(hs, 1, batch, &waves, &splits);
+        gemm_default_launch(hs, 1, batch, generic, &waves, &splits);
         out->threads_per_block = waves * 64;
-        out->blocks = (int32_t)(gemm_row_blocks(hs, 1, waves) * splits);
+        out->blocks = (int32_t)(gemm_row_blocks(hs, 1, gemm_min_waves(batch)) * splits);
         return SE12_OK;
     }
     default_launch(h->TR, h->TC, h->cu_count, h->s_cap, batch, false, generic, &waves, &splits);
@@ -455,7 +458,10 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [%d, %d] at batch %d", fn,
                         launch->threads_per_block, min_threads, max_threads, batch);
         waves = launch->threads_per_block / 64;
-        if (mfma) grid_rows = gemm_row_blocks(hs, count, waves);
+        if (mfma && waves % gemm_min_waves(batch) != 0)
+            return fail(SE12_E_INVALID, "%s: %d waves per block at batch %d: the MFMA kernel takes %d tile rows per block "
+                        "times K groups", fn, waves, batch, gemm_min_waves(batch));
+        if (mfma) grid_rows = gemm_row_blocks(hs, count, gemm_min_waves(batch));
         if (launch->blocks <= 0 || launch->blocks % grid_rows != 0)
             return fail(SE12_E_INVALID, "%s: blocks %d must be a positive multiple of the %lld %s", fn, launch->blocks,
                         (long long)grid_rows, mfma ? "row blocks (tile rows / waves, rounded up, per matrix)" : "tile rows");
@@ -465,8 +471,8 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             return fail(SE12_E_CAPACITY, "%s: %d K splits exceed the limit %d at batch %d", fn, splits, cap, batch);
     } else {
         if (mfma) {
-            gemm_default_launch(hs, count, batch, &waves, &splits);
-            grid_rows = gemm_row_blocks(hs, count, waves);
+            gemm_default_launch(hs, count, batch, generic, &waves, &splits);
+            grid_rows = gemm_row_blocks(hs, count, gemm_min_waves(batch));
         } else {
             default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, &waves, &splits);
         }
@@ -484,6 +490,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         const int32_t bl = std::min<int32_t>(step, batch - b0);
         GemvGroupArgs g{};
         g.count = count;
+        g.rows_per_block = mfma ? gemm_min_waves(bl) : 1;
         int32_t start = 0;
         for (int32_t i = 0; i < count; ++i) {
             const se12_handle* h = hs[i];
@@ -506,7 +513,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.TC = h->TC;
             a.S = splits;
             g.tr_start[i] = start;
-            start += mfma ? (int32_t)ceil_div(h->TR, waves) : h->TR;
+            start += mfma ? (int32_t)ceil_div(h->TR, gemm_min_waves(bl)) : h->TR;
         }
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);

@@ -5,17 +5,19 @@
 // lws/adapters/cuda/kernels/gemv_se12.cu:50-142 at batch B, which runs one
 // warp per (row, batch) element and reads W B times.
 //
-// Grid: block = W wave64s over W consecutive tile rows (wave w owns tile row
-// W * row_block + w), blockIdx.y = K split s covering the K tiles
-// [s*TC/S, (s+1)*TC/S). A grouped launch serves up to 4 matrices with the
-// same K: their row blocks follow one another along blockIdx.x.
+// Grid: block = R x KG wave64s: R consecutive tile rows (R = ceil(batch / 8),
+// the fewest waves whose threads load an x slab in one go) times KG K groups;
+// wave w owns tile row R * row_block + w % R and, of the split's K tiles, the
+// ones of K group w / R (every KG-th tile). blockIdx.y = K split s covering
+// the K tiles [s*TC/S, (s+1)*TC/S). A grouped launch serves up to 4 matrices
+// with the same K: their row blocks follow one another along blockIdx.x.
 //
-// Per K tile the block's waves share one copy of the x slab (batch rows x 256
-// columns, BF16) in LDS, double-buffered: every thread requests up to 4
-// pieces of 16 bytes of slab i + 2 while its wave decodes tile i and writes
-// those of slab i + 1 to the other buffer after its MFMAs; the block meets
-// once per K tile. Each wave requests its tile streams two tiles ahead of
-// the decode (the edge-handling variants load and use in turn).
+// Per step each K group's waves share one copy of their x slab (batch rows x
+// 256 columns, BF16) in LDS, double-buffered: every thread requests up to 4
+// pieces of 16 bytes of the slabs of step i + 2 while its wave decodes tile
+// i and writes those of step i + 1 to the other buffer after its MFMAs; the
+// block meets once per step. Each wave requests its tile streams two tiles
+// ahead of the decode (the edge-handling variants load and use in turn).
 //
 // A wave decodes its 16x256 tile in four parts of 64 columns, lane l taking
 // row l % 16 and the 16 columns 64 p + 16 (l / 16) .. + 15 of part p (the
@@ -31,16 +33,19 @@
 // past the batch in a 16-row group read stale LDS: MFMA output column n
 // depends on B column n only, and those columns are not stored.
 //
-// A wave owns whole tile rows, so there is no cross-wave reduction: it adds
-// its K tiles in ascending order, and for S > 1 the last wave of a tile row to
-// finish (device-scope arrival counter, reset by that wave) adds the S
-// partials in ascending split order. The launch shape (W, S) fixes every sum:
-// the raw-BF16 twin (same kernel, RAW) is bit-identical under one shape.
+// A wave adds its K tiles in ascending order; the K groups of a tile row are
+// added in LDS in ascending group order by the group-0 wave, and for S > 1
+// the last wave of a tile row to finish (device-scope arrival counter, reset
+// by that wave) adds the S partials in ascending split order. The launch
+// shape (W, S) fixes every sum: the raw-BF16 twin (same kernel, RAW) is
+// bit-identical under one shape.
 //
 // FAST variants need K % 256 == 0 and 16-byte aligned x rows (and, for the
 // raw twin, N % 16 == 0 and an aligned W); GENERIC variants guard loads by
 // the matrix edges and zero weights and x past K (padding can decode to
 // +inf when codebook[0] = 255).
+#include <algorithm>
+
 #include "se12_device.hpp"
 #include "se12_internal.hpp"
 
@@ -66,14 +71,23 @@ struct XPieces {
 // the matrix): a load skipped on some path leaves the compiler unable to
 // count the loads in flight, and it then waits for all of them - the
 // prefetched tiles included - before the next decode.
+// The slabs of one step: K group g's slab is x at K tile kb + g + KG i
+// (clamped into the split; a clamped slab is loaded but not used). Piece p
+// of the step: group p / (batch * 32), batch row (p % (batch * 32)) / 32,
+// columns 8 (p % 32) .. + 7.
 template <bool GENERIC>
-__device__ __forceinline__ XPieces load_x_slab(const GemvArgs& a, int batch, int kt, int tid, int threads) {
+__device__ __forceinline__ XPieces load_x_slab(const GemvArgs& a, int batch, int kb, int n, int KG, int i, int tid,
+                                               int threads) {
     XPieces xr;
+    const int per = batch * 32;
 #pragma unroll
     for (int k = 0; k < kGemmXPieces; ++k) {
-        const int p = min(tid + k * threads, batch * 32 - 1);
-        const uint16_t* row = static_cast<const uint16_t*>(a.x) + (int64_t)(p >> 5) * a.K;
-        const int64_t col = (int64_t)kt * kTileCols + 8 * (p & 31);
+        const int p = min(tid + k * threads, KG * per - 1);
+        const int g = p / per, q = p - g * per;
+        const int t = g + KG * i;
+        const int kt = kb + (t < n ? t : n - 1);
+        const uint16_t* row = static_cast<const uint16_t*>(a.x) + (int64_t)(q >> 5) * a.K;
+        const int64_t col = (int64_t)kt * kTileCols + 8 * (q & 31);
         if constexpr (!GENERIC) {
             xr.v[k] = *reinterpret_cast<const uint4*>(row + col);
         } else {
@@ -90,13 +104,17 @@ __device__ __forceinline__ XPieces load_x_slab(const GemvArgs& a, int batch, int
     return xr;
 }
 
-// pieces past the slab repeat the last piece: the same bytes to the same
-// address as the thread that owns it
-__device__ __forceinline__ void store_x_slab(char* xb, const XPieces& xr, int batch, int tid, int threads) {
+// pieces past the step's slabs repeat the last piece: the same bytes to the
+// same address as the thread that owns it. Group g's slab sits at xb + g *
+// slab_bytes.
+__device__ __forceinline__ void store_x_slab(char* xb, int slab_bytes, const XPieces& xr, int batch, int KG, int tid,
+                                             int threads) {
+    const int per = batch * 32;
 #pragma unroll
     for (int k = 0; k < kGemmXPieces; ++k) {
-        const int p = min(tid + k * threads, batch * 32 - 1);
-        *reinterpret_cast<uint4*>(xb + (p >> 5) * kRowBytes + 16 * (p & 31)) = xr.v[k];
+        const int p = min(tid + k * threads, KG * per - 1);
+        const int g = p / per, q = p - g * per;
+        *reinterpret_cast<uint4*>(xb + g * slab_bytes + (q >> 5) * kRowBytes + 16 * (q & 31)) = xr.v[k];
     }
 }
 
@@ -215,10 +233,13 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     const GemvArgs& a = ga.m[mi];
     const int threads = blockDim.x;
     const int W = threads >> 6;
+    const int R = ga.rows_per_block;
+    const int KG = W / R;
     const int tid = threadIdx.x;
     const uint32_t lane = threadIdx.x & 63u;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int tr = ((int)blockIdx.x - ga.tr_start[mi]) * W + w;
+    const int kg = w / R;
+    const int tr = ((int)blockIdx.x - ga.tr_start[mi]) * R + (w - kg * R);
     const bool active = tr < a.TR;
     const int trl = active ? tr : a.TR - 1;  // row the loads of an idle wave use
     const int S = a.S;
@@ -226,15 +247,18 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     const int kb = (int)(((uint32_t)s * (uint32_t)a.TC) / (uint32_t)S);
     const int ke = (int)(((uint32_t)(s + 1) * (uint32_t)a.TC) / (uint32_t)S);
     const int n = ke - kb;
+    const int steps = (n + KG - 1) / KG;  // K group kg takes the split's tiles kg, kg + KG, ...
     const int64_t row_tiles = (int64_t)trl * a.TC;
-    char* xbuf = gsm;
+    const int slab_bytes = x_slab_bytes<BG>();
+    char* xbuf = gsm;  // [2 buffers][KG slabs]
 
     floatx4_t acc[BG];
 #pragma unroll
     for (int g = 0; g < BG; ++g) acc[g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto load_tile_i = [&](GemmTile<RAW>& t, int i) {
-        const int kt = kb + (i < n ? i : n - 1);
+        const int j = kg + KG * i;
+        const int kt = kb + (j < n ? j : n - 1);
         if constexpr (RAW) {
             load_raw_rows<GENERIC>(t.r, a, trl, kt, lane);
         } else {
@@ -243,9 +267,9 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
         }
     };
     auto use_tile = [&](const GemmTile<RAW>& t, int i) {
-        const int kt = kb + i;
+        const int kt = kb + kg + KG * i;
         const int lim = GENERIC ? (int)(a.K - (int64_t)kt * kTileCols) : kTileCols;
-        const char* xb = xbuf + (i & 1) * x_slab_bytes<BG>();
+        const char* xb = xbuf + ((i & 1) * KG + kg) * slab_bytes;
         // one part: weights (row layout) -> A operands -> the part's MFMAs
         auto part = [&](int p, uint32_t wv[8]) {
             if constexpr (GENERIC) zero_past_k(wv, row_layout_col(p, lane), lim);
@@ -292,49 +316,74 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     // Tile streams and x pieces are requested D - 1 steps ahead of their
     // use (D = 3; the GENERIC variants, whose element-wise loads are packed
     // as they arrive, load and use in turn): under a full-bandwidth stream
-    // even the L2 hits of x take about a step to return. Steps run in groups
-    // of D so that every step's loads are issued on every path (steps past
-    // the last tile reload it and skip the decode): a load skipped on some
-    // path would make the compiler wait for all loads in flight. Slab i + 1
-    // is stored to LDS at the end of step i.
+    // even the L2 hits of x take about a step to return. The loop body holds
+    // D steps so that every step's loads are issued on every path that goes
+    // on (loads past the last tile reload it): a load skipped on some path
+    // would make the compiler wait for all loads in flight. Slab i + 1 is
+    // stored to LDS at the end of step i.
     constexpr int D = GENERIC ? 1 : 3;
-    auto slab = [&](int i) { return kb + (i < n ? i : n - 1); };
+    auto x_step = [&](int i) { return load_x_slab<GENERIC>(a, batch, kb, n, KG, i, tid, threads); };
+    auto has_tile = [&](int i) { return kg + KG * i < n; };
     if constexpr (D == 3) {
         GemmTile<RAW> t0, t1, t2;
         load_tile_i(t0, 0);
-        XPieces x0 = load_x_slab<GENERIC>(a, batch, slab(0), tid, threads);
+        XPieces x0 = x_step(0);
         load_tile_i(t1, 1);
-        XPieces x1 = load_x_slab<GENERIC>(a, batch, slab(1), tid, threads);
+        XPieces x1 = x_step(1);
         XPieces x2;
         if constexpr (!RAW) store_block_lut(lut, lutv, lane);
-        store_x_slab(xbuf, x0, batch, tid, threads);
+        store_x_slab(xbuf, slab_bytes, x0, batch, KG, tid, threads);
         lds_barrier();
         auto step = [&](const GemmTile<RAW>& cur, GemmTile<RAW>& ahead, const XPieces& x_next, XPieces& x_ahead,
                         int i) {
-            x_ahead = load_x_slab<GENERIC>(a, batch, slab(i + 2), tid, threads);
+            x_ahead = x_step(i + 2);
             load_tile_i(ahead, i + 2);
-            if (i < n) use_tile(cur, i);  // an idle wave decodes row trl; its sums are dropped
-            store_x_slab(xbuf + ((i + 1) & 1) * x_slab_bytes<BG>(), x_next, batch, tid, threads);
+            if (has_tile(i)) use_tile(cur, i);  // an idle wave decodes row trl; its sums are dropped
+            store_x_slab(xbuf + ((i + 1) & 1) * KG * slab_bytes, slab_bytes, x_next, batch, KG, tid, threads);
             lds_barrier();
         };
-        for (int i = 0; i < n; i += 3) {
+        // the loop leaves after the last step (not after a group of three):
+        // past it nothing waits on the loads it issued
+        int i = 0;
+        while (true) {
             step(t0, t2, x1, x2, i);
-            step(t1, t0, x2, x0, i + 1);
-            step(t2, t1, x0, x1, i + 2);
+            if (++i >= steps) break;
+            step(t1, t0, x2, x0, i);
+            if (++i >= steps) break;
+            step(t2, t1, x0, x1, i);
+            if (++i >= steps) break;
         }
     } else {
         GemmTile<RAW> t0;
-        XPieces xr = load_x_slab<GENERIC>(a, batch, slab(0), tid, threads);
+        XPieces xr = x_step(0);
         if constexpr (!RAW) store_block_lut(lut, lutv, lane);
-        store_x_slab(xbuf, xr, batch, tid, threads);
+        store_x_slab(xbuf, slab_bytes, xr, batch, KG, tid, threads);
         lds_barrier();
-        for (int i = 0; i < n; ++i) {
-            xr = load_x_slab<GENERIC>(a, batch, slab(i + 1), tid, threads);
+        for (int i = 0; i < steps; ++i) {
+            xr = x_step(i + 1);
             load_tile_i(t0, i);
-            use_tile(t0, i);
-            store_x_slab(xbuf + ((i + 1) & 1) * x_slab_bytes<BG>(), xr, batch, tid, threads);
+            if (has_tile(i)) use_tile(t0, i);
+            store_x_slab(xbuf + ((i + 1) & 1) * KG * slab_bytes, slab_bytes, xr, batch, KG, tid, threads);
             lds_barrier();
         }
+    }
+    // the K groups of a tile row: groups 1..KG-1 hand their sums to group 0
+    // through LDS (the x slabs are no longer read: every wave passed the
+    // last step's barrier), which adds them in ascending group order
+    if (KG > 1) {
+        float* red = reinterpret_cast<float*>(gsm);  // [KG - 1][R][64 lanes][BG][4]
+        const int rw = w - kg * R;
+        if (kg > 0) {
+#pragma unroll
+            for (int g = 0; g < BG; ++g)
+                *reinterpret_cast<floatx4_t*>(red + ((((kg - 1) * R + rw) * 64 + (int)lane) * BG + g) * 4) = acc[g];
+        }
+        lds_barrier();
+        if (kg > 0) return;
+        for (int k = 1; k < KG; ++k)
+#pragma unroll
+            for (int g = 0; g < BG; ++g)
+                acc[g] += *reinterpret_cast<const floatx4_t*>(red + ((((k - 1) * R + rw) * 64 + (int)lane) * BG + g) * 4);
     }
     if (!active) return;
 
@@ -399,13 +448,16 @@ hipError_t gemm_b(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStrea
 }  // namespace
 
 size_t gemm_lds_bytes(int waves, int batch) {
-    (void)waves;
     const int bg = batch > 16 ? 2 : 1;
-    return (size_t)2 * 16 * bg * kRowBytes;
+    const int rows = gemm_min_waves(batch), kgroups = std::max(1, waves / rows);
+    const size_t slabs = (size_t)2 * kgroups * 16 * bg * kRowBytes;
+    const size_t sums = (size_t)(kgroups - 1) * rows * 64 * bg * 4 * sizeof(float);
+    return std::max(slabs, sums);
 }
 
 hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
-    if (batch < 1 || batch > 32 || p.waves * 64 * kGemmXPieces < batch * 32) return hipErrorInvalidValue;
+    const int rows = gemm_min_waves(batch);
+    if (batch < 1 || batch > 32 || p.waves % rows != 0 || a.rows_per_block != rows) return hipErrorInvalidValue;
     if (batch > 16) return p.raw ? gemm_b<2, true>(a, batch, p, stream) : gemm_b<2, false>(a, batch, p, stream);
     return p.raw ? gemm_b<1, true>(a, batch, p, stream) : gemm_b<1, false>(a, batch, p, stream);
 }

@@ -33,6 +33,7 @@ struct GemvGroupArgs {
     GemvArgs m[kMaxGroup];
     int32_t tr_start[kMaxGroup + 1];
     int32_t count;
+    int32_t rows_per_block;   // MFMA: tile rows per block (waves = rows x K groups)
 };
 
 // How one GEMV launch runs: the launch shape (waves per block, blocks =
@@ -133,6 +134,9 @@ constexpr int kGemmMaxThreads = 512;
 // the edge-handling (GENERIC) MFMA variants, whose element-wise loads need
 // more registers, take at most 4 waves per block (enough for 32 batch rows)
 constexpr int kGemmMaxThreadsGeneric = 256;
+// the default MFMA launch aims at this many waves per CU (rows x K groups x
+// splits over the grid)
+constexpr int kGemmWavesPerCu = 4;
 constexpr int kGemmMaxSplits = 16;
 constexpr int kGemmXPieces = 4;
 constexpr int gemm_min_waves(int batch) { return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces); }

@@ -71,9 +71,11 @@ def mfma_min_waves(batch: int) -> int:
 
 
 def grid_rows(output_rows: int, waves: int, batch: int = 1, float32_activations: bool = False) -> int:
-    """Blocks per K split: one per tile row, or per `waves` tile rows (MFMA)."""
+    """Blocks per K split: one per tile row, or (MFMA) one per
+    mfma_min_waves(batch) tile rows, whatever the waves per block (a block's
+    waves are its tile rows times its K groups)."""
     tr = tile_rows(output_rows)
-    return -(-tr // waves) if uses_mfma(batch, float32_activations) else tr
+    return -(-tr // mfma_min_waves(batch)) if uses_mfma(batch, float32_activations) else tr
 
 
 def configuration(waves: int, k_splits: int, output_rows: int, batch: int = 1,
@@ -117,6 +119,8 @@ def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int =
     lo = WAVE_SIZE * (mfma_min_waves(batch) if uses_mfma(batch, float32_activations) else 1)
     if tpb % WAVE_SIZE or not lo <= tpb <= hi:
         raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [{lo}, {hi}]")
+    if uses_mfma(batch, float32_activations) and (tpb // WAVE_SIZE) % mfma_min_waves(batch):
+        raise ValueError(f"the MFMA kernel takes a multiple of {mfma_min_waves(batch)} waves per block at batch {batch}")
     rows = grid_rows(output_rows, tpb // WAVE_SIZE, batch, float32_activations)
     if blocks <= 0 or blocks % rows:
         raise ValueError(f"blocks {blocks} must be a positive multiple of {rows}")
@@ -135,7 +139,7 @@ def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_a
     splits = [s for s in K_SPLIT_CANDIDATES if s <= min(tc, max_k_splits(batch, float32_activations))]
     out = []
     for waves in WAVES_PER_BLOCK_CANDIDATES:
-        if not lo <= waves <= mw:
+        if not lo <= waves <= mw or (mfma and waves % lo):
             continue
         for s in splits:
             if mfma or waves <= -(-tc // s):

@@ -94,14 +94,21 @@ def test_encoder_rejects_bad_shapes():
 
 def test_launch_candidates_respect_each_kernels_limits():
     """BF16 batches of 5+ rows take the batched MFMA kernel (at most 8 waves
-    per block and 16 K splits); FP32 x and smaller batches the dot2 kernel."""
+    per block, a multiple of batch / 8, and 16 K splits); FP32 x and smaller
+    batches the dot2 kernel."""
     from se12_amd.launch import (candidate_configurations, configuration, max_waves_per_block, uses_mfma,
                                  waves_and_splits)
 
     assert not uses_mfma(4) and uses_mfma(5) and not uses_mfma(32, float32_activations=True)
-    # MFMA blocks count row blocks of `waves` tile rows and need batch / 8 waves
-    assert configuration(4, 3, 2304, batch=8).blocks.value == 36 * 3
+    # MFMA blocks count row blocks of batch / 8 tile rows (rounded up); a
+    # block's waves are those rows times K groups
+    assert configuration(4, 3, 2304, batch=8).blocks.value == 144 * 3
+    assert configuration(4, 3, 2304, batch=32).blocks.value == 36 * 3
+    assert configuration(8, 1, 2304, batch=17).blocks.value == 48
     assert configuration(4, 3, 2304, batch=4).blocks.value == 144 * 3
+    with pytest.raises(ValueError, match="multiple of 3"):
+        waves_and_splits(configuration(4, 1, 2304, batch=17), 2304, batch=17)
+    assert all(waves_and_splits(c, 2304, batch=24, k=9216)[0] % 3 == 0 for c in candidate_configurations(2304, 9216, batch=24))
     assert min(waves_and_splits(c, 2304, batch=32, k=9216)[0] for c in candidate_configurations(2304, 9216, batch=32)) == 4
     assert max_waves_per_block(1) == 16 and max_waves_per_block(6) == 8
     for batch, f32, max_s in ((1, False, 36), (6, False, 16), (32, False, 16), (6, True, 36)):

@@ -344,10 +344,14 @@ static int64_t gemm_row_blocks(se12_handle* const* hs, int32_t count, int32_t ro
     return rb;
 }
 
-// Default launch of the MFMA kernel: rows per block fixed by the batch (the
-// fewest waves whose threads load an x slab, batch / 8 rounded up), then K
-// groups and K splits for about kGemmWavesPerCu waves per CU, each wave
-// keeping 3 or more K tiles for the two-tile prefetch.
+// Default launch of the MFMA kernel, fitted to sweeps of (K groups, K splits)
+// on MI355X over the Gemma-2 2B/9B shapes at B = 5..32: rows per block fixed
+// by the batch (the fewest waves whose threads load an x slab, batch / 8
+// rounded up); then about 3.4 waves per CU in all (tile rows x K groups x
+// splits: 864 on 256 CUs), K groups first (up to 6 with one row per block,
+// 2 with more; at least 2 K tiles per wave), splits for the rest (at least 3
+// K tiles per wave). 14336x3584: 1 x 1; 2304x9216: 6 x 1 at B <= 8, 2 x 3 at
+// B = 9..24; 4096x2304: 3 x 1 at B <= 8.
 static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, bool generic, int32_t* waves_out,
                                 int32_t* splits_out) {
     const se12_handle* h0 = hs[0];
@@ -355,14 +359,15 @@ static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t b
     for (int32_t i = 0; i < count; ++i) tr += hs[i]->TR;
     const int64_t cus = std::max<int32_t>(1, h0->cu_count);
     const int64_t rows = gemm_min_waves(batch);
-    const int64_t target = kGemmWavesPerCu * cus;  // waves = tile rows x K groups x splits
+    const int64_t target = 27 * cus / 8;
+    const int64_t m = std::max<int64_t>(1, (2 * target + tr) / (2 * tr));  // K groups x splits
     const int64_t max_waves = (generic ? kGemmMaxThreadsGeneric : kGemmMaxThreads) / 64;
-    const int64_t kg_max = std::max<int64_t>(1, std::min<int64_t>(max_waves / rows, h0->TC / 3));
-    const int64_t kg = std::max<int64_t>(1, std::min<int64_t>(kg_max, ceil_div(target, tr)));
+    const int64_t kg_max = std::max<int64_t>(1, std::min<int64_t>({max_waves / rows, rows == 1 ? 6 : 2, h0->TC / 2}));
+    const int64_t kg = std::min(m, kg_max);
     const int64_t cap = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kGemmMaxSplits, (int64_t)h0->s_cap,
                                                                h0->TC / (3 * kg)}));
     *waves_out = (int32_t)(rows * kg);
-    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, target / (tr * kg)));
+    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, (2 * m + kg) / (2 * kg)));
 }
 
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {

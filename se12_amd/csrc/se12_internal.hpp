@@ -134,9 +134,7 @@ constexpr int kGemmMaxThreads = 512;
 // the edge-handling (GENERIC) MFMA variants, whose element-wise loads need
 // more registers, take at most 4 waves per block (enough for 32 batch rows)
 constexpr int kGemmMaxThreadsGeneric = 256;
-// the default MFMA launch aims at this many waves per CU (rows x K groups x
-// splits over the grid)
-constexpr int kGemmWavesPerCu = 4;
+
 constexpr int kGemmMaxSplits = 16;
 constexpr int kGemmXPieces = 4;
 constexpr int gemm_min_waves(int batch) { return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces); }

@@ -158,6 +158,36 @@ int se12_gemv(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch,
 int se12_gemv_grouped(se12_handle* const* handles, int32_t count, const void* x_dev, int32_t x_dtype,
                       int32_t batch, float* const* y_dev, const se12_launch* launch, void* stream);
 
+/* Products with a decoder step fused into their tail (no reference
+ * counterpart: the reference leaves everything but the linear layers to the
+ * framework; these let a decode step skip the separate launches of
+ * se12_step_gelu_mul and se12_step_rmsnorm, with the same arithmetic).
+ *
+ * se12_gemv_gelu_mul: the grouped product of two handles with the same rows
+ * (gate, up), y[0] and y[1] FP32 [batch, rows] as se12_gemv_grouped, then
+ * out[b, n] = bf16(gelu_tanh(bf16(y[0][b, n])) * bf16(y[1][b, n])), BF16
+ * [batch, rows].
+ *
+ * se12_gemv_rmsnorm: y = W x as se12_gemv, then for each batch row
+ * residual = bf16(residual + norm(bf16(y)) * (1 + w1)),
+ * out = norm(residual) * (1 + w2), norm(t) = t * rsqrt(mean(t^2) + eps) in
+ * FP32; residual and out BF16 [batch, rows], w1 and w2 BF16 [rows],
+ * rows <= 8192.
+ *
+ * Where the product runs the dot2 kernel (batch rows per launch <= 4, or FP32
+ * x) and, for the norm, rows % 4 == 0, y, w1, w2, residual and out are
+ * 8-byte aligned and the row fits a block's LDS (10 bytes per row of W;
+ * gfx950 blocks take up to 160 KiB), the block completing the inputs of the
+ * step runs it;
+ * otherwise (MFMA launches for BF16 x with batch >= 5, longer rows) the
+ * separate step kernel follows the product. Same stream, allocation and
+ * ordering rules as se12_gemv. */
+int se12_gemv_gelu_mul(se12_handle* const* gate_up, const void* x_dev, int32_t x_dtype, int32_t batch,
+                       float* const* y_dev, uint16_t* out_dev, const se12_launch* launch, void* stream);
+int se12_gemv_rmsnorm(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch, float* y_dev,
+                      const uint16_t* w1_dev, const uint16_t* w2_dev, uint16_t* residual_dev, uint16_t* out_dev,
+                      float eps, const se12_launch* launch, void* stream);
+
 /* Decodes the whole matrix to row-major BF16 bits [rows, cols] (cropped).
  * Replaces the lws_se12_decode launch plus the device untile/crop of
  * CudaSe12WeightDecoder (lws/adapters/cuda/se12_decoder.py:58-76,147-185;

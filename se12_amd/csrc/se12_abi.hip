@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "se12_gfx950.h"
+#include "se12_step.h"
 #include "se12_device.hpp"
 #include "se12_internal.hpp"
 
@@ -39,6 +40,7 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
@@ -61,6 +63,7 @@ struct DeviceScope {
 };
 
 constexpr int32_t kMaxSplits = 64;
+constexpr int32_t kStepNormMaxRows = 8192;  // se12_step_rmsnorm's hidden limit
 constexpr size_t kSideBytes = 64;  // one side record per tile (16 dwords)
 
 }  // namespace
@@ -138,9 +141,11 @@ static int bind_common(se12_handle* h, int64_t rows, int64_t cols, int32_t max_b
         if (max_batch >= kGemmMinBatch) pe = std::max<int64_t>(pe, (int64_t)std::min(h->s_cap, kGemmMaxSplits) * max_batch);
         h->partial_elems = pe * h->Np;
         SE12_HIP(hipMalloc(&h->partial, (size_t)h->partial_elems * sizeof(float)));
-        SE12_HIP(hipMalloc(&h->counters, (size_t)h->TR * sizeof(int32_t)));
-        SE12_HIP(hipMemset(h->counters, 0, (size_t)h->TR * sizeof(int32_t)));
     }
+    // arrival counters: split-K per tile row and the fused step tails'
+    const size_t counter_bytes = (size_t)gemv_counter_count(h->TR) * sizeof(int32_t);
+    SE12_HIP(hipMalloc(&h->counters, counter_bytes));
+    SE12_HIP(hipMemset(h->counters, 0, counter_bytes));
     return SE12_OK;
 }
 
@@ -425,7 +430,8 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped): one MFMA
 // launch for all rows, or one dot2 launch per 4 rows.
 static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, const void* x, int32_t x_dtype,
-                      int32_t batch, float* const* ys, const se12_launch* launch, void* stream) {
+                      int32_t batch, float* const* ys, const se12_launch* launch, void* stream,
+                      const GemvEpilogue* epi = nullptr) {
     if (count < 1 || count > kMaxGroup) return fail(SE12_E_INVALID, "%s: %d matrices, expected 1..%d", fn, count, kMaxGroup);
     if (!x) return fail(SE12_E_INVALID, "%s: NULL x", fn);
     if (x_dtype != SE12_X_BF16 && x_dtype != SE12_X_F32) return fail(SE12_E_INVALID, "%s: unknown x_dtype %d", fn, x_dtype);
@@ -491,6 +497,12 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             if ((int64_t)splits * b_first * hs[i]->Np > hs[i]->partial_elems)
                 return fail(SE12_E_CAPACITY, "%s: %d K splits at batch %d exceed handle %d's split-K workspace", fn,
                             splits, batch, i);
+    // the step tail runs in the dot2 kernel when its row fits the block's LDS
+    const bool fuse_epi =
+        epi && !mfma &&
+        (epi->kind != kEpiRmsNorm ||
+         ((int64_t)(gemv_norm_lds_bytes(h0->N) + kLutBytes) <= h0->lds_per_block && h0->N % 4 == 0 &&
+          aligned8(ys[0]) && aligned8(epi->w1) && aligned8(epi->w2) && aligned8(epi->residual) && aligned8(epi->out)));
     for (int32_t b0 = 0; b0 < batch; b0 += step) {
         const int32_t bl = std::min<int32_t>(step, batch - b0);
         GemvGroupArgs g{};
@@ -522,13 +534,27 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         }
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);
-        const GemvPlan p = mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
-                                : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
+        GemvPlan p = mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
+                          : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
+        if (fuse_epi) {
+            g.epi = *epi;
+            g.epi.out += (size_t)b0 * h0->N;
+            if (g.epi.residual) g.epi.residual += (size_t)b0 * h0->N;
+            if (epi->kind == kEpiRmsNorm) p.lds = std::max(p.lds, gemv_norm_lds_bytes(h0->N));
+        }
         if ((int64_t)(p.lds + kLutBytes) > h0->lds_per_block)
             return fail(SE12_E_CAPACITY, "%s: launch needs %zu bytes of LDS, the device allows %lld", fn, p.lds,
                         (long long)h0->lds_per_block);
         hipError_t e = mfma ? launch_gemm(g, bl, p, st) : launch_gemv(g, p, st);
         if (e != hipSuccess) return fail(SE12_E_HIP, "%s launch: %s", fn, hipGetErrorString(e));
+    }
+    if (epi && !fuse_epi) {
+        // the step runs as its own kernel after the product
+        const int rc = epi->kind == kEpiGeluMul
+                           ? se12_step_gelu_mul(ys[0], ys[1], SE12_STEP_F32, h0->N, epi->out, batch, (int32_t)h0->N, st)
+                           : se12_step_rmsnorm(ys[0], SE12_STEP_F32, h0->N, epi->w1, epi->residual, epi->w2, epi->out,
+                                               batch, (int32_t)h0->N, epi->eps, 0.0f, 1, st);
+        if (rc != SE12_STEP_OK) return fail(SE12_E_HIP, "%s step: %s", fn, se12_step_last_error());
     }
     return SE12_OK;
 }
@@ -546,6 +572,40 @@ int se12_gemv_grouped(se12_handle* const* handles, int32_t count, const void* x,
                       float* const* y, const se12_launch* launch, void* stream) {
     if (!handles || !y) return fail(SE12_E_INVALID, "se12_gemv_grouped: NULL handles or y");
     return gemv_group("se12_gemv_grouped", handles, count, x, x_dtype, batch, y, launch, stream);
+}
+
+int se12_gemv_gelu_mul(se12_handle* const* gate_up, const void* x, int32_t x_dtype, int32_t batch, float* const* y,
+                       uint16_t* out, const se12_launch* launch, void* stream) {
+    if (!gate_up || !y || !out) return fail(SE12_E_INVALID, "se12_gemv_gelu_mul: NULL handles, y or out");
+    if (!gate_up[0] || !gate_up[1]) return fail(SE12_E_INVALID, "se12_gemv_gelu_mul: NULL handle");
+    if (gate_up[0]->N != gate_up[1]->N)
+        return fail(SE12_E_INVALID, "se12_gemv_gelu_mul: gate and up have %lld and %lld rows",
+                    (long long)gate_up[0]->N, (long long)gate_up[1]->N);
+    if (gate_up[0]->N > INT32_MAX) return fail(SE12_E_INVALID, "se12_gemv_gelu_mul: too many rows");
+    GemvEpilogue e{};
+    e.kind = kEpiGeluMul;
+    e.out = out;
+    return gemv_group("se12_gemv_gelu_mul", gate_up, 2, x, x_dtype, batch, y, launch, stream, &e);
+}
+
+int se12_gemv_rmsnorm(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, const uint16_t* w1,
+                      const uint16_t* w2, uint16_t* residual, uint16_t* out, float eps, const se12_launch* launch,
+                      void* stream) {
+    if (!h || !y || !w1 || !w2 || !residual || !out)
+        return fail(SE12_E_INVALID, "se12_gemv_rmsnorm: NULL handle, y, weights, residual or out");
+    if (h->N > kStepNormMaxRows)
+        return fail(SE12_E_INVALID, "se12_gemv_rmsnorm: %lld rows, the norm takes at most %d", (long long)h->N,
+                    kStepNormMaxRows);
+    GemvEpilogue e{};
+    e.kind = kEpiRmsNorm;
+    e.eps = eps;
+    e.w1 = w1;
+    e.w2 = w2;
+    e.residual = residual;
+    e.out = out;
+    se12_handle* hs[1] = {h};
+    float* ys[1] = {y};
+    return gemv_group("se12_gemv_rmsnorm", hs, 1, x, x_dtype, batch, ys, launch, stream, &e);
 }
 
 static DecodeArgs decode_args(const se12_handle* h, uint16_t* out) {

@@ -31,11 +31,17 @@
 // ascending split order. The counter is reset by that block, so no memset is
 // needed between launches (graph-capture friendly).
 //
+// Optional decode-step tail (GemvEpilogue): the final y is then stored with
+// device-scope stores and the block completing a gate/up tile row pair, or
+// the whole matrix, applies the MLP gate or the residual RMSNorm in place of
+// a separate launch.
+//
 // FAST variants need K % 256 == 0, 16-byte aligned BF16 x rows, and for the
 // raw twin N % 16 == 0 and an aligned W; every other case runs the GENERIC
 // variants (element loads guarded by the matrix edges, weights past K zeroed).
 #include "se12_device.hpp"
 #include "se12_internal.hpp"
+#include "se12_step_math.hpp"
 
 namespace se12 {
 
@@ -68,6 +74,128 @@ __device__ __forceinline__ void load_x(XTile<B, XF32>& x, const GemvArgs& a, int
                 x.v[b][q] = lo | (hi << 16);
             }
         }
+    }
+}
+
+// device-scope load / store of FP32 results that another block of the same
+// launch wrote / will read
+__device__ __forceinline__ float load_dev(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The decode-step work of GemvEpilogue, run by the block that has just
+// written the final y of tile row `tr` (device-scope stores): it counts its
+// arrival, and the block completing a tile row pair (kEpiGeluMul) or the
+// matrix (kEpiRmsNorm) reads the results back and finishes the step. The
+// arithmetic is that of se12_step_gelu_mul / se12_step_rmsnorm mode 1; the
+// norm's sum of squares runs over this block's threads.
+template <int B>
+__device__ void gemv_epilogue(const GemvGroupArgs& ga, int tr, float* lds) {
+    using namespace se12step;
+    __shared__ int doer;
+    const GemvEpilogue& e = ga.epi;
+    const GemvArgs& a0 = ga.m[0];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const bool pair = e.kind == kEpiGeluMul;
+    int32_t* cnt = a0.counters + (pair ? (int64_t)a0.TR + tr : 2 * (int64_t)a0.TR);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this block's y stores are complete
+    __syncthreads();
+    if (tid == 0) {
+        const int old = __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        doer = old == (pair ? 1 : a0.TR - 1);
+    }
+    __syncthreads();
+    if (!doer) return;
+    if (tid == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t N = a0.N;
+    if (pair) {
+        if (tid < 16 * B) {
+            const int64_t o = (int64_t)(tid >> 4) * N + (int64_t)tr * kTileRows + (tid & 15);
+            if ((int64_t)tr * kTileRows + (tid & 15) < N)
+                e.out[o] = gelu_mul_bf16(round_bf16(load_dev(a0.y + o)), round_bf16(load_dev(ga.m[1].y + o)));
+        }
+        return;
+    }
+    // RMSNorm of each batch row, four elements per step (the host asks for
+    // rows % 4 == 0 and 8-byte aligned tensors): the row rounded to BF16, its
+    // weights and residual are staged in LDS with every load of a pass
+    // issued first; the passes then run out of LDS
+    const int n = (int)N, n4 = n >> 2;
+    float4* buf = reinterpret_cast<float4*>(lds);
+    uint2* w1s = reinterpret_cast<uint2*>(lds + n);
+    uint2* rs = w1s + n4;
+    uint2* w2s = rs + n4;
+    float* sh = reinterpret_cast<float*>(reinterpret_cast<char*>(lds) + ((10 * (size_t)n + 15) & ~(size_t)15));
+    const uint2* w1g = reinterpret_cast<const uint2*>(e.w1);
+    const uint2* w2g = reinterpret_cast<const uint2*>(e.w2);
+    for (int b = 0; b < B; ++b) {
+        const uint64_t* yr = reinterpret_cast<const uint64_t*>(a0.y + (int64_t)b * N);
+        uint2* res = reinterpret_cast<uint2*>(e.residual + (int64_t)b * N);
+        float ss = 0.0f;
+        for (int g0 = 0; g0 < n4; g0 += 2 * nt) {
+            uint64_t y01[2], y23[2];
+            uint2 c1[2], c2[2], c3[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int g = g0 + tid + k * nt;
+                const int gc = g < n4 ? g : n4 - 1;  // clamped: every load is issued unconditionally
+                y01[k] = __hip_atomic_load(yr + 2 * gc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                y23[k] = __hip_atomic_load(yr + 2 * gc + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                c1[k] = w1g[gc];
+                c2[k] = res[gc];
+                c3[k] = w2g[gc];
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int g = g0 + tid + k * nt;
+                if (g < n4) {
+                    const float4 x = make_float4(round_bf16(__uint_as_float((uint32_t)y01[k])),
+                                                 round_bf16(__uint_as_float((uint32_t)(y01[k] >> 32))),
+                                                 round_bf16(__uint_as_float((uint32_t)y23[k])),
+                                                 round_bf16(__uint_as_float((uint32_t)(y23[k] >> 32))));
+                    buf[g] = x;
+                    w1s[g] = c1[k];
+                    rs[g] = c2[k];
+                    w2s[g] = c3[k];
+                    ss += x.x * x.x;
+                    ss += x.y * x.y;
+                    ss += x.z * x.z;
+                    ss += x.w * x.w;
+                }
+            }
+        }
+        const float inv = rms_inv(block_sum(ss, sh), n, e.eps);
+        float ss2 = 0.0f;
+        auto lo = [](uint32_t u) { return bf16_to_f(u & 0xFFFFu); };
+        auto hi = [](uint32_t u) { return bf16_to_f(u >> 16); };
+        for (int g = tid; g < n4; g += nt) {
+            const float4 x = buf[g];
+            const uint2 w = w1s[g], r0 = rs[g];
+            float4 r;
+            r.x = round_bf16(lo(r0.x) + round_bf16(rms_scale(x.x, inv, lo(w.x))));
+            r.y = round_bf16(hi(r0.x) + round_bf16(rms_scale(x.y, inv, hi(w.x))));
+            r.z = round_bf16(lo(r0.y) + round_bf16(rms_scale(x.z, inv, lo(w.y))));
+            r.w = round_bf16(hi(r0.y) + round_bf16(rms_scale(x.w, inv, hi(w.y))));
+            buf[g] = r;
+            ss2 += r.x * r.x;
+            ss2 += r.y * r.y;
+            ss2 += r.z * r.z;
+            ss2 += r.w * r.w;
+        }
+        const float inv2 = rms_inv(block_sum(ss2, sh), n, e.eps);
+        uint2* out = reinterpret_cast<uint2*>(e.out + (int64_t)b * N);
+        for (int g = tid; g < n4; g += nt) {
+            const float4 r = buf[g];
+            const uint2 w = w2s[g];
+            auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
+            res[g] = make_uint2(pack(r.x, r.y), pack(r.z, r.w));
+            out[g] = make_uint2(pack(rms_scale(r.x, inv2, lo(w.x)), rms_scale(r.y, inv2, hi(w.x))),
+                                pack(rms_scale(r.z, inv2, lo(w.y)), rms_scale(r.w, inv2, hi(w.y))));
+        }
+        __syncthreads();  // the next row reuses the LDS
     }
 }
 
@@ -294,35 +422,37 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
     if (tid < 16 * B) {
         for (int ww = 0; ww < W; ++ww) v += red[(ww * B + b) * 16 + rr];
     }
-    if (S == 1) {
-        if (tid < 16 * B && n < a.N) a.y[(int64_t)b * a.N + n] = v;
-        return;
-    }
-    // Cross-block reduction without cache-wide maintenance: the partials are
-    // written with device-scope stores, each thread waits for its stores to
-    // complete before the block's arrival is counted, and the last block
-    // reads them back with device-scope loads. (A __threadfence() here would
-    // write back and invalidate the whole L2 of the XCD for every block.)
-    if (tid < 16 * B)
-        __hip_atomic_store(&a.partial[((int64_t)s * B + b) * a.Np + n], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    int* flag = reinterpret_cast<int*>(red);
-    if (tid == 0) {
-        const int old = __hip_atomic_fetch_add(&a.counters[tr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = (old == S - 1) ? 1 : 0;
-    }
-    __syncthreads();
-    if (*flag) {
+    const bool epi = ga.epi.kind != kEpiNone;
+    if (S > 1) {
+        // Cross-block reduction without cache-wide maintenance: the partials
+        // are written with device-scope stores, each thread waits for its
+        // stores to complete before the block's arrival is counted, and the
+        // last block reads them back with device-scope loads. (A
+        // __threadfence() here would write back and invalidate the whole L2
+        // of the XCD for every block.)
+        if (tid < 16 * B) store_dev(&a.partial[((int64_t)s * B + b) * a.Np + n], v);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        int* flag = reinterpret_cast<int*>(red);
+        if (tid == 0) {
+            const int old = __hip_atomic_fetch_add(&a.counters[tr], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = (old == S - 1) ? 1 : 0;
+        }
+        __syncthreads();
+        if (!*flag) return;
         if (tid < 16 * B) {
-            float sum = 0.0f;
-            for (int ss = 0; ss < S; ++ss)
-                sum += __hip_atomic_load(&a.partial[((int64_t)ss * B + b) * a.Np + n], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            if (n < a.N) a.y[(int64_t)b * a.N + n] = sum;
+            v = 0.0f;
+            for (int ss = 0; ss < S; ++ss) v += load_dev(&a.partial[((int64_t)ss * B + b) * a.Np + n]);
         }
         if (tid == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if (tid < 16 * B && n < a.N) {
+        if (epi)
+            store_dev(&a.y[(int64_t)b * a.N + n], v);  // read back by the block that runs the epilogue
+        else
+            a.y[(int64_t)b * a.N + n] = v;
+    }
+    if (epi) gemv_epilogue<B>(ga, tr, red);
 }
 
 namespace {

@@ -29,12 +29,43 @@ struct GemvArgs {
 // grid row tr_start[i] (tr_start[count] = the grid's rows).
 constexpr int kMaxGroup = 4;
 
+// Decode-step work done at the tail of a dot2 GEMV launch by the block that
+// completes its inputs (arrival counters after the matrix's split-K
+// counters: [TR, 2 TR) per tile row pair, [2 TR] for the whole matrix):
+//   kEpiGeluMul  two matrices of one N (gate, up): the block completing a
+//                tile row pair writes out = bf16(gelu_tanh(bf16(y0)) * bf16(y1))
+//                for its 16 rows;
+//   kEpiRmsNorm  one matrix with rows % 4 == 0 and 8-byte aligned y, w1,
+//                w2, residual and out: the block completing the last tile
+//                row runs, per batch row, residual = bf16(residual +
+//                norm(bf16(y), w1)), out = norm(residual, w2).
+constexpr int kEpiNone = 0;
+constexpr int kEpiGeluMul = 1;
+constexpr int kEpiRmsNorm = 2;
+
+struct GemvEpilogue {
+    int32_t kind;
+    float eps;
+    const uint16_t* w1;       // [N] BF16
+    const uint16_t* w2;       // [N] BF16
+    uint16_t* residual;       // [B, N] BF16
+    uint16_t* out;            // [B, N] BF16
+};
+
 struct GemvGroupArgs {
     GemvArgs m[kMaxGroup];
     int32_t tr_start[kMaxGroup + 1];
     int32_t count;
     int32_t rows_per_block;   // MFMA: tile rows per block (waves = rows x K groups)
+    GemvEpilogue epi;         // dot2 launches only
 };
+
+// arrival counters a handle holds: split-K per tile row, the epilogues' per
+// tile row pair and per matrix
+constexpr int64_t gemv_counter_count(int64_t tr) { return 2 * tr + 1; }
+// dynamic LDS of the kEpiRmsNorm tail: the row in FP32, w1 / residual / w2
+// as BF16, 32 floats for the block sums
+constexpr size_t gemv_norm_lds_bytes(int64_t n) { return (size_t)n * 10 + 32 * sizeof(float); }
 
 // How one GEMV launch runs: the launch shape (waves per block, blocks =
 // tile rows x splits) fixes the results; the variant (tiles per round `g`,

@@ -34,19 +34,9 @@
 #include <stdint.h>
 
 #include "se12_step.h"
+#include "se12_step_math.hpp"
 
 namespace se12step {
-
-__device__ __forceinline__ float bf16_to_f(uint32_t b) { return __uint_as_float(b << 16); }
-
-// float -> BF16 bits, round to nearest even (NaN stays a quiet NaN)
-__device__ __forceinline__ uint16_t f_to_bf16(float f) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)((u >> 16) | 0x40u);
-    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
-
-__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f(f_to_bf16(f)); }
 
 // element i of an FP32 or BF16 tensor, rounded to BF16 (the framework's
 // `.to(torch.bfloat16)` of a product output)
@@ -70,33 +60,6 @@ __device__ __forceinline__ void unpack8(const uint4 r, float* v) {
         v[2 * i] = __uint_as_float(w[i] << 16);
         v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
     }
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-// block-wide sum; `sh` holds >= 17 floats; every thread gets the result
-__device__ float block_sum(float v, float* sh) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    if ((threadIdx.x & 63) == 0) sh[w] = v;
-    __syncthreads();
-    if (w == 0) {
-        float t = (int)threadIdx.x < waves ? sh[threadIdx.x] : 0.0f;
-        t = wave_sum(t);
-        if (threadIdx.x == 0) sh[16] = t;
-    }
-    __syncthreads();
-    const float r = sh[16];
-    __syncthreads();
-    return r;
 }
 
 // (value, index) with the larger value, the smaller index on a tie
@@ -149,14 +112,14 @@ __global__ __launch_bounds__(kNormMaxThreads) void rmsnorm_kernel(NormArgs a) {
             if (a.in_scale != 0.0f) x[k] = round_bf16(x[k] * a.in_scale);  // scaled embedding row
         if (t + k * nt < a.hidden) ss += x[k] * x[k];
     }
-    const float inv = rsqrtf(block_sum(ss, sh) / (float)a.hidden + a.eps);
+    const float inv = rms_inv(block_sum(ss, sh), a.hidden, a.eps);
     if constexpr (MODE == 0) {
 #pragma unroll
         for (int k = 0; k < kNormPer; ++k) {
             const int i = t + k * nt;
             if (i < a.hidden) {
                 if (a.residual) a.residual[rbase + i] = f_to_bf16(x[k]);
-                a.out[rbase + i] = f_to_bf16((x[k] * inv) * (1.0f + w1[k]));
+                a.out[rbase + i] = f_to_bf16(rms_scale(x[k], inv, w1[k]));
             }
         }
         return;
@@ -165,17 +128,17 @@ __global__ __launch_bounds__(kNormMaxThreads) void rmsnorm_kernel(NormArgs a) {
     float ss2 = 0.0f;
 #pragma unroll
     for (int k = 0; k < kNormPer; ++k) {
-        const float n1 = round_bf16((x[k] * inv) * (1.0f + w1[k]));
+        const float n1 = round_bf16(rms_scale(x[k], inv, w1[k]));
         res[k] = round_bf16(res[k] + n1);
         if (t + k * nt < a.hidden) ss2 += res[k] * res[k];
     }
-    const float inv2 = rsqrtf(block_sum(ss2, sh) / (float)a.hidden + a.eps);
+    const float inv2 = rms_inv(block_sum(ss2, sh), a.hidden, a.eps);
 #pragma unroll
     for (int k = 0; k < kNormPer; ++k) {
         const int i = t + k * nt;
         if (i < a.hidden) {
             a.residual[rbase + i] = f_to_bf16(res[k]);
-            a.out[rbase + i] = f_to_bf16((res[k] * inv2) * (1.0f + w2[k]));
+            a.out[rbase + i] = f_to_bf16(rms_scale(res[k], inv2, w2[k]));
         }
     }
 }
@@ -222,7 +185,12 @@ __device__ __forceinline__ int window_lo(int p, int window) {
     return window > 0 ? (p - window + 1 > 0 ? p - window + 1 : 0) : 0;
 }
 
-template <int G>
+// Makes the wave wait for a loaded value here: issued before a branch on the
+// position, loads would otherwise be sunk past it and wait for it.
+__device__ __forceinline__ void pin(float v) { asm volatile("" ::"v"(v)); }
+__device__ __forceinline__ void pin(const uint4& v) { asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w)); }
+
+template <int G, int DT>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     __shared__ float qk[(G + 1) * kMaxHeadDim];   // rotated q of the G heads, then k
     __shared__ float red[4 * G * kChunk];         // per wave: G x 64 partial dot products
@@ -230,27 +198,57 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     const int kvb = blockIdx.x;                    // b * kvh + kh
     const int b = kvb / a.kvh, kh = kvb % a.kvh;
     const int c = blockIdx.y, j0 = c * kChunk;
+    const int d = a.d, half = d / 2;
+    const int L = a.max_len;
+
+    // Every load whose address does not depend on the position goes out
+    // together with the position's: q, k and v of the new token (to BF16),
+    // the rotary frequency and the chunk of the key cache. Lane group
+    // pg = 8 consecutive positions read as one 16-byte load per head-dim
+    // element; the 32 slices es take every 32nd element.
     const int64_t p64 = *a.pos;
+    __builtin_amdgcn_sched_barrier(0);  // the position's load goes out first
+    float xq[G], xk = 0.0f, vv = 0.0f, fr = 0.0f;
+    const int tc = t < d ? t : d - 1;
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+        xq[h] = load_as_bf16<DT>(a.q, (int64_t)b * a.q_stride + (int64_t)(kh * G + h) * d + tc);
+    xk = load_as_bf16<DT>(a.k, (int64_t)b * a.kv_stride + (int64_t)kh * d + tc);
+    vv = load_as_bf16<DT>(a.v, (int64_t)b * a.kv_stride + (int64_t)kh * d + tc);
+    fr = a.inv_freq[tc % half];
+    const int pg = t & 7, es = t >> 3;
+    const int jg = j0 + 8 * pg;
+    const int jgl = jg + 8 <= L ? jg : L - 8;     // L % 8 == 0: a group is wholly in or out
+    const uint16_t* kb = a.kt + (int64_t)kvb * d * L + jgl;
+    uint4 raw[kMaxHeadDim / 32];
+#pragma unroll
+    for (int i = 0; i < kMaxHeadDim / 32; ++i) {
+        const int e = es + 32 * i;
+        raw[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)(e < d ? e : d - 1) * L);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) pin(xq[h]);
+    pin(xk);
+    pin(vv);
+    pin(fr);
+#pragma unroll
+    for (int i = 0; i < kMaxHeadDim / 32; ++i) pin(raw[i]);
+
     if (p64 < 0 || p64 >= a.max_len) return;
     const int p = (int)p64, lo = window_lo(p, a.window);
     if (j0 > p || j0 + kChunk <= lo) return;
-    const int d = a.d, half = d / 2;
-    const int L = a.max_len;
     const bool holds_p = p < j0 + kChunk;
 
-    // q (and k) to BF16, rotary embedding with the framework's roundings
+    // rotary embedding of q and k with the framework's roundings
     float y[G + 1];
-    float vv = 0.0f;
     if (t < d) {
 #pragma unroll
-        for (int h = 0; h < G; ++h)
-            qk[h * d + t] = load_as_bf16(a.q, a.dtype, (int64_t)b * a.q_stride + (int64_t)(kh * G + h) * d + t);
-        qk[G * d + t] = load_as_bf16(a.k, a.dtype, (int64_t)b * a.kv_stride + (int64_t)kh * d + t);
-        if (holds_p) vv = load_as_bf16(a.v, a.dtype, (int64_t)b * a.kv_stride + (int64_t)kh * d + t);
+        for (int h = 0; h < G; ++h) qk[h * d + t] = xq[h];
+        qk[G * d + t] = xk;
     }
     __syncthreads();
     if (t < d) {
-        const float freq = (float)p * a.inv_freq[t % half];
+        const float freq = (float)p * fr;
         const float cs = round_bf16(cosf(freq)), sn = round_bf16(sinf(freq));
 #pragma unroll
         for (int h = 0; h <= G; ++h) {
@@ -270,19 +268,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // dot products: lane group pg = 8 consecutive positions read as one
-    // 16-byte load per head-dim element; the 32 slices es take every 32nd
-    // element (8 loads per thread, all in flight together)
-    const int pg = t & 7, es = t >> 3;
-    const int jg = j0 + 8 * pg;
-    const int jgl = jg + 8 <= L ? jg : L - 8;     // L % 8 == 0: a group is wholly in or out
-    const uint16_t* kb = a.kt + (int64_t)kvb * d * L + jgl;
-    uint4 raw[kMaxHeadDim / 32];
-#pragma unroll
-    for (int i = 0; i < kMaxHeadDim / 32; ++i) {
-        const int e = es + 32 * i;
-        raw[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)(e < d ? e : d - 1) * L);
-    }
+    // dot products of the chunk's keys with the G rotated queries
     float acc[8][G];
 #pragma unroll
     for (int m = 0; m < 8; ++m)
@@ -358,7 +344,51 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
     const int c = blockIdx.y, j0 = c * kChunk;
     const int d = a.d, L = a.max_len;
     const int64_t obase = (int64_t)b * a.heads * d + (int64_t)kh * G * d;
+    const int64_t row0 = (int64_t)b * a.heads + kh * G;
+    const int64_t lp = (int64_t)a.chunks * kChunk;
+
+    // Every load whose address does not depend on the position goes out
+    // together with the position's: the statistics of the first 64 chunks of
+    // the wave's heads (lane = chunk), the chunk's scores and its 64 rows of
+    // V (lane group eg = 8 consecutive head-dim elements, one 16-byte load
+    // per position; 8 position slices ps take every 8th position).
     const int64_t p64 = *a.pos;
+    __builtin_amdgcn_sched_barrier(0);  // the position's load goes out first
+    constexpr int kHeadsPerWave = (G + 3) / 4;
+    constexpr int kScoresPerThread = (G * kChunk + kAttnThreads - 1) / kAttnThreads;
+    float sm[kHeadsPerWave], sl[kHeadsPerWave], sc[kScoresPerThread];
+    const int cl = lane < a.chunks ? lane : a.chunks - 1;
+#pragma unroll
+    for (int k = 0; k < kHeadsPerWave; ++k) {
+        const int h = w + 4 * k < G ? w + 4 * k : G - 1;
+        const float* st = a.stats + (row0 + h) * a.chunks * 2;
+        sm[k] = st[cl * 2];
+        sl[k] = st[cl * 2 + 1];
+    }
+#pragma unroll
+    for (int k = 0; k < kScoresPerThread; ++k) {
+        const int i = t + kAttnThreads * k < G * kChunk ? t + kAttnThreads * k : G * kChunk - 1;
+        sc[k] = a.scores[(row0 + i / kChunk) * lp + j0 + i % kChunk];
+    }
+    const int eg = t & 31, ps = t >> 5;
+    const int e0 = 8 * eg;
+    const uint16_t* vb = a.vc + ((int64_t)kvb * L + j0) * d + (e0 < d ? e0 : d - 8);
+    uint4 raw[kChunk / 8];
+#pragma unroll
+    for (int i = 0; i < kChunk / 8; ++i) {
+        const int jj = ps + 8 * i;
+        raw[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)(j0 + jj < L ? jj : L - 1 - j0) * d);
+    }
+#pragma unroll
+    for (int k = 0; k < kHeadsPerWave; ++k) {
+        pin(sm[k]);
+        pin(sl[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kScoresPerThread; ++k) pin(sc[k]);
+#pragma unroll
+    for (int i = 0; i < kChunk / 8; ++i) pin(raw[i]);
+
     if (p64 < 0 || p64 >= L) {  // no cache slot: zeros, no cache or counter touched
         if (c == 0)
             for (int i = t; i < G * d; i += kAttnThreads) a.out[obase + i] = 0;
@@ -367,15 +397,20 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
     const int p = (int)p64, lo = window_lo(p, a.window);
     const int c_lo = lo / kChunk, c_hi = p / kChunk;
     if (c < c_lo || c > c_hi) return;
-    const int64_t row0 = (int64_t)b * a.heads + kh * G;
     // global max and sum of each head over its chunks (one wave per head)
-    for (int h = w; h < G; h += kAttnThreads / 64) {
+#pragma unroll
+    for (int k = 0; k < kHeadsPerWave; ++k) {
+        const int h = w + 4 * k;
+        if (h >= G) break;
         const float* st = a.stats + (row0 + h) * a.chunks * 2;
-        float m = -INFINITY;
-        for (int cc = c_lo + lane; cc <= c_hi; cc += 64) m = fmaxf(m, st[cc * 2]);
+        const bool mine = lane >= c_lo && lane <= c_hi;
+        float m = mine ? sm[k] : -INFINITY;
+        for (int cc = lane + 64; cc <= c_hi; cc += 64)
+            if (cc >= c_lo) m = fmaxf(m, st[cc * 2]);
         m = wave_max(m);
-        float s = 0.0f;
-        for (int cc = c_lo + lane; cc <= c_hi; cc += 64) s += st[cc * 2 + 1] * expf(st[cc * 2] - m);
+        float s = mine ? sl[k] * expf(sm[k] - m) : 0.0f;
+        for (int cc = lane + 64; cc <= c_hi; cc += 64)
+            if (cc >= c_lo) s += st[cc * 2 + 1] * expf(st[cc * 2] - m);
         s = wave_sum(s);
         if (lane == 0) {
             ms[2 * h] = m;
@@ -383,27 +418,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-    const int64_t lp = (int64_t)a.chunks * kChunk;
-    for (int i = t; i < G * kChunk; i += kAttnThreads) {
-        const int h = i / kChunk, jj = i % kChunk, j = j0 + jj;
-        float pr = 0.0f;
-        if (j <= p && j >= lo) pr = round_bf16(expf(a.scores[(row0 + h) * lp + j] - ms[2 * h]) / ms[2 * h + 1]);
-        prob[i] = pr;
+#pragma unroll
+    for (int k = 0; k < kScoresPerThread; ++k) {
+        const int i = t + kAttnThreads * k;
+        if (i < G * kChunk) {
+            const int h = i / kChunk, j = j0 + i % kChunk;
+            prob[i] = (j <= p && j >= lo) ? round_bf16(expf(sc[k] - ms[2 * h]) / ms[2 * h + 1]) : 0.0f;
+        }
     }
     __syncthreads();
-    // weighted V: lane group eg = 8 consecutive head-dim elements (one 16-byte
-    // load per position), 8 position slices ps take every 8th position
+    // weighted V
     const int jlo = lo > j0 ? lo - j0 : 0;
     const int jhi = p - j0 < kChunk - 1 ? p - j0 : kChunk - 1;
-    const int eg = t & 31, ps = t >> 5;
-    const int e0 = 8 * eg;
-    const uint16_t* vb = a.vc + ((int64_t)kvb * L + j0) * d + (e0 < d ? e0 : d - 8);
-    uint4 raw[kChunk / 8];
-#pragma unroll
-    for (int i = 0; i < kChunk / 8; ++i) {
-        const int jj = ps + 8 * i;
-        raw[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)(jj <= jhi ? jj : jhi) * d);
-    }
     float acc[8][G];
 #pragma unroll
     for (int m = 0; m < 8; ++m)
@@ -475,12 +501,7 @@ __global__ void gelu_mul_kernel(const void* gate, const void* up, int64_t stride
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (int64_t)rows * cols) return;
     const int64_t r = i / cols, c = i - r * cols;
-    const float x = load_as_bf16<DT>(gate, r * stride + c);
-    const float u = load_as_bf16<DT>(up, r * stride + c);
-    // the tanh form of GELU: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
-    const float inner = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
-    const float g = round_bf16(0.5f * x * (1.0f + tanhf(inner)));
-    out[i] = f_to_bf16(g * u);
+    out[i] = gelu_mul_bf16(load_as_bf16<DT>(gate, r * stride + c), load_as_bf16<DT>(up, r * stride + c));
 }
 
 // ---------------------------------------------------------------------------
@@ -638,7 +659,10 @@ bool attn_shape_ok(int32_t batch, int32_t heads, int32_t kv_heads, int32_t head_
 template <int G>
 void launch_attention(const AttnArgs& a, int blocks_x, hipStream_t stream) {
     const dim3 grid(blocks_x, a.chunks);
-    hipLaunchKernelGGL(attn_scores_kernel<G>, grid, dim3(kAttnThreads), 0, stream, a);
+    if (a.dtype == SE12_STEP_F32)
+        hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_F32>), grid, dim3(kAttnThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_BF16>), grid, dim3(kAttnThreads), 0, stream, a);
     hipLaunchKernelGGL(attn_pv_kernel<G>, grid, dim3(kAttnThreads), 0, stream, a);
 }
 

@@ -226,7 +226,7 @@ class Gemma2Decoder:
 
     def __init__(self, weights: Gemma2Weights, backend: str, batch: int, max_len: int,
                  encoded: dict | None = None, max_batch: int = nat.MAX_BATCH, scratch: torch.Tensor | None = None,
-                 fused_step: bool = True):
+                 fused_step: bool = True, fused_tails: bool = True):
         s = weights.shape
         max_len = -(-max_len // 8) * 8          # the step kernels read the caches 8 positions at a time
         self.s, self.w, self.batch, self.max_len = s, weights, batch, max_len
@@ -247,6 +247,9 @@ class Gemma2Decoder:
         self.last_logits = torch.zeros((batch, s.vocab), dtype=torch.bfloat16, device=dev)
         self.graph = None
         self.fused_step = fused_step
+        # the library backends run the MLP gate and the residual norms in the
+        # tails of the products that feed them (se12_gemv_gelu_mul / _rmsnorm)
+        self.fused_tails = fused_step and fused_tails and backend != "bf16"
         if fused_step:
             f32 = backend != "bf16"
             shapes = projection_shapes(s)
@@ -390,13 +393,22 @@ class Gemma2Decoder:
                                        B, s.heads, s.kv_heads, s.head_dim, self.max_len, self.scaling, s.attn_softcap,
                                        0 if li % 2 else s.sliding_window, nat.ptr(self.attn_ws), self.attn_ws.numel(),
                                        st))
+            nxt = self.w.layers[li + 1]["input_norm"] if li + 1 < s.layers else self.w.final_norm
+            if self.fused_tails:
+                from .hip import multiply_gelu_mul
+
+                ks = self.be.layers[li]
+                ks["o"].multiply_rmsnorm(self.attn, lw["post_attn_norm"], lw["pre_ffw_norm"], self.x, self.h, s.eps,
+                                         y=self.o_out)
+                multiply_gelu_mul(ks["gate"], ks["up"], self.h, self.m, ys=self.gu)
+                ks["down"].multiply_rmsnorm(self.m, lw["post_ffw_norm"], nxt, self.x, self.h, s.eps, y=self.down_out)
+                continue
             o = self.be.single_raw(li, "o", self.attn, self.o_out)
             ck(lib.se12_step_rmsnorm(nat.ptr(o), dt(o), o.shape[1], nat.ptr(lw["post_attn_norm"]), nat.ptr(self.x),
                                      nat.ptr(lw["pre_ffw_norm"]), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
             (g, go, gs), (u, uo, _) = self.be.grouped_raw(li, ("gate", "up"), self.h, self.gu)
             ck(lib.se12_step_gelu_mul(at(g, go), at(u, uo), dt(g), gs, nat.ptr(self.m), B, s.intermediate, st))
             dn = self.be.single_raw(li, "down", self.m, self.down_out)
-            nxt = self.w.layers[li + 1]["input_norm"] if li + 1 < s.layers else self.w.final_norm
             ck(lib.se12_step_rmsnorm(nat.ptr(dn), dt(dn), dn.shape[1], nat.ptr(lw["post_ffw_norm"]), nat.ptr(self.x),
                                      nat.ptr(nxt), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
         lg = self.be.logits_raw(self.h, self.logits_out)

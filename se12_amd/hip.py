@@ -142,6 +142,28 @@ class _GemvBase:
     def default_launch(self, batch: int) -> LaunchConfiguration:
         return self.handle.default_launch(batch)
 
+    def multiply_rmsnorm(self, activations: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, residual: torch.Tensor,
+                         out: torch.Tensor, eps: float, y: torch.Tensor | None = None,
+                         launch: LaunchConfiguration | None = None) -> torch.Tensor:
+        """y = x . W^T (FP32, as `multiply`), then per batch row the decoder's
+        post-norm, residual add and next pre-norm in the product's tail:
+        residual = bf16(residual + norm(bf16(y)) * (1 + w1)),
+        out = norm(residual) * (1 + w2), norm(t) = t * rsqrt(mean(t^2) + eps).
+        residual / out: BF16 [B, rows] (updated / written); returns y."""
+        x, xd = _activations(activations, self.cols, self.device)
+        b = x.shape[0]
+        y = _fp32_out(y, b, self.rows, self.device)
+        for t in (w1, w2):
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != (self.rows,) or not t.is_contiguous() or t.device != self.device:
+                raise ValueError(f"norm weights must be contiguous bfloat16 [{self.rows}] on {self.device}")
+        for t in (residual, out):
+            if t.dtype != torch.bfloat16 or tuple(t.shape) != (b, self.rows) or not t.is_contiguous() or t.device != self.device:
+                raise ValueError(f"residual and out must be contiguous bfloat16 [{b}, {self.rows}] on {self.device}")
+        nat.check(nat.lib().se12_gemv_rmsnorm(self.handle.raw, nat.ptr(x), xd, b, nat.ptr(y), nat.ptr(w1), nat.ptr(w2),
+                                              nat.ptr(residual), nat.ptr(out), float(eps), _launch_struct(launch),
+                                              nat.stream_ptr()))
+        return y
+
 
 class Se12MatVecKernel(_GemvBase):
     """Fused SE12 decode + GEMV bound to one SE12 matrix (gemv.py:180-226).
@@ -187,6 +209,47 @@ class RawBf16MatVecKernel(_GemvBase):
         self.rows, self.cols = self.weights.shape
         self.device = _device_of(self.weights)
         self.handle = bind_raw_bf16(self.weights, max_batch)
+
+
+def _activations(activations: torch.Tensor, cols: int, device) -> tuple[torch.Tensor, int]:
+    x = activations.unsqueeze(0) if activations.dim() == 1 else activations
+    if x.dim() != 2 or x.shape[1] != cols:
+        raise ValueError(f"activations must be [B, {cols}], got {tuple(activations.shape)}")
+    if x.device != device:
+        raise ValueError(f"activations on {x.device}, weights on {device}")
+    if x.dtype == torch.bfloat16:
+        return x.contiguous(), nat.X_BF16
+    if x.dtype == torch.float32:
+        return x.contiguous(), nat.X_F32
+    raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
+
+
+def _fp32_out(out: torch.Tensor | None, b: int, rows: int, device) -> torch.Tensor:
+    if out is None:
+        return torch.empty((b, rows), dtype=torch.float32, device=device)
+    if out.shape != (b, rows) or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be a contiguous float32 [B, rows] tensor")
+    return out
+
+
+def multiply_gelu_mul(gate, up, activations: torch.Tensor, out: torch.Tensor, ys: list[torch.Tensor] | None = None,
+                      launch: LaunchConfiguration | None = None) -> list[torch.Tensor]:
+    """The grouped product of two bound matrices with the same rows (the MLP's
+    gate and up), then out = bf16(gelu_tanh(bf16(y_gate)) * bf16(y_up)) in the
+    product's tail. out: BF16 [B, rows]; returns the FP32 [y_gate, y_up]."""
+    if gate.rows != up.rows or gate.cols != up.cols or gate.device != up.device or type(gate) is not type(up):
+        raise ValueError("gate and up need one shape, one device and one format")
+    x, xd = _activations(activations, gate.cols, gate.device)
+    b = x.shape[0]
+    ys = [_fp32_out(None, b, gate.rows, gate.device) for _ in range(2)] if ys is None else \
+        [_fp32_out(t, b, gate.rows, gate.device) for t in ys]
+    if out.dtype != torch.bfloat16 or tuple(out.shape) != (b, gate.rows) or not out.is_contiguous() or out.device != gate.device:
+        raise ValueError(f"out must be a contiguous bfloat16 [{b}, {gate.rows}] tensor on {gate.device}")
+    hs = (ctypes.c_void_p * 2)(gate.handle.raw.value, up.handle.raw.value)
+    yp = (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr())
+    nat.check(nat.lib().se12_gemv_gelu_mul(hs, nat.ptr(x), xd, b, yp, nat.ptr(out), _launch_struct(launch),
+                                           nat.stream_ptr()))
+    return ys
 
 
 def multiply_grouped(kernels, activations: torch.Tensor, launch: LaunchConfiguration | None = None,

@@ -1,0 +1,179 @@
+"""Products with a decode-step tail (se12_gemv_gelu_mul, se12_gemv_rmsnorm)
+against the same product followed by the separate step kernel
+(se12_step_gelu_mul, se12_step_rmsnorm mode 1):
+
+- the FP32 products are bit-identical (same kernel, same launch shape);
+- the MLP gate is element-wise with the same arithmetic: bit-identical;
+- the norm's sum of squares runs over the GEMV block's threads instead of
+  the norm kernel's, so its FP32 sum may round differently, and a one-ulp
+  change of a normalised value can move the BF16 residual sum further where
+  it cancels: residual and output bit-identical on >= 99% of elements and
+  within 2^-7 of the row's largest magnitude everywhere;
+- both stay right over repeated calls and graph replays (their arrival
+  counters reset themselves), for the SE12 kernel and the raw twin, FAST and
+  edge-handling variants, batch rows split over several dot2 launches, and
+  where the step runs as its own kernel (MFMA batches, rows % 4 != 0)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from gpu_helpers import to_device
+from oracle import se12_codec as o
+from se12_amd import _native as nat
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(gpu, seed):
+    g = torch.Generator(device=gpu)
+    g.manual_seed(seed)
+    return g
+
+
+def _norm_close(got: torch.Tensor, want: torch.Tensor, min_exact: float = 0.99) -> None:
+    assert got.dtype == torch.bfloat16 and want.dtype == torch.bfloat16 and got.shape == want.shape
+    same = got.view(torch.int16) == want.view(torch.int16)
+    assert same.float().mean().item() >= min_exact
+    err = (got.float() - want.float()).abs().amax(dim=1)
+    scale = want.float().abs().amax(dim=1)
+    assert bool((err <= scale * 2.0 ** -7).all()), (err, scale)
+
+
+def _kernel(rows, cols, seed, fmt, gpu):
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+
+    bits = o.normal_bf16(rows, cols, seed=seed, std=0.02)
+    if fmt == "raw":
+        return RawBf16MatVecKernel(torch.from_numpy(bits).to(gpu).view(torch.bfloat16), max_batch=8)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    return Se12MatVecKernel(to_device(enc, gpu), max_batch=8)
+
+
+def _x(batch, cols, gpu, seed, dtype=torch.bfloat16):
+    return torch.randn((batch, cols), generator=_gen(gpu, seed), device=gpu).to(dtype)
+
+
+@pytest.mark.parametrize("fmt", ["se12", "raw"])
+@pytest.mark.parametrize("rows,cols,batch,dtype", [
+    (512, 768, 1, torch.bfloat16),      # FAST, one launch
+    (9216, 2304, 1, torch.bfloat16),    # Gemma-2-2B gate / up
+    (200, 300, 3, torch.bfloat16),      # edge-handling variant, ragged rows
+    (256, 512, 6, torch.float32),       # FP32 x: two dot2 launches (4 + 2 rows)
+    (384, 512, 8, torch.bfloat16),      # MFMA product, then the separate kernel
+])
+def test_gelu_mul_tail_equals_the_separate_kernel(gpu, fmt, rows, cols, batch, dtype):
+    from se12_amd.hip import multiply_gelu_mul, multiply_grouped
+
+    gate, up = _kernel(rows, cols, 1, fmt, gpu), _kernel(rows, cols, 2, fmt, gpu)
+    x = _x(batch, cols, gpu, 3, dtype)
+    want_y = multiply_grouped([gate, up], x)
+    want = torch.empty((batch, rows), dtype=torch.bfloat16, device=gpu)
+    nat.step_check(nat.lib().se12_step_gelu_mul(nat.ptr(want_y[0]), nat.ptr(want_y[1]), nat.STEP_F32, rows,
+                                                nat.ptr(want), batch, rows, nat.stream_ptr()))
+    for call in range(3):  # the pair counters reset themselves
+        out = torch.full((batch, rows), float("nan"), dtype=torch.bfloat16, device=gpu)
+        ys = multiply_gelu_mul(gate, up, x, out)
+        torch.cuda.synchronize()
+        assert torch.equal(ys[0], want_y[0]) and torch.equal(ys[1], want_y[1]), call
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), call
+
+
+def _norm_inputs(batch, rows, gpu, seed):
+    g = _gen(gpu, seed)
+    w1 = (torch.randn(rows, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    w2 = (torch.randn(rows, generator=g, device=gpu) * 0.1).to(torch.bfloat16)
+    res = torch.randn((batch, rows), generator=g, device=gpu).to(torch.bfloat16)
+    return w1, w2, res
+
+
+def _separate_norm(y, w1, w2, res, eps):
+    batch, rows = y.shape
+    res = res.clone()
+    out = torch.empty_like(res)
+    nat.step_check(nat.lib().se12_step_rmsnorm(nat.ptr(y), nat.STEP_F32, rows, nat.ptr(w1), nat.ptr(res), nat.ptr(w2),
+                                               nat.ptr(out), batch, rows, eps, 0.0, 1, nat.stream_ptr()))
+    return res, out
+
+
+@pytest.mark.parametrize("fmt", ["se12", "raw"])
+@pytest.mark.parametrize("rows,cols,batch,dtype", [
+    (2304, 9216, 1, torch.bfloat16),    # Gemma-2-2B down_proj
+    (2304, 2048, 1, torch.bfloat16),    # Gemma-2-2B o_proj
+    (100, 256, 2, torch.bfloat16),      # one K tile: no split-K
+    (300, 700, 3, torch.bfloat16),      # edge-handling variant, ragged rows
+    (298, 512, 1, torch.bfloat16),      # rows % 4 != 0: separate kernel
+    (256, 1024, 5, torch.float32),      # FP32 x: two dot2 launches (4 + 1 rows)
+    (512, 512, 8, torch.bfloat16),      # MFMA product, then the separate kernel
+    (8192, 256, 1, torch.bfloat16),     # 80 KiB of LDS for the tail (gfx950 blocks may take 160 KiB)
+])
+def test_rmsnorm_tail_matches_the_separate_kernel(gpu, fmt, rows, cols, batch, dtype):
+    k = _kernel(rows, cols, 5, fmt, gpu)
+    x = _x(batch, cols, gpu, 6, dtype)
+    w1, w2, res0 = _norm_inputs(batch, rows, gpu, 7)
+    eps = 1e-6
+    want_y = k.multiply(x)
+    want_res, want_out = _separate_norm(want_y, w1, w2, res0, eps)
+    res = res0.clone()
+    for call in range(3):  # the matrix counter resets itself; the residual accumulates
+        out = torch.full((batch, rows), float("nan"), dtype=torch.bfloat16, device=gpu)
+        y = k.multiply_rmsnorm(x, w1, w2, res, out, eps)
+        torch.cuda.synchronize()
+        assert torch.equal(y, want_y), call
+        _norm_close(res, want_res)
+        _norm_close(out, want_out)
+        if call < 2:
+            want_res, want_out = _separate_norm(want_y, w1, w2, res, eps)
+
+
+def test_tails_replay_in_a_graph(gpu):
+    """Five replays of a captured gate/up + down product pair with their tails,
+    each checked against eager calls on the same inputs."""
+    from se12_amd.hip import multiply_gelu_mul
+
+    gate, up = _kernel(1024, 512, 11, "se12", gpu), _kernel(1024, 512, 12, "se12", gpu)
+    down = _kernel(512, 1024, 13, "se12", gpu)
+    x = _x(1, 512, gpu, 14)
+    w1, w2, res0 = _norm_inputs(1, 512, gpu, 15)
+    m = torch.empty((1, 1024), dtype=torch.bfloat16, device=gpu)
+    gu = [torch.empty((1, 1024), dtype=torch.float32, device=gpu) for _ in range(2)]
+    yd = torch.empty((1, 512), dtype=torch.float32, device=gpu)
+    res = res0.clone()
+    h = torch.empty((1, 512), dtype=torch.bfloat16, device=gpu)
+
+    def step():
+        multiply_gelu_mul(gate, up, x, m, ys=gu)
+        down.multiply_rmsnorm(m, w1, w2, res, h, 1e-6, y=yd)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(5):
+        res.copy_(res0)
+        g.replay()
+        torch.cuda.synchronize()
+        got = (m.clone(), res.clone(), h.clone())
+        res.copy_(res0)
+        step()
+        torch.cuda.synchronize()
+        assert torch.equal(got[0], m) and torch.equal(got[1], res) and torch.equal(got[2], h), rep
+
+
+def test_tail_arguments_are_checked(gpu):
+    from se12_amd.hip import multiply_gelu_mul
+
+    gate, up = _kernel(256, 512, 1, "se12", gpu), _kernel(128, 512, 2, "se12", gpu)
+    x = _x(1, 512, gpu, 3)
+    with pytest.raises(ValueError):
+        multiply_gelu_mul(gate, up, x, torch.empty((1, 256), dtype=torch.bfloat16, device=gpu))
+    k = _kernel(256, 512, 4, "se12", gpu)
+    w1, w2, res = _norm_inputs(1, 256, gpu, 5)
+    with pytest.raises(ValueError):
+        k.multiply_rmsnorm(x, w1[:128], w2, res, torch.empty_like(res), 1e-6)

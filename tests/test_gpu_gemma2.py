@@ -148,3 +148,24 @@ def test_agrees_with_transformers_gemma2(gpu):
     with torch.no_grad():
         ref2 = hf(torch.cat([prompt, first.view(1, 1)], dim=1)).logits[:, -1].float()
     assert (d.last_logits.float() - ref2).abs().max().item() <= 0.02 * max(ref2.abs().max().item(), 1.0)
+
+
+def test_fused_tails_agree_with_separate_step_kernels(gpu):
+    """The products with the MLP gate and the residual norms in their tails
+    against the same step with those as separate kernels: layer 0's K/V slot
+    (before any tail) bit-identical, the rest within BF16 rounding."""
+    w = Gemma2Weights.random(TINY, gpu, seed=9)
+    enc = _encoded(w)
+    prompt = _prompt(gpu, 1, 10, seed=5)
+    ds = []
+    for tails in (True, False):
+        d = Gemma2Decoder(w, "se12", 1, max_len=24, encoded=enc, fused_tails=tails)
+        assert d.fused_tails == tails
+        d.prefill(prompt)
+        d.decode(1, graph=False)
+        torch.cuda.synchronize()
+        ds.append(d)
+    a, b = ds
+    assert torch.equal(a.kt[0], b.kt[0]) and torch.equal(a.v[0], b.v[0])
+    assert _close(a.kt[1][..., 10], b.kt[1][..., 10]) and _close(a.v[1][:, :, 10], b.v[1][:, :, 10])
+    assert _close(a.x, b.x) and _close(a.last_logits, b.last_logits)

@@ -190,6 +190,108 @@ __device__ __forceinline__ int window_lo(int p, int window) {
 __device__ __forceinline__ void pin(float v) { asm volatile("" ::"v"(v)); }
 __device__ __forceinline__ void pin(const uint4& v) { asm volatile("" ::"v"(v.x), "v"(v.y), "v"(v.z), "v"(v.w)); }
 
+// Rotary embedding, with the framework's roundings, of the G queries and
+// the key whose element t thread t < d holds in x[0..G]; the rotated values
+// land in y and in qk ([G + 1][d] in LDS). Every thread of the block calls
+// it (two barriers).
+template <int G>
+__device__ __forceinline__ void rotate_qk(float* qk, const float (&x)[G + 1], float fr, int p, int d, int t,
+                                          float (&y)[G + 1]) {
+    const int half = d / 2;
+    if (t < d) {
+#pragma unroll
+        for (int h = 0; h <= G; ++h) qk[h * d + t] = x[h];
+    }
+    __syncthreads();
+    if (t < d) {
+        const float freq = (float)p * fr;
+        const float cs = round_bf16(cosf(freq)), sn = round_bf16(sinf(freq));
+#pragma unroll
+        for (int h = 0; h <= G; ++h) {
+            const float* xv = qk + h * d;
+            const float rot = t < half ? -xv[t + half] : xv[t - half];
+            y[h] = round_bf16(round_bf16(xv[t] * cs) + round_bf16(rot * sn));
+        }
+    }
+    __syncthreads();
+    if (t < d) {
+#pragma unroll
+        for (int h = 0; h <= G; ++h) qk[h * d + t] = y[h];
+    }
+}
+
+// One 64-position chunk of keys against the G rotated queries in qk, for a
+// team of 4 waves (tt = thread in the team): lane group pg = tt % 8 takes 8
+// consecutive positions jgl.. (one 16-byte load per head-dim element), the
+// 32 slices es = tt / 8 every 32nd element. The key at position p comes from
+// qk (its cache slot is written in the same launch). The wave's 8 slices
+// are summed (lane bits 3..5) and lanes 0..7 write the wave's sums to red
+// ([4 waves][G][64]).
+template <int G>
+__device__ __forceinline__ void chunk_key_dots(const uint4 (&raw)[kMaxHeadDim / 32], const float* qk, int d, int tt,
+                                               int jgl, int p, float* red) {
+    const int pg = tt & 7, es = tt >> 3, tw = tt >> 6;
+    float acc[8][G];
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[m][h] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMaxHeadDim / 32; ++i) {
+        const int e = es + 32 * i;
+        if (e < d) {
+            float kv[8];
+            unpack8(raw[i], kv);
+#pragma unroll
+            for (int m = 0; m < 8; ++m)
+                if (jgl + m == p) kv[m] = qk[G * d + e];
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const float qv = qk[h * d + e];
+#pragma unroll
+                for (int m = 0; m < 8; ++m) acc[m][h] += qv * kv[m];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 8; ++m)
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            float v = acc[m][h];
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[m][h] = v;
+        }
+    if ((tt & 63) < 8) {
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+#pragma unroll
+            for (int m = 0; m < 8; ++m) red[(tw * G + h) * kChunk + 8 * pg + m] = acc[m][h];
+    }
+}
+
+// For thread t < 64 (one wave): the score of position j0 + t for each head
+// (the 4 waves' dots in order, scaling, soft-capping, -inf outside
+// [lo, p]) and the chunk's max m and sum l of exp(score - m).
+template <int G>
+__device__ __forceinline__ void chunk_scores(const float* red, const AttnArgs& a, int t, int j0, int p, int lo,
+                                             float (&sc)[G], float (&m)[G], float (&l)[G]) {
+    const int jq = j0 + t;
+    const bool valid = jq <= p && jq >= lo;
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const float dot = red[(0 * G + h) * kChunk + t] + red[(1 * G + h) * kChunk + t] +
+                          red[(2 * G + h) * kChunk + t] + red[(3 * G + h) * kChunk + t];
+        float v = round_bf16(round_bf16(dot) * a.scaling);
+        if (a.softcap > 0.0f) v = round_bf16(round_bf16(tanhf(round_bf16(v / a.softcap))) * a.softcap);
+        if (!valid) v = -INFINITY;
+        sc[h] = v;
+        m[h] = wave_max(v);                      // >= 1 valid position per chunk
+        l[h] = wave_sum(valid ? expf(v - m[h]) : 0.0f);
+    }
+}
+
 template <int G, int DT>
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     __shared__ float qk[(G + 1) * kMaxHeadDim];   // rotated q of the G heads, then k
@@ -239,94 +341,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     if (j0 > p || j0 + kChunk <= lo) return;
     const bool holds_p = p < j0 + kChunk;
 
-    // rotary embedding of q and k with the framework's roundings
-    float y[G + 1];
-    if (t < d) {
+    float x[G + 1], y[G + 1];
 #pragma unroll
-        for (int h = 0; h < G; ++h) qk[h * d + t] = xq[h];
-        qk[G * d + t] = xk;
+    for (int h = 0; h < G; ++h) x[h] = xq[h];
+    x[G] = xk;
+    rotate_qk<G>(qk, x, fr, p, d, t, y);
+    if (t < d && holds_p) {
+        a.kt[((int64_t)kvb * d + t) * L + p] = f_to_bf16(y[G]);
+        a.vc[((int64_t)kvb * L + p) * d + t] = f_to_bf16(vv);
     }
     __syncthreads();
-    if (t < d) {
-        const float freq = (float)p * fr;
-        const float cs = round_bf16(cosf(freq)), sn = round_bf16(sinf(freq));
-#pragma unroll
-        for (int h = 0; h <= G; ++h) {
-            const float* x = qk + h * d;
-            const float rot = t < half ? -x[t + half] : x[t - half];
-            y[h] = round_bf16(round_bf16(x[t] * cs) + round_bf16(rot * sn));
-        }
-    }
-    __syncthreads();
-    if (t < d) {
-#pragma unroll
-        for (int h = 0; h <= G; ++h) qk[h * d + t] = y[h];
-        if (holds_p) {
-            a.kt[((int64_t)kvb * d + t) * L + p] = f_to_bf16(y[G]);
-            a.vc[((int64_t)kvb * L + p) * d + t] = f_to_bf16(vv);
-        }
-    }
-    __syncthreads();
-
-    // dot products of the chunk's keys with the G rotated queries
-    float acc[8][G];
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-        for (int h = 0; h < G; ++h) acc[m][h] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kMaxHeadDim / 32; ++i) {
-        const int e = es + 32 * i;
-        if (e < d) {
-            float kv[8];
-            unpack8(raw[i], kv);
-            // the new key is not in the cache yet for this block: take it from LDS
-#pragma unroll
-            for (int m = 0; m < 8; ++m)
-                if (jgl + m == p) kv[m] = qk[G * d + e];
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float qv = qk[h * d + e];
-#pragma unroll
-                for (int m = 0; m < 8; ++m) acc[m][h] += qv * kv[m];
-            }
-        }
-    }
-    // the 8 slices of a wave (lane bits 3..5), then the 4 waves in order
-#pragma unroll
-    for (int m = 0; m < 8; ++m)
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            float s = acc[m][h];
-            s += __shfl_xor(s, 8, 64);
-            s += __shfl_xor(s, 16, 64);
-            s += __shfl_xor(s, 32, 64);
-            acc[m][h] = s;
-        }
-    if (lane < 8) {
-#pragma unroll
-        for (int h = 0; h < G; ++h)
-#pragma unroll
-            for (int m = 0; m < 8; ++m) red[(w * G + h) * kChunk + 8 * pg + m] = acc[m][h];
-    }
+    chunk_key_dots<G>(raw, qk, d, t, jgl, p, red);
     __syncthreads();
     if (t < kChunk) {
-        const int jq = j0 + t;
-        const bool valid = jq <= p && jq >= lo;
+        float sc[G], m[G], l[G];
+        chunk_scores<G>(red, a, t, j0, p, lo, sc, m, l);
         const int64_t lp = (int64_t)a.chunks * kChunk;
+#pragma unroll
         for (int h = 0; h < G; ++h) {
-            const float dot = red[(0 * G + h) * kChunk + t] + red[(1 * G + h) * kChunk + t] +
-                              red[(2 * G + h) * kChunk + t] + red[(3 * G + h) * kChunk + t];
-            float sc = round_bf16(round_bf16(dot) * a.scaling);
-            if (a.softcap > 0.0f) sc = round_bf16(round_bf16(tanhf(round_bf16(sc / a.softcap))) * a.softcap);
-            if (!valid) sc = -INFINITY;
             const int64_t row = (int64_t)b * a.heads + kh * G + h;
-            a.scores[row * lp + jq] = sc;
-            const float m = wave_max(sc);                      // >= 1 valid position per chunk
-            const float l = wave_sum(valid ? expf(sc - m) : 0.0f);
+            a.scores[row * lp + j0 + t] = sc[h];
             if (t == 0) {
-                a.stats[(row * a.chunks + c) * 2 + 0] = m;
-                a.stats[(row * a.chunks + c) * 2 + 1] = l;
+                a.stats[(row * a.chunks + c) * 2 + 0] = m[h];
+                a.stats[(row * a.chunks + c) * 2 + 1] = l[h];
             }
         }
     }

@@ -147,6 +147,11 @@ ATTN_CASES = [
     (2, 4, 4, 128, 200, 199, 0, torch.float32),
     (1, 8, 2, 64, 256, 130, 0, torch.float32),
     (2, 16, 2, 128, 96, 70, 0, torch.float32),
+    (1, 8, 4, 256, 1024, 1023, 0, torch.float32),
+    (1, 8, 4, 256, 1024, 1000, 300, torch.bfloat16),
+    (2, 8, 4, 256, 1280, 1100, 0, torch.float32),
+    (1, 8, 4, 256, 1280, 1279, 512, torch.bfloat16),
+    (1, 8, 8, 64, 1096, 777, 0, torch.float32),
 ]
 
 
@@ -184,8 +189,9 @@ def test_attention_step(gpu, batch, heads, kvh, d, L, pos, window, dtype):
     assert torch.equal(out, out2)
 
 
-def test_attention_position_outside_the_cache_touches_nothing(gpu):
-    batch, heads, kvh, d, L = 1, 4, 2, 64, 80
+@pytest.mark.parametrize("L", [80, 1096])
+def test_attention_position_outside_the_cache_touches_nothing(gpu, L):
+    batch, heads, kvh, d = 1, 4, 2, 64
     q = torch.ones((batch, heads * d), device=gpu)
     k = torch.ones((batch, kvh * d), device=gpu)
     kt = torch.full((batch, kvh, d, L), 3.0, device=gpu).to(torch.bfloat16)

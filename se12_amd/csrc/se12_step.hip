@@ -150,11 +150,17 @@ __global__ __launch_bounds__(kNormMaxThreads) void rmsnorm_kernel(NormArgs a) {
 //           also writes the new K/V slot), the chunk's scores for the G query
 //           heads of the KV head, the chunk's max m_c and sum l_c of
 //           exp(s - m_c);
-//   pv      the global max M = max m_c and sum S = sum l_c exp(m_c - M), the
-//           chunk's probabilities p = bf16(exp(s - M) / S) (softmax in FP32,
-//           rounded as the framework rounds it), the partial sum p . V in
-//           FP32; the last block of a (sequence, KV head) adds the partials
-//           in chunk order and rounds to BF16.
+//   pv      one block per (sequence, KV head, 32 head-dim columns, span of
+//           positions): the global max M = max m_c and sum S =
+//           sum l_c exp(m_c - M), the probabilities p = bf16(exp(s - M) / S)
+//           (softmax in FP32, rounded as the framework rounds it) and the
+//           sum p . V of its columns over its span in FP32. A span covers
+//           1024 positions (256 x G query heads of registers per thread),
+//           so caches up to that need one span and write the output
+//           directly; longer ones write partial sums that the last block of
+//           a (sequence, KV head, columns) adds in span order. Splitting
+//           the columns instead of the positions keeps a short cache's
+//           blocks free of that cross-block reduction.
 // ---------------------------------------------------------------------------
 
 constexpr int kChunk = 64;
@@ -174,8 +180,8 @@ struct AttnArgs {
     uint16_t* out;           // [B, heads * d]
     float* scores;           // [B, heads, chunks * 64]
     float* stats;            // [B, heads, chunks, 2]: m_c, l_c
-    float* partial;          // [B, heads, chunks, d]
-    int* counters;           // [B * kvh], zero between launches
+    float* partial;          // [B, heads, spans <= chunks, d]
+    int* counters;           // [B * kvh * column blocks], zero between launches
     int heads, kvh, d, max_len, chunks;
     float scaling, softcap;
     int window;
@@ -369,31 +375,42 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     }
 }
 
+// weighted V: positions per thread (all loads in flight at once) and the
+// span of positions of one block
+constexpr int kPvCols = 32;
+template <int G>
+constexpr int pv_per_thread() { return G <= 2 ? 16 : 32 / G; }
+template <int G>
+constexpr int pv_span() { return (kAttnThreads / (kPvCols / 8)) * pv_per_thread<G>(); }
+
 template <int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
-    __shared__ float prob[G * kChunk];
+    constexpr int P = pv_per_thread<G>();
+    constexpr int kSpan = pv_span<G>();
     __shared__ float ms[2 * G];
-    __shared__ float red[4 * G * kMaxHeadDim];    // per wave: G x d partial sums
+    __shared__ float red[4 * G * kPvCols];        // per wave: G x 32 column sums
     __shared__ int flag;
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
     const int kvb = blockIdx.x;
     const int b = kvb / a.kvh, kh = kvb % a.kvh;
-    const int c = blockIdx.y, j0 = c * kChunk;
+    const int cb = blockIdx.y, sp = blockIdx.z;
     const int d = a.d, L = a.max_len;
     const int64_t obase = (int64_t)b * a.heads * d + (int64_t)kh * G * d;
     const int64_t row0 = (int64_t)b * a.heads + kh * G;
     const int64_t lp = (int64_t)a.chunks * kChunk;
+    // thread: 8-column group cq of the block's 32 columns, position slice ps
+    const int cq = t & 3, ps = t >> 2;
+    const int e0 = cb * kPvCols + 8 * cq;
+    const uint16_t* vb = a.vc + (int64_t)kvb * L * d + (e0 < d ? e0 : d - 8);
+    const int jb = sp * kSpan;
 
     // Every load whose address does not depend on the position goes out
     // together with the position's: the statistics of the first 64 chunks of
-    // the wave's heads (lane = chunk), the chunk's scores and its 64 rows of
-    // V (lane group eg = 8 consecutive head-dim elements, one 16-byte load
-    // per position; 8 position slices ps take every 8th position).
+    // the wave's heads (lane = chunk), and the span's V rows and scores.
     const int64_t p64 = *a.pos;
     __builtin_amdgcn_sched_barrier(0);  // the position's load goes out first
     constexpr int kHeadsPerWave = (G + 3) / 4;
-    constexpr int kScoresPerThread = (G * kChunk + kAttnThreads - 1) / kAttnThreads;
-    float sm[kHeadsPerWave], sl[kHeadsPerWave], sc[kScoresPerThread];
+    float sm[kHeadsPerWave], sl[kHeadsPerWave];
     const int cl = lane < a.chunks ? lane : a.chunks - 1;
 #pragma unroll
     for (int k = 0; k < kHeadsPerWave; ++k) {
@@ -402,19 +419,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
         sm[k] = st[cl * 2];
         sl[k] = st[cl * 2 + 1];
     }
+    uint4 vr[P];
+    float sc[P][G];
 #pragma unroll
-    for (int k = 0; k < kScoresPerThread; ++k) {
-        const int i = t + kAttnThreads * k < G * kChunk ? t + kAttnThreads * k : G * kChunk - 1;
-        sc[k] = a.scores[(row0 + i / kChunk) * lp + j0 + i % kChunk];
-    }
-    const int eg = t & 31, ps = t >> 5;
-    const int e0 = 8 * eg;
-    const uint16_t* vb = a.vc + ((int64_t)kvb * L + j0) * d + (e0 < d ? e0 : d - 8);
-    uint4 raw[kChunk / 8];
+    for (int i = 0; i < P; ++i) {
+        const int j = jb + ps + 64 * i;
+        const int jc = j < L ? j : L - 1;
+        vr[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)jc * d);
 #pragma unroll
-    for (int i = 0; i < kChunk / 8; ++i) {
-        const int jj = ps + 8 * i;
-        raw[i] = *reinterpret_cast<const uint4*>(vb + (int64_t)(j0 + jj < L ? jj : L - 1 - j0) * d);
+        for (int h = 0; h < G; ++h) sc[i][h] = a.scores[(row0 + h) * lp + jc];
     }
 #pragma unroll
     for (int k = 0; k < kHeadsPerWave; ++k) {
@@ -422,18 +435,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
         pin(sl[k]);
     }
 #pragma unroll
-    for (int k = 0; k < kScoresPerThread; ++k) pin(sc[k]);
+    for (int i = 0; i < P; ++i) {
+        pin(vr[i]);
 #pragma unroll
-    for (int i = 0; i < kChunk / 8; ++i) pin(raw[i]);
+        for (int h = 0; h < G; ++h) pin(sc[i][h]);
+    }
 
     if (p64 < 0 || p64 >= L) {  // no cache slot: zeros, no cache or counter touched
-        if (c == 0)
+        if (cb == 0 && sp == 0)
             for (int i = t; i < G * d; i += kAttnThreads) a.out[obase + i] = 0;
         return;
     }
     const int p = (int)p64, lo = window_lo(p, a.window);
+    const int s_lo = lo / kSpan, s_hi = p / kSpan;
+    if (sp < s_lo || sp > s_hi) return;
     const int c_lo = lo / kChunk, c_hi = p / kChunk;
-    if (c < c_lo || c > c_hi) return;
     // global max and sum of each head over its chunks (one wave per head)
 #pragma unroll
     for (int k = 0; k < kHeadsPerWave; ++k) {
@@ -455,78 +471,75 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
         }
     }
     __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kScoresPerThread; ++k) {
-        const int i = t + kAttnThreads * k;
-        if (i < G * kChunk) {
-            const int h = i / kChunk, j = j0 + i % kChunk;
-            prob[i] = (j <= p && j >= lo) ? round_bf16(expf(sc[k] - ms[2 * h]) / ms[2 * h + 1]) : 0.0f;
-        }
-    }
-    __syncthreads();
-    // weighted V
-    const int jlo = lo > j0 ? lo - j0 : 0;
-    const int jhi = p - j0 < kChunk - 1 ? p - j0 : kChunk - 1;
     float acc[8][G];
 #pragma unroll
     for (int m = 0; m < 8; ++m)
 #pragma unroll
         for (int h = 0; h < G; ++h) acc[m][h] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kChunk / 8; ++i) {
-        const int jj = ps + 8 * i;
-        if (jj >= jlo && jj <= jhi) {   // V past pos may hold anything (0 x NaN)
+    for (int i = 0; i < P; ++i) {
+        const int j = jb + ps + 64 * i;
+        if (j >= lo && j <= p) {   // V past pos may hold anything (0 x NaN)
             float v[8];
-            unpack8(raw[i], v);
+            unpack8(vr[i], v);
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                const float pr = prob[h * kChunk + jj];
+                const float pr = round_bf16(expf(sc[i][h] - ms[2 * h]) / ms[2 * h + 1]);
 #pragma unroll
                 for (int m = 0; m < 8; ++m) acc[m][h] += pr * v[m];
             }
         }
     }
-    // the two position slices of a wave, then the 4 waves in order
+    // the 16 position slices of a wave (lane bits 2..5), then the 4 waves in order
 #pragma unroll
     for (int m = 0; m < 8; ++m)
 #pragma unroll
-        for (int h = 0; h < G; ++h) acc[m][h] += __shfl_xor(acc[m][h], 32, 64);
-    if (lane < 32 && e0 < d) {
+        for (int h = 0; h < G; ++h) {
+            float v = acc[m][h];
+            v += __shfl_xor(v, 4, 64);
+            v += __shfl_xor(v, 8, 64);
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            acc[m][h] = v;
+        }
+    if (lane < 4) {
 #pragma unroll
         for (int h = 0; h < G; ++h)
 #pragma unroll
-            for (int m = 0; m < 8; ++m) red[(w * G + h) * kMaxHeadDim + e0 + m] = acc[m][h];
+            for (int m = 0; m < 8; ++m) red[(w * G + h) * kPvCols + 8 * cq + m] = acc[m][h];
     }
     __syncthreads();
-    const int nvalid = c_hi - c_lo + 1;
-    for (int i = t; i < G * d; i += kAttnThreads) {
-        const int h = i / d, e = i % d;
-        const float o = red[(0 * G + h) * kMaxHeadDim + e] + red[(1 * G + h) * kMaxHeadDim + e] +
-                        red[(2 * G + h) * kMaxHeadDim + e] + red[(3 * G + h) * kMaxHeadDim + e];
-        if (nvalid == 1)
-            a.out[obase + i] = f_to_bf16(o);
-        else
-            __hip_atomic_store(&a.partial[((row0 + h) * a.chunks + c) * d + e], o, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    const int nspans = s_hi - s_lo + 1;
+    const int h = t / kPvCols, e = cb * kPvCols + t % kPvCols;
+    const bool owner = t < G * kPvCols && e < d;
+    float o = 0.0f;
+    if (owner)
+        o = red[(0 * G + h) * kPvCols + t % kPvCols] + red[(1 * G + h) * kPvCols + t % kPvCols] +
+            red[(2 * G + h) * kPvCols + t % kPvCols] + red[(3 * G + h) * kPvCols + t % kPvCols];
+    if (nspans == 1) {
+        if (owner) a.out[obase + h * d + e] = f_to_bf16(o);
+        return;
     }
-    if (nvalid == 1) return;
+    // several spans: partial sums [row][span][d], the last block of the
+    // (sequence, KV head, columns) adds them in span order
+    float* part = a.partial + (row0 + h) * (int64_t)a.chunks * d;
+    if (owner) __hip_atomic_store(&part[(int64_t)sp * d + e], o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    int* counter = &a.counters[(int64_t)kvb * gridDim.y + cb];
     if (t == 0) {
-        const int old = __hip_atomic_fetch_add(&a.counters[kvb], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        flag = old == nvalid - 1;
+        const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        flag = old == nspans - 1;
     }
     __syncthreads();
     if (!flag) return;
-    for (int i = t; i < G * d; i += kAttnThreads) {
-        const int h = i / d, e = i % d;
-        float o = 0.0f;
-        for (int cc = c_lo; cc <= c_hi; ++cc)
-            o += __hip_atomic_load(&a.partial[((row0 + h) * a.chunks + cc) * d + e], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        a.out[obase + i] = f_to_bf16(o);
+    if (owner) {
+        float sum = 0.0f;
+        for (int ss = s_lo; ss <= s_hi; ++ss)
+            sum += __hip_atomic_load(&part[(int64_t)ss * d + e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        a.out[obase + h * d + e] = f_to_bf16(sum);
     }
-    if (t == 0) __hip_atomic_store(&a.counters[kvb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -678,7 +691,7 @@ AttnLayout attn_layout(int32_t batch, int32_t heads, int32_t kv_heads, int32_t h
     AttnLayout l;
     l.chunks = (max_len + kChunk - 1) / kChunk;
     l.counters = 0;
-    l.scores = up256((int64_t)batch * kv_heads * sizeof(int));
+    l.scores = up256((int64_t)batch * kv_heads * (kMaxHeadDim / kPvCols) * sizeof(int));
     l.stats = l.scores + up256((int64_t)batch * heads * l.chunks * kChunk * sizeof(float));
     l.partial = l.stats + up256((int64_t)batch * heads * l.chunks * 2 * sizeof(float));
     l.total = l.partial + up256((int64_t)batch * heads * l.chunks * head_dim * sizeof(float));
@@ -700,7 +713,8 @@ void launch_attention(const AttnArgs& a, int blocks_x, hipStream_t stream) {
         hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_F32>), grid, dim3(kAttnThreads), 0, stream, a);
     else
         hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_BF16>), grid, dim3(kAttnThreads), 0, stream, a);
-    hipLaunchKernelGGL(attn_pv_kernel<G>, grid, dim3(kAttnThreads), 0, stream, a);
+    const dim3 pv_grid(blocks_x, (a.d + kPvCols - 1) / kPvCols, (a.max_len + pv_span<G>() - 1) / pv_span<G>());
+    hipLaunchKernelGGL(attn_pv_kernel<G>, pv_grid, dim3(kAttnThreads), 0, stream, a);
 }
 
 struct ArgmaxLayout {

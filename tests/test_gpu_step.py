@@ -152,6 +152,8 @@ ATTN_CASES = [
     (2, 8, 4, 256, 1280, 1100, 0, torch.float32),
     (1, 8, 4, 256, 1280, 1279, 512, torch.bfloat16),
     (1, 8, 8, 64, 1096, 777, 0, torch.float32),
+    (1, 16, 2, 128, 600, 590, 0, torch.float32),        # 8 query heads per KV head over 3 spans
+    (2, 16, 4, 64, 520, 519, 200, torch.bfloat16),      # 4 per KV head over 2 spans, windowed
 ]
 
 

@@ -188,6 +188,29 @@ int se12_gemv_rmsnorm(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_
                       const uint16_t* w1_dev, const uint16_t* w2_dev, uint16_t* residual_dev, uint16_t* out_dev,
                       float eps, const se12_launch* launch, void* stream);
 
+/* The product of the decoder's next normalised input, with the norm in the
+ * product's head (no reference counterpart; same motivation as above): for
+ * each batch row, from the previous product's FP32 output y_prev [batch,
+ * cols],
+ *   r = bf16(residual_in + norm(bf16(y_prev)) * (1 + w1)),
+ *   h = norm(r) * (1 + w2)   (norm as in se12_gemv_rmsnorm),
+ * residual_out = r and h_out = h (BF16 [batch, cols]), then y[i] = W_i h for
+ * the `count` handles (as se12_gemv_grouped). gelu_out non-NULL (two handles
+ * with one row count): the MLP gate of se12_gemv_gelu_mul as well.
+ * residual_in and residual_out are either the same tensor or disjoint.
+ * Where the product runs the dot2 kernel with BF16 x (batch <= 4), whole K
+ * tiles, distinct residuals, 16-byte aligned y_prev and 8-byte aligned
+ * weights, residuals and h_out, and a block's LDS holds cols x (12 x batch
+ * + 4) bytes, every block of the product rebuilds h in LDS (sums of squares
+ * over its threads) and block (0, 0) writes residual_out and h_out;
+ * otherwise the norm runs as its own kernel (se12_step_rmsnorm mode 1)
+ * before the product. Same stream, allocation and ordering rules as
+ * se12_gemv. */
+int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y_prev_dev, int32_t batch,
+                      const uint16_t* w1_dev, const uint16_t* w2_dev, const uint16_t* residual_in_dev,
+                      uint16_t* residual_out_dev, uint16_t* h_out_dev, float eps, float* const* y_dev,
+                      uint16_t* gelu_out_dev, const se12_launch* launch, void* stream);
+
 /* Decodes the whole matrix to row-major BF16 bits [rows, cols] (cropped).
  * Replaces the lws_se12_decode launch plus the device untile/crop of
  * CudaSe12WeightDecoder (lws/adapters/cuda/se12_decoder.py:58-76,147-185;

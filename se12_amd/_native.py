@@ -119,6 +119,11 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_float,
          ctypes.POINTER(Launch), c_void_p],
     ),
+    "se12_gemv_prenorm": (
+        c_i32,
+        [ctypes.POINTER(c_void_p), c_i32, c_void_p, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         ctypes.c_float, ctypes.POINTER(c_void_p), c_void_p, ctypes.POINTER(Launch), c_void_p],
+    ),
     "se12_decode": (c_i32, [c_void_p, c_void_p, c_void_p]),
     "se12_decode_rows": (c_i32, [c_void_p, c_void_p, c_i64, c_void_p, c_void_p]),
     "se12_codebook_from_histogram": (c_i32, [ctypes.POINTER(ctypes.c_uint64), c_u8p]),

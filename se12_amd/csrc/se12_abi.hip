@@ -431,7 +431,7 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // launch for all rows, or one dot2 launch per 4 rows.
 static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, const void* x, int32_t x_dtype,
                       int32_t batch, float* const* ys, const se12_launch* launch, void* stream,
-                      const GemvEpilogue* epi = nullptr) {
+                      const GemvEpilogue* epi = nullptr, const GemvPrologue* pro = nullptr) {
     if (count < 1 || count > kMaxGroup) return fail(SE12_E_INVALID, "%s: %d matrices, expected 1..%d", fn, count, kMaxGroup);
     if (!x) return fail(SE12_E_INVALID, "%s: NULL x", fn);
     if (x_dtype != SE12_X_BF16 && x_dtype != SE12_X_F32) return fail(SE12_E_INVALID, "%s: unknown x_dtype %d", fn, x_dtype);
@@ -497,6 +497,20 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             if ((int64_t)splits * b_first * hs[i]->Np > hs[i]->partial_elems)
                 return fail(SE12_E_CAPACITY, "%s: %d K splits at batch %d exceed handle %d's split-K workspace", fn,
                             splits, batch, i);
+    // the x prologue runs in the dot2 kernel when its rows fit the block's
+    // LDS; the caller has checked the rest
+    const bool fuse_pro = pro && !mfma && !generic &&
+                          (int64_t)(gemv_xn_lds_bytes(h0->K, b_first, waves) + kLutBytes) <= h0->lds_per_block;
+    if (pro && !fuse_pro) {
+        // the norm as its own kernel into h_out, then the product of h_out
+        hipStream_t st0 = static_cast<hipStream_t>(stream);
+        if (pro->res_out != pro->res_in)
+            SE12_HIP(hipMemcpyAsync(pro->res_out, pro->res_in, (size_t)batch * h0->K * 2, hipMemcpyDeviceToDevice, st0));
+        const int rc = se12_step_rmsnorm(pro->y_prev, SE12_STEP_F32, h0->K, pro->w1, pro->res_out, pro->w2, pro->h_out,
+                                         batch, (int32_t)h0->K, pro->eps, 0.0f, 1, st0);
+        if (rc != SE12_STEP_OK) return fail(SE12_E_HIP, "%s norm: %s", fn, se12_step_last_error());
+        return gemv_group(fn, hs, count, pro->h_out, SE12_X_BF16, batch, ys, launch, stream, epi, nullptr);
+    }
     // the step tail runs in the dot2 kernel when its row fits the block's LDS
     const bool fuse_epi =
         epi && !mfma &&
@@ -536,6 +550,15 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         const bool gen = generic || !aligned16(g.m[0].x);
         GemvPlan p = mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
                           : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
+        if (fuse_pro) {
+            g.pro = *pro;
+            g.pro.y_prev += (size_t)b0 * h0->K;
+            g.pro.res_in += (size_t)b0 * h0->K;
+            g.pro.res_out += (size_t)b0 * h0->K;
+            g.pro.h_out += (size_t)b0 * h0->K;
+            p.xn = true;
+            p.lds = gemv_xn_lds_bytes(h0->K, bl, waves);
+        }
         if (fuse_epi) {
             g.epi = *epi;
             g.epi.out += (size_t)b0 * h0->N;
@@ -606,6 +629,56 @@ int se12_gemv_rmsnorm(se12_handle* h, const void* x, int32_t x_dtype, int32_t ba
     se12_handle* hs[1] = {h};
     float* ys[1] = {y};
     return gemv_group("se12_gemv_rmsnorm", hs, 1, x, x_dtype, batch, ys, launch, stream, &e);
+}
+
+int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y_prev, int32_t batch,
+                      const uint16_t* w1, const uint16_t* w2, const uint16_t* residual_in, uint16_t* residual_out,
+                      uint16_t* h_out, float eps, float* const* y, uint16_t* gelu_out, const se12_launch* launch,
+                      void* stream) {
+    const char* fn = "se12_gemv_prenorm";
+    if (!handles || !y || !y_prev || !w1 || !w2 || !residual_in || !residual_out || !h_out)
+        return fail(SE12_E_INVALID, "%s: NULL handles, y, y_prev, weights, residuals or h_out", fn);
+    if (count < 1 || count > kMaxGroup) return fail(SE12_E_INVALID, "%s: %d matrices, expected 1..%d", fn, count, kMaxGroup);
+    if (!handles[0]) return fail(SE12_E_INVALID, "%s: NULL handle 0", fn);
+    const int64_t K = handles[0]->K;
+    if (K > kStepNormMaxRows) return fail(SE12_E_INVALID, "%s: %lld columns, the norm takes at most %d", fn, (long long)K,
+                                          kStepNormMaxRows);
+    if (batch < 1) return fail(SE12_E_INVALID, "%s: batch %d", fn, batch);
+    const size_t row_bytes = (size_t)batch * K * 2;
+    const char* ri = reinterpret_cast<const char*>(residual_in);
+    const char* ro = reinterpret_cast<const char*>(residual_out);
+    if (ri != ro && ri < ro + row_bytes && ro < ri + row_bytes)
+        return fail(SE12_E_INVALID, "%s: residual_in and residual_out overlap without being the same tensor", fn);
+    GemvPrologue pr{};
+    pr.y_prev = y_prev;
+    pr.w1 = w1;
+    pr.w2 = w2;
+    pr.res_in = residual_in;
+    pr.res_out = residual_out;
+    pr.h_out = h_out;
+    pr.eps = eps;
+    // the in-kernel prologue reads residual_in while block (0, 0) writes
+    // residual_out, and takes 16-byte rows of y_prev: otherwise the norm runs
+    // as its own kernel
+    const bool ok = ri != ro && K % 4 == 0 && aligned16(y_prev) && aligned8(w1) && aligned8(w2) && aligned8(residual_in) &&
+                    aligned8(residual_out) && aligned8(h_out);
+    GemvEpilogue e{};
+    if (gelu_out) {
+        if (count != 2 || !handles[1] || handles[0]->N != handles[1]->N)
+            return fail(SE12_E_INVALID, "%s: the MLP gate takes two matrices of one row count", fn);
+        e.kind = kEpiGeluMul;
+        e.out = gelu_out;
+    }
+    if (!ok) {
+        // same results through the separate kernels (in-place residual update)
+        hipStream_t st = static_cast<hipStream_t>(stream);
+        if (ri != ro) SE12_HIP(hipMemcpyAsync(residual_out, residual_in, row_bytes, hipMemcpyDeviceToDevice, st));
+        const int rc = se12_step_rmsnorm(y_prev, SE12_STEP_F32, K, w1, residual_out, w2, h_out, batch, (int32_t)K, eps,
+                                         0.0f, 1, st);
+        if (rc != SE12_STEP_OK) return fail(SE12_E_HIP, "%s norm: %s", fn, se12_step_last_error());
+        return gemv_group(fn, handles, count, h_out, SE12_X_BF16, batch, y, launch, stream, gelu_out ? &e : nullptr);
+    }
+    return gemv_group(fn, handles, count, h_out, SE12_X_BF16, batch, y, launch, stream, gelu_out ? &e : nullptr, &pr);
 }
 
 static DecodeArgs decode_args(const se12_handle* h, uint16_t* out) {

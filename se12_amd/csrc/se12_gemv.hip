@@ -51,12 +51,17 @@ struct XTile {
     uint32_t v[B][XF32 ? 16 : 8];
 };
 
-template <int B, bool XF32, bool GENERIC>
-__device__ __forceinline__ void load_x(XTile<B, XF32>& x, const GemvArgs& a, int kt, uint32_t lane) {
+template <int B, bool XF32, bool GENERIC, bool XN>
+__device__ __forceinline__ void load_x(XTile<B, XF32>& x, const GemvArgs& a, int kt, uint32_t lane, const uint16_t* xs) {
     const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
 #pragma unroll
     for (int b = 0; b < B; ++b) {
-        if constexpr (!GENERIC) {
+        if constexpr (XN) {  // x rebuilt by the prologue, in LDS
+            const uint4* p = reinterpret_cast<const uint4*>(xs + b * (int)a.K + (int)col);
+            const uint4 u0 = p[0], u1 = p[1];
+            x.v[b][0] = u0.x; x.v[b][1] = u0.y; x.v[b][2] = u0.z; x.v[b][3] = u0.w;
+            x.v[b][4] = u1.x; x.v[b][5] = u1.y; x.v[b][6] = u1.z; x.v[b][7] = u1.w;
+        } else if constexpr (!GENERIC) {
             const uint4* p = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + b * a.K + col);
             const uint4 u0 = p[0], u1 = p[1];
             x.v[b][0] = u0.x; x.v[b][1] = u0.y; x.v[b][2] = u0.z; x.v[b][3] = u0.w;
@@ -84,6 +89,98 @@ __device__ __forceinline__ float load_dev(const float* p) {
 }
 __device__ __forceinline__ void store_dev(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// GemvPrologue: every block rebuilds x (the decoder's next normalised input)
+// from the previous product's FP32 output into LDS, with the arithmetic of
+// se12_step_rmsnorm mode 1 (sums of squares over this block's threads).
+// Its inputs are staged into LDS by direct-to-LDS loads (no registers held,
+// so the first round's weights go out at the same time); the passes then
+// run out of LDS. Block (0, 0) writes the new residual and x.
+//
+// LDS (16-byte aligned pieces, K % 256 == 0): x [B][K] BF16 (the kernel's
+// x), y [B][K] FP32 (then the residual), residual [B][K] BF16, w1 [K], w2 [K].
+// bytes [0, n) of src into LDS at dst (16-byte aligned, n % 16 == 0), one
+// KiB per wave instruction (lane i: bytes 16 i .. 16 i + 15 of the KiB)
+__device__ __forceinline__ void stage_to_lds(const void* src, void* dst, int n, int w, int W, uint32_t lane) {
+    for (int c = w * 1024; c < n; c += W * 1024) {
+        const int off = c + (int)lane * 16;
+        if (off < n)
+            __builtin_amdgcn_global_load_lds(static_cast<const char*>(src) + off, static_cast<char*>(dst) + c, 16, 0, 0);
+    }
+}
+
+template <int B>
+__device__ __forceinline__ void gemv_prologue_stage(const GemvPrologue& pr, int64_t K, char* stage, int w, int W,
+                                                    uint32_t lane) {
+    const int k = (int)K;
+    char* ys = stage;
+    char* rs = ys + (size_t)B * k * 4;
+    char* w1s = rs + (size_t)B * k * 2;
+    char* w2s = w1s + (size_t)k * 2;
+    stage_to_lds(pr.y_prev, ys, B * k * 4, w, W, lane);
+    stage_to_lds(pr.res_in, rs, B * k * 2, w, W, lane);
+    stage_to_lds(pr.w1, w1s, k * 2, w, W, lane);
+    stage_to_lds(pr.w2, w2s, k * 2, w, W, lane);
+}
+
+// after the staged loads have landed (the caller waits and meets the block)
+template <int B>
+__device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* stage, uint16_t* xs, float* sh) {
+    using namespace se12step;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    const int k = (int)K, n4 = k >> 2;
+    float4* ys = reinterpret_cast<float4*>(stage);
+    const uint2* rs = reinterpret_cast<const uint2*>(stage + (size_t)B * k * 4);
+    const uint2* w1s = reinterpret_cast<const uint2*>(stage + (size_t)B * k * 6);
+    const uint2* w2s = w1s + n4;
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+    auto lo = [](uint32_t u) { return bf16_to_f(u & 0xFFFFu); };
+    auto hi = [](uint32_t u) { return bf16_to_f(u >> 16); };
+    auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
+    for (int b = 0; b < B; ++b) {
+        float4* yb = ys + (size_t)b * n4;
+        const uint2* rb = rs + (size_t)b * n4;
+        float ss = 0.0f;
+        for (int g = tid; g < n4; g += nt) {
+            const float4 v = yb[g];
+            const float4 t = make_float4(round_bf16(v.x), round_bf16(v.y), round_bf16(v.z), round_bf16(v.w));
+            ss += t.x * t.x;
+            ss += t.y * t.y;
+            ss += t.z * t.z;
+            ss += t.w * t.w;
+        }
+        const float inv = rms_inv(block_sum(ss, sh), k, pr.eps);
+        float ss2 = 0.0f;
+        for (int g = tid; g < n4; g += nt) {
+            const float4 v = yb[g];
+            const uint2 c1 = w1s[g], c2 = rb[g];
+            float4 r;
+            r.x = round_bf16(lo(c2.x) + round_bf16(rms_scale(round_bf16(v.x), inv, lo(c1.x))));
+            r.y = round_bf16(hi(c2.x) + round_bf16(rms_scale(round_bf16(v.y), inv, hi(c1.x))));
+            r.z = round_bf16(lo(c2.y) + round_bf16(rms_scale(round_bf16(v.z), inv, lo(c1.y))));
+            r.w = round_bf16(hi(c2.y) + round_bf16(rms_scale(round_bf16(v.w), inv, hi(c1.y))));
+            yb[g] = r;  // this thread's own elements: no other thread reads them
+            ss2 += r.x * r.x;
+            ss2 += r.y * r.y;
+            ss2 += r.z * r.z;
+            ss2 += r.w * r.w;
+        }
+        const float inv2 = rms_inv(block_sum(ss2, sh), k, pr.eps);
+        uint2* xb = reinterpret_cast<uint2*>(xs + (size_t)b * k);
+        for (int g = tid; g < n4; g += nt) {
+            const float4 r = yb[g];
+            const uint2 c3 = w2s[g];
+            const uint2 h = make_uint2(pack(rms_scale(r.x, inv2, lo(c3.x)), rms_scale(r.y, inv2, hi(c3.x))),
+                                       pack(rms_scale(r.z, inv2, lo(c3.y)), rms_scale(r.w, inv2, hi(c3.y))));
+            xb[g] = h;
+            if (writer) {
+                reinterpret_cast<uint2*>(pr.res_out + (int64_t)b * K)[g] = make_uint2(pack(r.x, r.y), pack(r.z, r.w));
+                reinterpret_cast<uint2*>(pr.h_out + (int64_t)b * K)[g] = h;
+            }
+        }
+    }
+    __syncthreads();
 }
 
 // The decode-step work of GemvEpilogue, run by the block that has just
@@ -310,11 +407,14 @@ struct Round {
     RawLoads r[RAW ? G : 1];
 };
 
-template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC>
+template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC, bool XN>
 __global__ __launch_bounds__(gemv_max_threads(B, XF32, RAW, G, PF, GENERIC))
 __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(GemvGroupArgs ga) {
     SE12_DECLARE_LUT(lut);
-    extern __shared__ __attribute__((aligned(16))) float red[];
+    extern __shared__ __attribute__((aligned(16))) float dyn[];
+    // dynamic LDS: [x of the prologue (XN), 16-byte aligned] then the reductions
+    uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
+    float* red = XN ? dyn + lds_align16(gemv_pro_x_bytes(ga.m[0].K, B)) / sizeof(float) : dyn;
     // the block's matrix (wave-uniform) and its tile row
     int mi = 0;
 #pragma unroll
@@ -352,7 +452,7 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
             load_side(rd.side, a.side, row_tiles + tile_at(r * G + ((int)(lane >> 4) < G ? (int)(lane >> 4) : G - 1)), lane);
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) load_x<B, XF32, GENERIC>(rd.x[g], a, tile_at(r * G + g), lane);
+        for (int g = 0; g < G; ++g) load_x<B, XF32, GENERIC, XN>(rd.x[g], a, tile_at(r * G + g), lane, xs);
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             const int kt = tile_at(r * G + g);
@@ -361,6 +461,23 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
             else
                 load_tile(rd.t[g], a.sm, a.ec, row_tiles + kt, lane);
         }
+    };
+    // the first round of an XN launch: weights before the prologue, x after it
+    auto load_round_w = [&](Round<B, XF32, RAW, G>& rd, int r) {
+        if constexpr (!RAW)
+            load_side(rd.side, a.side, row_tiles + tile_at(r * G + ((int)(lane >> 4) < G ? (int)(lane >> 4) : G - 1)), lane);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const int kt = tile_at(r * G + g);
+            if constexpr (RAW)
+                load_raw_tile<GENERIC>(rd.r[g], a, tr, kt, lane);
+            else
+                load_tile(rd.t[g], a.sm, a.ec, row_tiles + kt, lane);
+        }
+    };
+    auto load_round_x = [&](Round<B, XF32, RAW, G>& rd, int r) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) load_x<B, XF32, GENERIC, XN>(rd.x[g], a, tile_at(r * G + g), lane, xs);
     };
     auto use_round = [&](const Round<B, XF32, RAW, G>& rd, int r) {
 #pragma unroll
@@ -380,10 +497,23 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
     if constexpr (!RAW) lutv = reinterpret_cast<const uint4*>(a.lut)[lane];
     __builtin_amdgcn_sched_barrier(0);  // the table load goes out first
     Round<B, XF32, RAW, G> r0, r1;
-    load_round(r0, 0);
-    if constexpr (!RAW) {
-        store_block_lut(lut, lutv, lane);
-        lds_barrier();
+    if constexpr (XN) {
+        // the prologue's inputs (straight to LDS) and the first round's
+        // weights go out together; x of the first round after the prologue
+        char* stage = reinterpret_cast<char*>(red) + lds_align16((size_t)W * B * 16 * sizeof(float));
+        gemv_prologue_stage<B>(ga.pro, a.K, stage, w, W, lane);
+        load_round_w(r0, 0);
+        if constexpr (!RAW) store_block_lut(lut, lutv, lane);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged inputs have landed
+        __syncthreads();
+        gemv_prologue_compute<B>(ga.pro, a.K, stage, xs, red);  // ends with a barrier
+        load_round_x(r0, 0);
+    } else {
+        load_round(r0, 0);
+        if constexpr (!RAW) {
+            store_block_lut(lut, lutv, lane);
+            lds_barrier();
+        }
     }
     if constexpr (PF) {
         int r = 0;
@@ -457,10 +587,10 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
 
 namespace {
 
-template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC>
+template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC, bool XN = false>
 hipError_t go(const GemvGroupArgs& a, int threads, int blocks, size_t lds, hipStream_t stream) {
     (void)blocks;
-    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC>), dim3(a.tr_start[a.count], a.m[0].S), dim3(threads), lds,
+    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC, XN>), dim3(a.tr_start[a.count], a.m[0].S), dim3(threads), lds,
                        stream, a);
     return hipGetLastError();
 }
@@ -468,6 +598,9 @@ hipError_t go(const GemvGroupArgs& a, int threads, int blocks, size_t lds, hipSt
 template <int B, bool RAW>
 hipError_t launch_b(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream) {
     const int threads = p.waves * 64;
+    if (p.xn)
+        return p.pf ? go<B, false, RAW, 1, true, false, true>(a, threads, p.blocks, p.lds, stream)
+                    : go<B, false, RAW, 1, false, false, true>(a, threads, p.blocks, p.lds, stream);
     if (p.generic)
         return p.xf32 ? go<B, true, RAW, 1, false, true>(a, threads, p.blocks, p.lds, stream)
                       : go<B, false, RAW, 1, false, true>(a, threads, p.blocks, p.lds, stream);

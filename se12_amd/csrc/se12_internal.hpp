@@ -52,13 +52,43 @@ struct GemvEpilogue {
     uint16_t* out;            // [B, N] BF16
 };
 
+// Decode-step work done at the head of a dot2 GEMV launch (the XN kernel
+// variants): instead of reading x, every block rebuilds it from the previous
+// product's FP32 output y_prev, for each batch row,
+//   r = bf16(residual_in + norm(bf16(y_prev), w1)),  x = norm(r, w2)
+// (norm(t, w) = t * rsqrt(mean(t^2) + eps) * (1 + w)), into LDS; block
+// (0, 0) also writes r to residual_out and x to h_out. residual_in and
+// residual_out must not overlap (the launch's other blocks still read
+// residual_in).
+struct GemvPrologue {
+    const float* y_prev;      // [B, K]
+    const uint16_t* w1;       // [K] BF16
+    const uint16_t* w2;       // [K] BF16
+    const uint16_t* res_in;   // [B, K] BF16
+    uint16_t* res_out;        // [B, K] BF16
+    uint16_t* h_out;          // [B, K] BF16
+    float eps;
+};
+
 struct GemvGroupArgs {
     GemvArgs m[kMaxGroup];
     int32_t tr_start[kMaxGroup + 1];
     int32_t count;
     int32_t rows_per_block;   // MFMA: tile rows per block (waves = rows x K groups)
     GemvEpilogue epi;         // dot2 launches only
+    GemvPrologue pro;         // XN variants only
 };
+
+// Dynamic LDS of an XN launch, in 16-byte aligned pieces: x of the batch
+// rows (BF16), the cross-wave reduction, and the prologue's staged inputs
+// (y_prev FP32 and residual_in BF16 per batch row, w1 and w2).
+constexpr size_t lds_align16(size_t n) { return (n + 15) / 16 * 16; }
+constexpr size_t gemv_pro_x_bytes(int64_t k, int batch) { return (size_t)k * batch * 2; }
+constexpr size_t gemv_pro_stage_bytes(int64_t k, int batch) { return (size_t)k * (batch * 4 + batch * 2 + 4); }
+inline size_t gemv_xn_lds_bytes(int64_t k, int batch, int waves) {
+    return lds_align16(gemv_pro_x_bytes(k, batch)) + lds_align16((size_t)waves * batch * 16 * sizeof(float)) +
+           gemv_pro_stage_bytes(k, batch);
+}
 
 // arrival counters a handle holds: split-K per tile row, the epilogues' per
 // tile row pair and per matrix
@@ -75,6 +105,7 @@ struct GemvPlan {
     bool xf32;
     bool raw;
     bool generic;
+    bool xn;  // x rebuilt by the prologue (GemvPrologue)
     int g;
     int pf;  // rounds in flight ahead of the decoded one (0 or 1)
     int waves;

@@ -258,6 +258,11 @@ class Gemma2Decoder:
                 return torch.empty((batch, n), dtype=dtype, device=dev)
 
             self.x = buf(s.hidden, torch.bfloat16)          # residual stream
+            # the products with the norm in their head write the updated
+            # residual to the other buffer; `residual` is the current one
+            # after a step
+            self.x2 = buf(s.hidden, torch.bfloat16) if self.fused_tails else None
+            self.residual = self.x
             self.h = buf(s.hidden, torch.bfloat16)          # normalised input of the next product
             self.emb = buf(s.hidden, torch.bfloat16)
             self.attn = buf(s.heads * s.head_dim, torch.bfloat16)
@@ -386,36 +391,66 @@ class Gemma2Decoder:
         self.be.embed_into(self.ids, self.emb)
         ck(lib.se12_step_rmsnorm(nat.ptr(self.emb), BF16, s.hidden, nat.ptr(self.w.layers[0]["input_norm"]),
                                  nat.ptr(self.x), None, nat.ptr(self.h), B, s.hidden, s.eps, self.embed_scale_value, 0, st))
-        for li, lw in enumerate(self.w.layers):
-            (q, qo, qs), (k, ko, ks), (v, vo, _) = self.be.grouped_raw(li, ("q", "k", "v"), self.h, self.qkv)
-            ck(lib.se12_step_attention(at(q, qo), at(k, ko), at(v, vo), dt(q), qs, ks, nat.ptr(self.kt[li]),
-                                       nat.ptr(self.v[li]), nat.ptr(self.inv_freq), nat.ptr(self.pos), nat.ptr(self.attn),
-                                       B, s.heads, s.kv_heads, s.head_dim, self.max_len, self.scaling, s.attn_softcap,
-                                       0 if li % 2 else s.sliding_window, nat.ptr(self.attn_ws), self.attn_ws.numel(),
-                                       st))
-            nxt = self.w.layers[li + 1]["input_norm"] if li + 1 < s.layers else self.w.final_norm
-            if self.fused_tails:
-                from .hip import multiply_gelu_mul
-
-                ks = self.be.layers[li]
-                ks["o"].multiply_rmsnorm(self.attn, lw["post_attn_norm"], lw["pre_ffw_norm"], self.x, self.h, s.eps,
-                                         y=self.o_out)
-                multiply_gelu_mul(ks["gate"], ks["up"], self.h, self.m, ys=self.gu)
-                ks["down"].multiply_rmsnorm(self.m, lw["post_ffw_norm"], nxt, self.x, self.h, s.eps, y=self.down_out)
-                continue
-            o = self.be.single_raw(li, "o", self.attn, self.o_out)
-            ck(lib.se12_step_rmsnorm(nat.ptr(o), dt(o), o.shape[1], nat.ptr(lw["post_attn_norm"]), nat.ptr(self.x),
-                                     nat.ptr(lw["pre_ffw_norm"]), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
-            (g, go, gs), (u, uo, _) = self.be.grouped_raw(li, ("gate", "up"), self.h, self.gu)
-            ck(lib.se12_step_gelu_mul(at(g, go), at(u, uo), dt(g), gs, nat.ptr(self.m), B, s.intermediate, st))
-            dn = self.be.single_raw(li, "down", self.m, self.down_out)
-            ck(lib.se12_step_rmsnorm(nat.ptr(dn), dt(dn), dn.shape[1], nat.ptr(lw["post_ffw_norm"]), nat.ptr(self.x),
-                                     nat.ptr(nxt), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
+        if self.fused_tails:
+            self._layers_fused_tails()
+        else:
+            for li, lw in enumerate(self.w.layers):
+                (q, qo, qs), (k, ko, ks), (v, vo, _) = self.be.grouped_raw(li, ("q", "k", "v"), self.h, self.qkv)
+                self._attention(li, at(q, qo), at(k, ko), at(v, vo), dt(q), qs, ks)
+                nxt = self.w.layers[li + 1]["input_norm"] if li + 1 < s.layers else self.w.final_norm
+                o = self.be.single_raw(li, "o", self.attn, self.o_out)
+                ck(lib.se12_step_rmsnorm(nat.ptr(o), dt(o), o.shape[1], nat.ptr(lw["post_attn_norm"]), nat.ptr(self.x),
+                                         nat.ptr(lw["pre_ffw_norm"]), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
+                (g, go, gs), (u, uo, _) = self.be.grouped_raw(li, ("gate", "up"), self.h, self.gu)
+                ck(lib.se12_step_gelu_mul(at(g, go), at(u, uo), dt(g), gs, nat.ptr(self.m), B, s.intermediate, st))
+                dn = self.be.single_raw(li, "down", self.m, self.down_out)
+                ck(lib.se12_step_rmsnorm(nat.ptr(dn), dt(dn), dn.shape[1], nat.ptr(lw["post_ffw_norm"]),
+                                         nat.ptr(self.x), nat.ptr(nxt), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
         lg = self.be.logits_raw(self.h, self.logits_out)
         ck(lib.se12_step_logits_argmax(nat.ptr(lg), dt(lg), lg.shape[1], B, s.vocab, s.final_softcap,
                                        nat.ptr(self.last_logits), nat.ptr(self.ids), nat.ptr(self.tokens), self.max_len,
                                        nat.ptr(self.step_index), nat.ptr(self.logits_ws), self.logits_ws.numel(), st))
         ck(lib.se12_step_advance(nat.ptr(self.pos), nat.ptr(self.step_index), st))
+
+    def _attention(self, li: int, q_ptr: int, k_ptr: int, v_ptr: int, dtype: int, q_stride: int, kv_stride: int) -> None:
+        s = self.s
+        nat.step_check(nat.lib().se12_step_attention(
+            q_ptr, k_ptr, v_ptr, dtype, q_stride, kv_stride, nat.ptr(self.kt[li]), nat.ptr(self.v[li]),
+            nat.ptr(self.inv_freq), nat.ptr(self.pos), nat.ptr(self.attn), self.batch, s.heads, s.kv_heads, s.head_dim,
+            self.max_len, self.scaling, s.attn_softcap, 0 if li % 2 else s.sliding_window, nat.ptr(self.attn_ws),
+            self.attn_ws.numel(), nat.stream_ptr()))
+
+    def _layers_fused_tails(self) -> None:
+        """The layers with the step folded into the library products: every
+        norm but the last in the head of the product that reads it
+        (se12_gemv_prenorm: q/k/v, gate/up), the MLP gate in the gate/up
+        tail, the final norm in the last down_proj's tail. 6 launches per
+        layer: q/k/v, attention (2), o, gate/up, down."""
+        from .hip import multiply_grouped, multiply_prenorm
+
+        s = self.s
+        ra, rb = self.x, self.x2     # the residual, and the buffer its update goes to
+        for li, lw in enumerate(self.w.layers):
+            ks = self.be.layers[li]
+            qkv = [ks["q"], ks["k"], ks["v"]]
+            if li == 0:
+                multiply_grouped(qkv, self.h, outs=self.qkv)
+            else:
+                multiply_prenorm(qkv, self.down_out, self.w.layers[li - 1]["post_ffw_norm"], lw["input_norm"], ra, rb,
+                                 self.h, s.eps, ys=self.qkv)
+                ra, rb = rb, ra
+            q, k, v = self.qkv
+            self._attention(li, q.data_ptr(), k.data_ptr(), v.data_ptr(), nat.STEP_F32, q.shape[1], k.shape[1])
+            ks["o"].multiply(self.attn, out=self.o_out)
+            multiply_prenorm([ks["gate"], ks["up"]], self.o_out, lw["post_attn_norm"], lw["pre_ffw_norm"], ra, rb, self.h,
+                             s.eps, ys=self.gu, gelu_out=self.m)
+            ra, rb = rb, ra
+            if li + 1 < s.layers:
+                ks["down"].multiply(self.m, out=self.down_out)
+            else:
+                ks["down"].multiply_rmsnorm(self.m, lw["post_ffw_norm"], self.w.final_norm, ra, self.h, s.eps,
+                                            y=self.down_out)
+        self.residual = ra
 
     def step(self) -> None:
         """One decode step, eagerly (fused step kernels, or framework ops)."""

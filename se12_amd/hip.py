@@ -252,6 +252,49 @@ def multiply_gelu_mul(gate, up, activations: torch.Tensor, out: torch.Tensor, ys
     return ys
 
 
+def multiply_prenorm(kernels, y_prev: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, residual_in: torch.Tensor,
+                     residual_out: torch.Tensor, h_out: torch.Tensor, eps: float, ys: list[torch.Tensor] | None = None,
+                     gelu_out: torch.Tensor | None = None, launch: LaunchConfiguration | None = None) -> list[torch.Tensor]:
+    """The decoder's next normalised input and its products in one launch
+    (se12_gemv_prenorm): per batch row of the previous product's FP32 output
+    y_prev [B, K], r = bf16(residual_in + norm(bf16(y_prev)) * (1 + w1)),
+    h = norm(r) * (1 + w2); residual_out = r, h_out = h, then y_i = h . W_i^T
+    for up to 4 bound matrices with K columns (and, with gelu_out and two
+    matrices, the MLP gate of `multiply_gelu_mul`). residual_in and
+    residual_out are the same tensor or disjoint. Returns the FP32 y_i."""
+    kernels = list(kernels)
+    if not 1 <= len(kernels) <= nat.MAX_GROUP:
+        raise ValueError(f"1..{nat.MAX_GROUP} matrices per launch, got {len(kernels)}")
+    k0 = kernels[0]
+    for k in kernels:
+        if k.cols != k0.cols or k.device != k0.device or type(k) is not type(k0):
+            raise ValueError("the matrices need one K, one device and one format")
+    if y_prev.dtype != torch.float32 or y_prev.dim() != 2 or y_prev.shape[1] != k0.cols or not y_prev.is_contiguous():
+        raise ValueError(f"y_prev must be a contiguous float32 [B, {k0.cols}] tensor")
+    b = y_prev.shape[0]
+    for t in (w1, w2):
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != (k0.cols,) or not t.is_contiguous() or t.device != k0.device:
+            raise ValueError(f"norm weights must be contiguous bfloat16 [{k0.cols}] on {k0.device}")
+    for t in (residual_in, residual_out, h_out):
+        if t.dtype != torch.bfloat16 or tuple(t.shape) != (b, k0.cols) or not t.is_contiguous() or t.device != k0.device:
+            raise ValueError(f"residuals and h_out must be contiguous bfloat16 [{b}, {k0.cols}] on {k0.device}")
+    ys = [_fp32_out(None, b, k.rows, k0.device) for k in kernels] if ys is None else \
+        [_fp32_out(t, b, k.rows, k0.device) for k, t in zip(kernels, ys)]
+    if gelu_out is not None:
+        if len(kernels) != 2 or kernels[0].rows != kernels[1].rows:
+            raise ValueError("the MLP gate takes two matrices with the same rows")
+        if gelu_out.dtype != torch.bfloat16 or tuple(gelu_out.shape) != (b, k0.rows) or not gelu_out.is_contiguous():
+            raise ValueError(f"gelu_out must be a contiguous bfloat16 [{b}, {k0.rows}] tensor")
+    n = len(kernels)
+    hs = (ctypes.c_void_p * n)(*[k.handle.raw.value for k in kernels])
+    yp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in ys])
+    nat.check(nat.lib().se12_gemv_prenorm(hs, n, nat.ptr(y_prev), b, nat.ptr(w1), nat.ptr(w2), nat.ptr(residual_in),
+                                          nat.ptr(residual_out), nat.ptr(h_out), float(eps), yp,
+                                          None if gelu_out is None else nat.ptr(gelu_out), _launch_struct(launch),
+                                          nat.stream_ptr()))
+    return ys
+
+
 def multiply_grouped(kernels, activations: torch.Tensor, launch: LaunchConfiguration | None = None,
                      outs: list[torch.Tensor] | None = None) -> list[torch.Tensor]:
     """y_i = x . W_i^T for up to 4 bound matrices with the same K (e.g. q, k, v

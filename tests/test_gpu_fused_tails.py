@@ -1,6 +1,6 @@
 """Products with a decode-step tail (se12_gemv_gelu_mul, se12_gemv_rmsnorm)
-against the same product followed by the separate step kernel
-(se12_step_gelu_mul, se12_step_rmsnorm mode 1):
+or head (se12_gemv_prenorm) against the same product with the separate step
+kernel (se12_step_gelu_mul, se12_step_rmsnorm mode 1):
 
 - the FP32 products are bit-identical (same kernel, same launch shape);
 - the MLP gate is element-wise with the same arithmetic: bit-identical;
@@ -177,3 +177,112 @@ def test_tail_arguments_are_checked(gpu):
     w1, w2, res = _norm_inputs(1, 256, gpu, 5)
     with pytest.raises(ValueError):
         k.multiply_rmsnorm(x, w1[:128], w2, res, torch.empty_like(res), 1e-6)
+
+
+def _prenorm_case(gpu, kernels, batch, seed, same_residual=False, launch=None):
+    from se12_amd.hip import multiply_grouped, multiply_prenorm
+
+    K = kernels[0].cols
+    g = _gen(gpu, seed)
+    y_prev = torch.randn((batch, K), generator=g, device=gpu) * 3.0
+    w1, w2, res0 = _norm_inputs(batch, K, gpu, seed + 1)
+    eps = 1e-6
+    want_res, want_h = _separate_norm(y_prev, w1, w2, res0, eps)
+    res_in = res0.clone()
+    res_out = res_in if same_residual else torch.full_like(res0, float("nan"))
+    h = torch.full_like(res0, float("nan"))
+    ys = multiply_prenorm(kernels, y_prev, w1, w2, res_in, res_out, h, eps, launch=launch)
+    torch.cuda.synchronize()
+    _norm_close(res_out, want_res)
+    _norm_close(h, want_h)
+    if not same_residual:
+        assert torch.equal(res_in, res0)
+    # the products are those of the h the launch wrote
+    for got, want in zip(ys, multiply_grouped(kernels, h, launch=launch)):
+        assert torch.equal(got, want)
+    return ys, h
+
+
+@pytest.mark.parametrize("fmt", ["se12", "raw"])
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_prenorm_qkv_shapes(gpu, fmt, batch):
+    """Gemma-2-2B q/k/v (2048/1024/1024 x 2304) from the previous down_proj output."""
+    kernels = [_kernel(2048, 2304, 21, fmt, gpu), _kernel(1024, 2304, 22, fmt, gpu), _kernel(1024, 2304, 23, fmt, gpu)]
+    for call in range(2):
+        _prenorm_case(gpu, kernels, batch, 30 + call)
+
+
+@pytest.mark.parametrize("fmt", ["se12", "raw"])
+def test_prenorm_gate_up_with_the_mlp_gate(gpu, fmt):
+    from se12_amd.hip import multiply_prenorm
+
+    gate, up = _kernel(9216, 2304, 24, fmt, gpu), _kernel(9216, 2304, 25, fmt, gpu)
+    ys, h = _prenorm_case(gpu, [gate, up], 1, 40)
+    g = _gen(gpu, 40)
+    y_prev = torch.randn((1, 2304), generator=g, device=gpu) * 3.0
+    w1, w2, res0 = _norm_inputs(1, 2304, gpu, 41)
+    m = torch.empty((1, 9216), dtype=torch.bfloat16, device=gpu)
+    res_out, h = torch.empty_like(res0), torch.empty_like(res0)
+    ys = multiply_prenorm([gate, up], y_prev, w1, w2, res0, res_out, h, 1e-6, gelu_out=m)
+    want = torch.empty_like(m)
+    nat.step_check(nat.lib().se12_step_gelu_mul(nat.ptr(ys[0]), nat.ptr(ys[1]), nat.STEP_F32, 9216, nat.ptr(want), 1,
+                                                9216, nat.stream_ptr()))
+    torch.cuda.synchronize()
+    assert torch.equal(m, want)
+
+
+@pytest.mark.parametrize("rows,cols,batch,same,waves", [
+    (512, 2304, 1, True, None),    # one residual tensor: the norm runs as its own kernel
+    (256, 1024, 6, False, None),   # MFMA product
+    (200, 700, 2, False, None),    # edge-handling product
+    (512, 2304, 1, False, 1),      # one wave per block
+    (64, 8192, 1, False, None),    # the longest row the norm takes
+    (64, 8192, 4, False, None),    # 4 rows of 8192: more than a block's LDS, separate kernel
+])
+def test_prenorm_separate_kernel_paths(gpu, rows, cols, batch, same, waves):
+    from se12_amd.launch import configuration
+
+    k = _kernel(rows, cols, 50, "se12", gpu)
+    launch = None if waves is None else configuration(waves, 1, rows, batch)
+    _prenorm_case(gpu, [k], batch, 51, same_residual=same, launch=launch)
+
+
+def test_prenorm_replays_in_a_graph(gpu):
+    """Ping-pong residuals over two products (q/k/v then gate/up), captured
+    once and replayed five times against eager calls."""
+    from se12_amd.hip import multiply_prenorm
+
+    qkv = [_kernel(512, 1024, 61, "se12", gpu), _kernel(256, 1024, 62, "se12", gpu)]
+    gu = [_kernel(2048, 1024, 63, "se12", gpu), _kernel(2048, 1024, 64, "se12", gpu)]
+    g = _gen(gpu, 65)
+    y1 = torch.randn((1, 1024), generator=g, device=gpu)
+    y2 = torch.randn((1, 1024), generator=g, device=gpu)
+    w = [(torch.randn(1024, generator=g, device=gpu) * 0.1).to(torch.bfloat16) for _ in range(4)]
+    r0 = torch.randn((1, 1024), generator=g, device=gpu).to(torch.bfloat16)
+    ra, rb, h = r0.clone(), torch.empty_like(r0), torch.empty_like(r0)
+    m = torch.empty((1, 2048), dtype=torch.bfloat16, device=gpu)
+    outs = [[torch.empty((1, k.rows), device=gpu) for k in ks] for ks in (qkv, gu)]
+
+    def step():
+        multiply_prenorm(qkv, y1, w[0], w[1], ra, rb, h, 1e-6, ys=outs[0])
+        multiply_prenorm(gu, y2, w[2], w[3], rb, ra, h, 1e-6, ys=outs[1], gelu_out=m)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(5):
+        ra.copy_(r0)
+        gr.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (ra, rb, h, m, *outs[0], *outs[1])]
+        ra.copy_(r0)
+        step()
+        torch.cuda.synchronize()
+        for a, b in zip(got, (ra, rb, h, m, *outs[0], *outs[1])):
+            assert torch.equal(a, b), rep

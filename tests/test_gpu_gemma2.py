@@ -151,9 +151,10 @@ def test_agrees_with_transformers_gemma2(gpu):
 
 
 def test_fused_tails_agree_with_separate_step_kernels(gpu):
-    """The products with the MLP gate and the residual norms in their tails
-    against the same step with those as separate kernels: layer 0's K/V slot
-    (before any tail) bit-identical, the rest within BF16 rounding."""
+    """The products with the residual norms in their heads and tails and the
+    MLP gate in their tails against the same step with those as separate
+    kernels: layer 0's K/V slot (before any of them) bit-identical, the rest
+    within BF16 rounding."""
     w = Gemma2Weights.random(TINY, gpu, seed=9)
     enc = _encoded(w)
     prompt = _prompt(gpu, 1, 10, seed=5)
@@ -168,4 +169,4 @@ def test_fused_tails_agree_with_separate_step_kernels(gpu):
     a, b = ds
     assert torch.equal(a.kt[0], b.kt[0]) and torch.equal(a.v[0], b.v[0])
     assert _close(a.kt[1][..., 10], b.kt[1][..., 10]) and _close(a.v[1][:, :, 10], b.v[1][:, :, 10])
-    assert _close(a.x, b.x) and _close(a.last_logits, b.last_logits)
+    assert _close(a.residual, b.residual) and _close(a.last_logits, b.last_logits)

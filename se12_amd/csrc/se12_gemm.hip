@@ -10,7 +10,8 @@
 // wave w owns tile row R * row_block + w % R and, of the split's K tiles, the
 // ones of K group w / R (every KG-th tile). blockIdx.y = K split s covering
 // the K tiles [s*TC/S, (s+1)*TC/S). A grouped launch serves up to 4 matrices
-// with the same K: their row blocks follow one another along blockIdx.x.
+// with the same K: blockIdx.z = matrix, blockIdx.x = row block (the grid's x
+// spans the tallest matrix; blocks past a shorter one's rows leave at once).
 //
 // Per step each K group's waves share one copy of their x slab (batch rows x
 // 256 columns, BF16) in LDS, double-buffered: every thread requests up to 4
@@ -227,10 +228,7 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
                                                                                                   int batch) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) char gsm[];
-    int mi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxGroup; ++i) mi += (i < ga.count && (int)blockIdx.x >= ga.tr_start[i]) ? 1 : 0;
-    const GemvArgs& a = ga.m[mi];
+    const GemvArgs& a = ga.m[blockIdx.z];  // the matrix comes from the grid
     const int threads = blockDim.x;
     const int W = threads >> 6;
     const int R = ga.rows_per_block;
@@ -239,7 +237,8 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     const uint32_t lane = threadIdx.x & 63u;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int kg = w / R;
-    const int tr = ((int)blockIdx.x - ga.tr_start[mi]) * R + (w - kg * R);
+    if ((int)blockIdx.x * R >= a.TR) return;  // past a shorter matrix of a grouped launch
+    const int tr = (int)blockIdx.x * R + (w - kg * R);
     const bool active = tr < a.TR;
     const int trl = active ? tr : a.TR - 1;  // row the loads of an idle wave use
     const int S = a.S;
@@ -437,7 +436,7 @@ namespace {
 
 template <int BG, bool RAW>
 hipError_t gemm_b(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
-    const dim3 grid(a.tr_start[a.count], a.m[0].S), block(p.waves * 64);
+    const dim3 grid(group_grid_x(a), a.m[0].S, a.count), block(p.waves * 64);
     if (p.generic)
         hipLaunchKernelGGL((gemm_kernel<BG, RAW, true>), grid, block, p.lds, stream, a, batch);
     else

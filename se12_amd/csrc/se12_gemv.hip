@@ -11,7 +11,8 @@
 // Grid: block = W wave64s, one (tile row, K split) per block: blockIdx.x =
 // tile row, blockIdx.y = split s, covering the K tiles [s*TC/S, (s+1)*TC/S).
 // A grouped launch serves up to 4 matrices with the same K (q/k/v, gate/up)
-// that share x: their tile rows follow one another along blockIdx.x.
+// that share x: blockIdx.z = matrix, and the grid's x spans the tallest one
+// (blocks past a shorter matrix's tile rows leave at once).
 // Wave w of a block takes the split's tiles w, w + W, w + 2W, ... so in each
 // round the block's waves read W consecutive tiles (contiguous HBM). The
 // launch shape (W, S) alone fixes every accumulation order.
@@ -134,7 +135,7 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
     const uint2* rs = reinterpret_cast<const uint2*>(stage + (size_t)B * k * 4);
     const uint2* w1s = reinterpret_cast<const uint2*>(stage + (size_t)B * k * 6);
     const uint2* w2s = w1s + n4;
-    const bool writer = blockIdx.x == 0 && blockIdx.y == 0;
+    const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
     auto lo = [](uint32_t u) { return bf16_to_f(u & 0xFFFFu); };
     auto hi = [](uint32_t u) { return bf16_to_f(u >> 16); };
     auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
@@ -412,16 +413,29 @@ __global__ __launch_bounds__(gemv_max_threads(B, XF32, RAW, G, PF, GENERIC))
 __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(GemvGroupArgs ga) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) float dyn[];
+    // The block's matrix and tile row come from the grid, and every argument
+    // the block needs goes out in one batch of scalar loads (the compiler
+    // would otherwise issue each where it is first used, one waiting behind
+    // the other, and a load issued at the tail would hold the last stores).
+    const GemvArgs a = ga.m[blockIdx.z];
+    const int epi_kind = ga.epi.kind;
+    const int threads = (int)blockDim.x;  // an implicit argument, also a scalar load
+    GemvPrologue pro{};
+    if constexpr (XN) {
+        pro = ga.pro;
+        asm volatile("" ::"s"(a.sm), "s"(a.ec), "s"(a.lut), "s"(a.side), "s"(a.wraw), "s"(a.x), "s"(a.y), "s"(a.K),
+                     "s"(a.TR), "s"(a.TC), "s"(a.S), "s"(epi_kind), "s"(threads), "s"(pro.y_prev), "s"(pro.res_in),
+                     "s"(pro.w1), "s"(pro.w2));
+    } else {
+        asm volatile("" ::"s"(a.sm), "s"(a.ec), "s"(a.lut), "s"(a.side), "s"(a.wraw), "s"(a.x), "s"(a.y), "s"(a.K),
+                     "s"(a.TR), "s"(a.TC), "s"(a.S), "s"(epi_kind), "s"(threads));
+    }
+    const int tr = (int)blockIdx.x;
+    if (tr >= a.TR) return;  // past a shorter matrix of a grouped launch
     // dynamic LDS: [x of the prologue (XN), 16-byte aligned] then the reductions
     uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
-    float* red = XN ? dyn + lds_align16(gemv_pro_x_bytes(ga.m[0].K, B)) / sizeof(float) : dyn;
-    // the block's matrix (wave-uniform) and its tile row
-    int mi = 0;
-#pragma unroll
-    for (int i = 1; i < kMaxGroup; ++i) mi += (i < ga.count && (int)blockIdx.x >= ga.tr_start[i]) ? 1 : 0;
-    const GemvArgs& a = ga.m[mi];
-    const int tr = (int)blockIdx.x - ga.tr_start[mi];
-    const int W = blockDim.x >> 6;
+    float* red = XN ? dyn + lds_align16(gemv_pro_x_bytes(a.K, B)) / sizeof(float) : dyn;
+    const int W = threads >> 6;
     const uint32_t lane = threadIdx.x & 63u;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int S = a.S;
@@ -501,12 +515,12 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         // the prologue's inputs (straight to LDS) and the first round's
         // weights go out together; x of the first round after the prologue
         char* stage = reinterpret_cast<char*>(red) + lds_align16((size_t)W * B * 16 * sizeof(float));
-        gemv_prologue_stage<B>(ga.pro, a.K, stage, w, W, lane);
+        gemv_prologue_stage<B>(pro, a.K, stage, w, W, lane);
         load_round_w(r0, 0);
         if constexpr (!RAW) store_block_lut(lut, lutv, lane);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged inputs have landed
         __syncthreads();
-        gemv_prologue_compute<B>(ga.pro, a.K, stage, xs, red);  // ends with a barrier
+        gemv_prologue_compute<B>(pro, a.K, stage, xs, red);  // ends with a barrier
         load_round_x(r0, 0);
     } else {
         load_round(r0, 0);
@@ -552,7 +566,7 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
     if (tid < 16 * B) {
         for (int ww = 0; ww < W; ++ww) v += red[(ww * B + b) * 16 + rr];
     }
-    const bool epi = ga.epi.kind != kEpiNone;
+    const bool epi = epi_kind != kEpiNone;
     if (S > 1) {
         // Cross-block reduction without cache-wide maintenance: the partials
         // are written with device-scope stores, each thread waits for its
@@ -590,7 +604,7 @@ namespace {
 template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC, bool XN = false>
 hipError_t go(const GemvGroupArgs& a, int threads, int blocks, size_t lds, hipStream_t stream) {
     (void)blocks;
-    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC, XN>), dim3(a.tr_start[a.count], a.m[0].S), dim3(threads), lds,
+    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC, XN>), dim3(group_grid_x(a), a.m[0].S, a.count), dim3(threads), lds,
                        stream, a);
     return hipGetLastError();
 }

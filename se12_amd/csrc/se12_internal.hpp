@@ -79,6 +79,14 @@ struct GemvGroupArgs {
     GemvPrologue pro;         // XN variants only
 };
 
+// The launch grid of a group: x = the tallest matrix's tile rows (row blocks
+// for the MFMA kernel), y = K splits, z = matrix.
+inline int32_t group_grid_x(const GemvGroupArgs& a) {
+    int32_t x = 0;
+    for (int i = 0; i < a.count; ++i) x = a.tr_start[i + 1] - a.tr_start[i] > x ? a.tr_start[i + 1] - a.tr_start[i] : x;
+    return x;
+}
+
 // Dynamic LDS of an XN launch, in 16-byte aligned pieces: x of the batch
 // rows (BF16), the cross-wave reduction, and the prologue's staged inputs
 // (y_prev FP32 and residual_in BF16 per batch row, w1 and w2).

@@ -228,10 +228,15 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
                                                                                                   int batch) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) char gsm[];
-    const GemvArgs& a = ga.m[blockIdx.z];  // the matrix comes from the grid
+    // the matrix comes from the grid; every argument the block needs goes out
+    // in one batch of scalar loads (issued where first used, each would wait
+    // behind the one before)
+    const GemvArgs a = ga.m[blockIdx.z];
     const int threads = blockDim.x;
-    const int W = threads >> 6;
     const int R = ga.rows_per_block;
+    asm volatile("" ::"s"(a.sm), "s"(a.ec), "s"(a.lut), "s"(a.side), "s"(a.wraw), "s"(a.x), "s"(a.y), "s"(a.K),
+                 "s"(a.TR), "s"(a.TC), "s"(a.S), "s"(R), "s"(threads), "s"(batch));
+    const int W = threads >> 6;
     const int KG = W / R;
     const int tid = threadIdx.x;
     const uint32_t lane = threadIdx.x & 63u;

@@ -38,6 +38,15 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source flags. The GEMV kernels take matrix 0's hot arguments as their
+# first 9 kernel arguments and have the dispatch preload them into SGPRs
+# (gfx950 kernarg preload; LLVM also emits the load sequence for firmware
+# without it), so their first tile loads need no kernel-argument round trip.
+SOURCE_FLAGS = {
+    "se12_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
+}
+
+
 def spilling_kernels(remarks: str) -> list[str]:
     """Kernels that hipcc's resource-usage remarks report as spilling VGPRs or
     using scratch memory: a launch bound set too high for the variant. (SGPR
@@ -76,7 +85,8 @@ def build(verbose: bool = False) -> pathlib.Path:
     for src in SOURCES:
         obj = objdir / (src + ".o")
         objects.append(obj)
-        cmd = [cc, *HIP_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src), "-o", str(obj)]
+        cmd = [cc, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), "-Rpass-analysis=kernel-resource-usage", "-c", str(CSRC / src),
+               "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))

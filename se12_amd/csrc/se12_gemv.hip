@@ -408,34 +408,69 @@ struct Round {
     RawLoads r[RAW ? G : 1];
 };
 
+// The leading arguments hold matrix 0's hot arguments (the weight stream
+// pointer: sm, or W for the raw twin; ec, side records, pair table, x; tile
+// columns, K splits, tile rows; waves per block). The library is built with
+// those 9 arguments preloaded into SGPRs by the dispatch, so a block of
+// matrix 0 issues its first tile loads without waiting for a kernel-argument
+// load; the rest of the arguments (and every argument of matrices 1..3)
+// arrive by scalar loads.
 template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC, bool XN>
 __global__ __launch_bounds__(gemv_max_threads(B, XF32, RAW, G, PF, GENERIC))
-__attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(GemvGroupArgs ga) {
+__attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))) void gemv_kernel(
+    const void* w0, const uint8_t* ec0, const uint32_t* side0, const uint32_t* lut0, const void* x0, int32_t TC0,
+    int32_t S0, int32_t TR0, int32_t W, GemvGroupArgs ga) {
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) float dyn[];
-    // The block's matrix and tile row come from the grid, and every argument
-    // the block needs goes out in one batch of scalar loads (the compiler
-    // would otherwise issue each where it is first used, one waiting behind
-    // the other, and a load issued at the tail would hold the last stores).
-    const GemvArgs a = ga.m[blockIdx.z];
-    const int epi_kind = ga.epi.kind;
-    const int threads = (int)blockDim.x;  // an implicit argument, also a scalar load
+    // the block's matrix and tile row come from the grid
+    const int z = blockIdx.z;
+    const GemvArgs& m = ga.m[z];
+    GemvArgs a = {};
+    if (z == 0) {
+        if constexpr (RAW)
+            a.wraw = static_cast<const uint16_t*>(w0);
+        else
+            a.sm = static_cast<const uint8_t*>(w0);
+        a.ec = ec0;
+        a.side = side0;
+        a.lut = lut0;
+        a.x = x0;
+        a.TC = TC0;
+        a.S = S0;
+        a.TR = TR0;
+    } else {
+        // one batch of scalar loads (issued where first used, each would wait
+        // behind the one before)
+        a.sm = m.sm;
+        a.wraw = m.wraw;
+        a.ec = m.ec;
+        a.side = m.side;
+        a.lut = m.lut;
+        a.x = m.x;
+        a.TC = m.TC;
+        a.S = m.S;
+        a.TR = m.TR;
+        asm volatile("" ::"s"(a.sm), "s"(a.wraw), "s"(a.ec), "s"(a.side), "s"(a.lut), "s"(a.x), "s"(a.TC), "s"(a.S),
+                     "s"(a.TR));
+    }
+    a.fb_raw = m.fb_raw;
+    a.ovf_raw = m.ovf_raw;
+    a.y = m.y;
+    a.partial = m.partial;
+    a.counters = m.counters;
+    a.N = m.N;
+    a.K = m.K;
+    a.Np = m.Np;
     GemvPrologue pro{};
     if constexpr (XN) {
-        pro = ga.pro;
-        asm volatile("" ::"s"(a.sm), "s"(a.ec), "s"(a.lut), "s"(a.side), "s"(a.wraw), "s"(a.x), "s"(a.y), "s"(a.K),
-                     "s"(a.TR), "s"(a.TC), "s"(a.S), "s"(epi_kind), "s"(threads), "s"(pro.y_prev), "s"(pro.res_in),
-                     "s"(pro.w1), "s"(pro.w2));
-    } else {
-        asm volatile("" ::"s"(a.sm), "s"(a.ec), "s"(a.lut), "s"(a.side), "s"(a.wraw), "s"(a.x), "s"(a.y), "s"(a.K),
-                     "s"(a.TR), "s"(a.TC), "s"(a.S), "s"(epi_kind), "s"(threads));
+        pro = ga.pro;  // needed before the first tile: one batch with K
+        asm volatile("" ::"s"(a.K), "s"(pro.y_prev), "s"(pro.res_in), "s"(pro.w1), "s"(pro.w2));
     }
     const int tr = (int)blockIdx.x;
     if (tr >= a.TR) return;  // past a shorter matrix of a grouped launch
     // dynamic LDS: [x of the prologue (XN), 16-byte aligned] then the reductions
     uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
     float* red = XN ? dyn + lds_align16(gemv_pro_x_bytes(a.K, B)) / sizeof(float) : dyn;
-    const int W = threads >> 6;
     const uint32_t lane = threadIdx.x & 63u;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int S = a.S;
@@ -529,6 +564,10 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
             lds_barrier();
         }
     }
+    // the arguments of the tail, loaded while the first tiles are in flight
+    // (a scalar load issued at the tail would hold the last stores)
+    const int epi_kind = ga.epi.kind;
+    asm volatile("" ::"s"(a.y), "s"(a.N), "s"(epi_kind));
     if constexpr (PF) {
         int r = 0;
         while (true) {
@@ -604,8 +643,10 @@ namespace {
 template <int B, bool XF32, bool RAW, int G, bool PF, bool GENERIC, bool XN = false>
 hipError_t go(const GemvGroupArgs& a, int threads, int blocks, size_t lds, hipStream_t stream) {
     (void)blocks;
-    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC, XN>), dim3(group_grid_x(a), a.m[0].S, a.count), dim3(threads), lds,
-                       stream, a);
+    const GemvArgs& m0 = a.m[0];
+    const void* w0 = RAW ? static_cast<const void*>(m0.wraw) : static_cast<const void*>(m0.sm);
+    hipLaunchKernelGGL((gemv_kernel<B, XF32, RAW, G, PF, GENERIC, XN>), dim3(group_grid_x(a), m0.S, a.count), dim3(threads), lds,
+                       stream, w0, m0.ec, m0.side, m0.lut, m0.x, m0.TC, m0.S, m0.TR, threads / 64, a);
     return hipGetLastError();
 }
 

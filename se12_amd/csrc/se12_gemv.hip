@@ -99,8 +99,9 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
 // so the first round's weights go out at the same time); the passes then
 // run out of LDS. Block (0, 0) writes the new residual and x.
 //
-// LDS (16-byte aligned pieces, K % 256 == 0): x [B][K] BF16 (the kernel's
-// x), y [B][K] FP32 (then the residual), residual [B][K] BF16, w1 [K], w2 [K].
+// LDS (16-byte aligned pieces, K % 256 == 0): x [B][K] BF16 (the new
+// residual, then the kernel's x), y [B][K] FP32, residual [B][K] BF16,
+// w1 [K], w2 [K].
 // bytes [0, n) of src into LDS at dst (16-byte aligned, n % 16 == 0), one
 // KiB per wave instruction (lane i: bytes 16 i .. 16 i + 15 of the KiB)
 __device__ __forceinline__ void stage_to_lds(const void* src, void* dst, int n, int w, int W, uint32_t lane) {
@@ -131,7 +132,7 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
     using namespace se12step;
     const int tid = threadIdx.x, nt = blockDim.x;
     const int k = (int)K, n4 = k >> 2;
-    float4* ys = reinterpret_cast<float4*>(stage);
+    const float4* ys = reinterpret_cast<const float4*>(stage);
     const uint2* rs = reinterpret_cast<const uint2*>(stage + (size_t)B * k * 4);
     const uint2* w1s = reinterpret_cast<const uint2*>(stage + (size_t)B * k * 6);
     const uint2* w2s = w1s + n4;
@@ -140,7 +141,7 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
     auto hi = [](uint32_t u) { return bf16_to_f(u >> 16); };
     auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
     for (int b = 0; b < B; ++b) {
-        float4* yb = ys + (size_t)b * n4;
+        const float4* yb = ys + (size_t)b * n4;
         const uint2* rb = rs + (size_t)b * n4;
         float ss = 0.0f;
         for (int g = tid; g < n4; g += nt) {
@@ -152,6 +153,9 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
             ss += t.w * t.w;
         }
         const float inv = rms_inv(block_sum(ss, sh), k, pr.eps);
+        // the new residual (BF16-exact) goes to x's place in LDS, where the
+        // same thread turns it into x
+        uint2* xb = reinterpret_cast<uint2*>(xs + (size_t)b * k);
         float ss2 = 0.0f;
         for (int g = tid; g < n4; g += nt) {
             const float4 v = yb[g];
@@ -161,22 +165,22 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
             r.y = round_bf16(hi(c2.x) + round_bf16(rms_scale(round_bf16(v.y), inv, hi(c1.x))));
             r.z = round_bf16(lo(c2.y) + round_bf16(rms_scale(round_bf16(v.z), inv, lo(c1.y))));
             r.w = round_bf16(hi(c2.y) + round_bf16(rms_scale(round_bf16(v.w), inv, hi(c1.y))));
-            yb[g] = r;  // this thread's own elements: no other thread reads them
+            xb[g] = make_uint2(pack(r.x, r.y), pack(r.z, r.w));
             ss2 += r.x * r.x;
             ss2 += r.y * r.y;
             ss2 += r.z * r.z;
             ss2 += r.w * r.w;
         }
         const float inv2 = rms_inv(block_sum(ss2, sh), k, pr.eps);
-        uint2* xb = reinterpret_cast<uint2*>(xs + (size_t)b * k);
         for (int g = tid; g < n4; g += nt) {
-            const float4 r = yb[g];
+            const uint2 rp = xb[g];
+            const float4 r = make_float4(lo(rp.x), hi(rp.x), lo(rp.y), hi(rp.y));
             const uint2 c3 = w2s[g];
             const uint2 h = make_uint2(pack(rms_scale(r.x, inv2, lo(c3.x)), rms_scale(r.y, inv2, hi(c3.x))),
                                        pack(rms_scale(r.z, inv2, lo(c3.y)), rms_scale(r.w, inv2, hi(c3.y))));
             xb[g] = h;
             if (writer) {
-                reinterpret_cast<uint2*>(pr.res_out + (int64_t)b * K)[g] = make_uint2(pack(r.x, r.y), pack(r.z, r.w));
+                reinterpret_cast<uint2*>(pr.res_out + (int64_t)b * K)[g] = rp;
                 reinterpret_cast<uint2*>(pr.h_out + (int64_t)b * K)[g] = h;
             }
         }

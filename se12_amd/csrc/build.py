@@ -44,6 +44,10 @@ HIP_FLAGS = [
 # without it), so their first tile loads need no kernel-argument round trip.
 SOURCE_FLAGS = {
     "se12_gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
+    # the attention kernels' leading arguments likewise (the position pointer,
+    # q / k / key cache or the softmax statistics, scores and value cache,
+    # and the sizes the first loads' addresses need)
+    "se12_step.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
 }
 
 

@@ -191,6 +191,13 @@ __device__ __forceinline__ int window_lo(int p, int window) {
     return window > 0 ? (p - window + 1 > 0 ? p - window + 1 : 0) : 0;
 }
 
+// a wave-uniform 64-bit value held in a vector register, as a scalar
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 // Makes the wave wait for a loaded value here: issued before a branch on the
 // position, loads would otherwise be sunk past it and wait for it.
 __device__ __forceinline__ void pin(float v) { asm volatile("" ::"v"(v)); }
@@ -299,7 +306,21 @@ __device__ __forceinline__ void chunk_scores(const float* red, const AttnArgs& a
 }
 
 template <int G, int DT>
-__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(const int64_t* pos, const void* q, const void* k,
+                                                                   uint16_t* kt, int32_t d_, int32_t L_, int32_t kvh,
+                                                                   int32_t q_stride, int32_t kv_stride, AttnArgs ga) {
+    // the leading arguments (preloaded into SGPRs by the dispatch) are the
+    // ones the first loads need; the rest arrive by scalar loads meanwhile
+    AttnArgs a = ga;
+    a.pos = pos;
+    a.q = q;
+    a.k = k;
+    a.kt = kt;
+    a.d = d_;
+    a.max_len = L_;
+    a.kvh = kvh;
+    a.q_stride = q_stride;
+    a.kv_stride = kv_stride;
     __shared__ float qk[(G + 1) * kMaxHeadDim];   // rotated q of the G heads, then k
     __shared__ float red[4 * G * kChunk];         // per wave: G x 64 partial dot products
     const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -310,20 +331,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
     const int L = a.max_len;
 
     // Every load whose address does not depend on the position goes out
-    // together with the position's: q, k and v of the new token (to BF16),
-    // the rotary frequency and the chunk of the key cache. Lane group
-    // pg = 8 consecutive positions read as one 16-byte load per head-dim
-    // element; the 32 slices es take every 32nd element.
-    const int64_t p64 = *a.pos;
-    __builtin_amdgcn_sched_barrier(0);  // the position's load goes out first
+    // together with the position's: q and k of the new token (to BF16) and
+    // the chunk of the key cache, all from preloaded arguments; then v and
+    // the rotary frequency, whose pointers are scalar loads. The position is
+    // a vector load, so that waiting for those scalar loads does not wait for
+    // it. Lane group pg = 8 consecutive positions read as one 16-byte load
+    // per head-dim element; the 32 slices es take every 32nd element.
+    const int64_t p64v = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     float xq[G], xk = 0.0f, vv = 0.0f, fr = 0.0f;
     const int tc = t < d ? t : d - 1;
 #pragma unroll
     for (int h = 0; h < G; ++h)
         xq[h] = load_as_bf16<DT>(a.q, (int64_t)b * a.q_stride + (int64_t)(kh * G + h) * d + tc);
     xk = load_as_bf16<DT>(a.k, (int64_t)b * a.kv_stride + (int64_t)kh * d + tc);
-    vv = load_as_bf16<DT>(a.v, (int64_t)b * a.kv_stride + (int64_t)kh * d + tc);
-    fr = a.inv_freq[tc % half];
     const int pg = t & 7, es = t >> 3;
     const int jg = j0 + 8 * pg;
     const int jgl = jg + 8 <= L ? jg : L - 8;     // L % 8 == 0: a group is wholly in or out
@@ -334,13 +354,15 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
         const int e = es + 32 * i;
         raw[i] = *reinterpret_cast<const uint4*>(kb + (int64_t)(e < d ? e : d - 1) * L);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the loads above go out first
+    vv = load_as_bf16<DT>(a.v, (int64_t)b * a.kv_stride + (int64_t)kh * d + tc);
+    fr = a.inv_freq[tc % half];
 #pragma unroll
     for (int h = 0; h < G; ++h) pin(xq[h]);
     pin(xk);
-    pin(vv);
-    pin(fr);
 #pragma unroll
     for (int i = 0; i < kMaxHeadDim / 32; ++i) pin(raw[i]);
+    const int64_t p64 = uniform_i64(p64v);
 
     if (p64 < 0 || p64 >= a.max_len) return;
     const int p = (int)p64, lo = window_lo(p, a.window);
@@ -365,7 +387,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(AttnArgs a) {
         const int64_t lp = (int64_t)a.chunks * kChunk;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            const int64_t row = (int64_t)b * a.heads + kh * G + h;
+            const int64_t row = (int64_t)b * a.kvh * G + kh * G + h;
             a.scores[row * lp + j0 + t] = sc[h];
             if (t == 0) {
                 a.stats[(row * a.chunks + c) * 2 + 0] = m[h];
@@ -384,7 +406,20 @@ template <int G>
 constexpr int pv_span() { return (kAttnThreads / (kPvCols / 8)) * pv_per_thread<G>(); }
 
 template <int G>
-__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const int64_t* pos, const float* stats, const float* scores,
+                                                               const uint16_t* vc, int32_t d_, int32_t L_, int32_t kvh,
+                                                               int32_t chunks, AttnArgs ga) {
+    // the leading arguments (preloaded into SGPRs by the dispatch) are the
+    // ones the first loads need; the rest arrive by scalar loads meanwhile
+    AttnArgs a = ga;
+    a.pos = pos;
+    a.stats = const_cast<float*>(stats);
+    a.scores = const_cast<float*>(scores);
+    a.vc = const_cast<uint16_t*>(vc);
+    a.d = d_;
+    a.max_len = L_;
+    a.kvh = kvh;
+    a.chunks = chunks;
     constexpr int P = pv_per_thread<G>();
     constexpr int kSpan = pv_span<G>();
     __shared__ float ms[2 * G];
@@ -395,8 +430,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
     const int b = kvb / a.kvh, kh = kvb % a.kvh;
     const int cb = blockIdx.y, sp = blockIdx.z;
     const int d = a.d, L = a.max_len;
-    const int64_t obase = (int64_t)b * a.heads * d + (int64_t)kh * G * d;
-    const int64_t row0 = (int64_t)b * a.heads + kh * G;
+    const int64_t obase = (int64_t)b * a.kvh * G * d + (int64_t)kh * G * d;
+    const int64_t row0 = (int64_t)b * a.kvh * G + kh * G;
     const int64_t lp = (int64_t)a.chunks * kChunk;
     // thread: 8-column group cq of the block's 32 columns, position slice ps
     const int cq = t & 3, ps = t >> 2;
@@ -407,8 +442,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
     // Every load whose address does not depend on the position goes out
     // together with the position's: the statistics of the first 64 chunks of
     // the wave's heads (lane = chunk), and the span's V rows and scores.
-    const int64_t p64 = *a.pos;
-    __builtin_amdgcn_sched_barrier(0);  // the position's load goes out first
+    const int64_t p64v = __hip_atomic_load(a.pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // a vector load
     constexpr int kHeadsPerWave = (G + 3) / 4;
     float sm[kHeadsPerWave], sl[kHeadsPerWave];
     const int cl = lane < a.chunks ? lane : a.chunks - 1;
@@ -441,6 +475,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(AttnArgs a) {
         for (int h = 0; h < G; ++h) pin(sc[i][h]);
     }
 
+    const int64_t p64 = uniform_i64(p64v);
     if (p64 < 0 || p64 >= L) {  // no cache slot: zeros, no cache or counter touched
         if (cb == 0 && sp == 0)
             for (int i = t; i < G * d; i += kAttnThreads) a.out[obase + i] = 0;
@@ -709,12 +744,16 @@ bool attn_shape_ok(int32_t batch, int32_t heads, int32_t kv_heads, int32_t head_
 template <int G>
 void launch_attention(const AttnArgs& a, int blocks_x, hipStream_t stream) {
     const dim3 grid(blocks_x, a.chunks);
+    const int32_t qs = (int32_t)a.q_stride, kvs = (int32_t)a.kv_stride;
     if (a.dtype == SE12_STEP_F32)
-        hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_F32>), grid, dim3(kAttnThreads), 0, stream, a);
+        hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_F32>), grid, dim3(kAttnThreads), 0, stream, a.pos, a.q, a.k, a.kt,
+                           a.d, a.max_len, a.kvh, qs, kvs, a);
     else
-        hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_BF16>), grid, dim3(kAttnThreads), 0, stream, a);
+        hipLaunchKernelGGL((attn_scores_kernel<G, SE12_STEP_BF16>), grid, dim3(kAttnThreads), 0, stream, a.pos, a.q, a.k,
+                           a.kt, a.d, a.max_len, a.kvh, qs, kvs, a);
     const dim3 pv_grid(blocks_x, (a.d + kPvCols - 1) / kPvCols, (a.max_len + pv_span<G>() - 1) / pv_span<G>());
-    hipLaunchKernelGGL(attn_pv_kernel<G>, pv_grid, dim3(kAttnThreads), 0, stream, a);
+    hipLaunchKernelGGL(attn_pv_kernel<G>, pv_grid, dim3(kAttnThreads), 0, stream, a.pos, a.stats, a.scores, a.vc, a.d,
+                       a.max_len, a.kvh, a.chunks, a);
 }
 
 struct ArgmaxLayout {
@@ -779,7 +818,7 @@ int se12_step_attention(const void* q, const void* k, const void* v, int32_t dty
     if (!q || !k || !v || !k_cache_t || !v_cache || !inv_freq || !pos || !out || !workspace || !dtype_ok(dtype))
         return step_fail("se12_step_attention: NULL argument or bad dtype");
     if (!attn_shape_ok(batch, heads, kv_heads, head_dim, max_len) || q_stride < (int64_t)heads * head_dim ||
-        kv_stride < (int64_t)kv_heads * head_dim)
+        kv_stride < (int64_t)kv_heads * head_dim || q_stride > INT32_MAX || kv_stride > INT32_MAX)
         return step_fail("se12_step_attention: bad shape");
     if (!aligned16(k_cache_t) || !aligned16(v_cache)) return step_fail("se12_step_attention: caches not 16-byte aligned");
     const AttnLayout l = attn_layout(batch, heads, kv_heads, head_dim, max_len);

@@ -99,9 +99,9 @@ __device__ __forceinline__ void store_dev(float* p, float v) {
 // so the first round's weights go out at the same time); the passes then
 // run out of LDS. Block (0, 0) writes the new residual and x.
 //
-// LDS (16-byte aligned pieces, K % 256 == 0): x [B][K] BF16 (the new
-// residual, then the kernel's x), y [B][K] FP32, residual [B][K] BF16,
-// w1 [K], w2 [K].
+// LDS (after the kernel's reduction area; 16-byte aligned pieces,
+// K % 256 == 0): y [B][K] FP32, residual [B][K] BF16, w1 [K], w2 [K], then
+// x [B][K] BF16 (the new residual, then the kernel's x).
 // bytes [0, n) of src into LDS at dst (16-byte aligned, n % 16 == 0), one
 // KiB per wave instruction (lane i: bytes 16 i .. 16 i + 15 of the KiB)
 __device__ __forceinline__ void stage_to_lds(const void* src, void* dst, int n, int w, int W, uint32_t lane) {
@@ -457,24 +457,29 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         asm volatile("" ::"s"(a.sm), "s"(a.wraw), "s"(a.ec), "s"(a.side), "s"(a.lut), "s"(a.x), "s"(a.TC), "s"(a.S),
                      "s"(a.TR));
     }
-    a.fb_raw = m.fb_raw;
-    a.ovf_raw = m.ovf_raw;
-    a.y = m.y;
-    a.partial = m.partial;
-    a.counters = m.counters;
-    a.N = m.N;
-    a.K = m.K;
-    a.Np = m.Np;
-    GemvPrologue pro{};
-    if constexpr (XN) {
-        pro = ga.pro;  // needed before the first tile: one batch with K
-        asm volatile("" ::"s"(a.K), "s"(pro.y_prev), "s"(pro.res_in), "s"(pro.w1), "s"(pro.w2));
-    }
+    // the other arguments: loaded once the first tiles are in flight, except
+    // where the first loads' addresses need K and N (raw twin, edge handling)
+    auto load_cold = [&]() {
+        a.fb_raw = m.fb_raw;
+        a.ovf_raw = m.ovf_raw;
+        a.y = m.y;
+        a.partial = m.partial;
+        a.counters = m.counters;
+        a.N = m.N;
+        a.K = m.K;
+        a.Np = m.Np;
+    };
+    constexpr bool kEarlyCold = RAW || GENERIC || B > 1;
+    if constexpr (kEarlyCold) load_cold();
     const int tr = (int)blockIdx.x;
     if (tr >= a.TR) return;  // past a shorter matrix of a grouped launch
     // dynamic LDS: [x of the prologue (XN), 16-byte aligned] then the reductions
-    uint16_t* xs = reinterpret_cast<uint16_t*>(dyn);
-    float* red = XN ? dyn + lds_align16(gemv_pro_x_bytes(a.K, B)) / sizeof(float) : dyn;
+    // dynamic LDS: the reductions, then (XN) the prologue's staged inputs and
+    // x, whose offsets depend on K (a scalar load): computed where first used
+    float* red = dyn;
+    char* const stage = reinterpret_cast<char*>(dyn) + lds_align16((size_t)W * B * 16 * sizeof(float));
+    auto x_lds = [&]() { return reinterpret_cast<uint16_t*>(stage + gemv_pro_stage_bytes(a.K, B)); };
+    uint16_t* xs = nullptr;
     const uint32_t lane = threadIdx.x & 63u;
     const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int S = a.S;
@@ -553,16 +558,21 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
     if constexpr (XN) {
         // the prologue's inputs (straight to LDS) and the first round's
         // weights go out together; x of the first round after the prologue
-        char* stage = reinterpret_cast<char*>(red) + lds_align16((size_t)W * B * 16 * sizeof(float));
-        gemv_prologue_stage<B>(pro, a.K, stage, w, W, lane);
+        // the first round's weights from the preloaded arguments, then the
+        // prologue's inputs once their pointers (scalar loads) are in
         load_round_w(r0, 0);
+        if constexpr (!kEarlyCold) load_cold();
+        const GemvPrologue pro = ga.pro;
+        gemv_prologue_stage<B>(pro, a.K, stage, w, W, lane);
         if constexpr (!RAW) store_block_lut(lut, lutv, lane);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the staged inputs have landed
         __syncthreads();
+        xs = x_lds();
         gemv_prologue_compute<B>(pro, a.K, stage, xs, red);  // ends with a barrier
         load_round_x(r0, 0);
     } else {
         load_round(r0, 0);
+        if constexpr (!kEarlyCold) load_cold();
         if constexpr (!RAW) {
             store_block_lut(lut, lutv, lane);
             lds_barrier();

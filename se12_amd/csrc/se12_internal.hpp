@@ -87,9 +87,9 @@ inline int32_t group_grid_x(const GemvGroupArgs& a) {
     return x;
 }
 
-// Dynamic LDS of an XN launch, in 16-byte aligned pieces: x of the batch
-// rows (BF16), the cross-wave reduction, and the prologue's staged inputs
-// (y_prev FP32 and residual_in BF16 per batch row, w1 and w2).
+// Dynamic LDS of an XN launch, in 16-byte aligned pieces: the cross-wave
+// reduction, the prologue's staged inputs (y_prev FP32 and residual_in BF16
+// per batch row, w1 and w2), and x of the batch rows (BF16).
 constexpr size_t lds_align16(size_t n) { return (n + 15) / 16 * 16; }
 constexpr size_t gemv_pro_x_bytes(int64_t k, int batch) { return (size_t)k * batch * 2; }
 constexpr size_t gemv_pro_stage_bytes(int64_t k, int batch) { return (size_t)k * (batch * 4 + batch * 2 + 4); }

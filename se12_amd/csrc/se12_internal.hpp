@@ -24,9 +24,10 @@ struct GemvArgs {
     int32_t S;                // K splits per tile row
 };
 
-// One launch over up to kMaxGroup matrices that share x (same K): the grid's
-// rows are the matrices' tile rows one after another, matrix i starting at
-// grid row tr_start[i] (tr_start[count] = the grid's rows).
+// One launch over up to kMaxGroup matrices that share x (same K): the
+// kernels take the matrix from blockIdx.z; tr_start[i] counts the grid rows
+// (tile rows, or MFMA row blocks) of the matrices before i, tr_start[count]
+// their total (the launch's `blocks` = that total x K splits).
 constexpr int kMaxGroup = 4;
 
 // Decode-step work done at the tail of a dot2 GEMV launch by the block that
@@ -198,7 +199,8 @@ hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t st
 // loads each x slab (batch x 256 BF16) with at most kGemmXPieces 16-byte
 // pieces per thread, so it needs at least batch / 8 waves; at most
 // kGemmMaxSplits K splits. The grid's x dimension counts row blocks
-// (ceil(tile rows / waves) per matrix), and tr_start is in those units.
+// (ceil(tile rows / rows per block) per matrix), and tr_start is in those
+// units.
 constexpr int kGemmMinBatch = 5;
 constexpr int kGemmMaxThreads = 512;
 // the edge-handling (GENERIC) MFMA variants, whose element-wise loads need

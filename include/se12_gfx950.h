@@ -188,6 +188,15 @@ int se12_gemv_rmsnorm(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_
                       const uint16_t* w1_dev, const uint16_t* w2_dev, uint16_t* residual_dev, uint16_t* out_dev,
                       float eps, const se12_launch* launch, void* stream);
 
+/* se12_gemv with the sums of squares of the output's tile rows (no reference
+ * counterpart; for the decoder's norms): y as se12_gemv, and
+ * row_ss[b, t] = sum over the 16 rows n of tile row t of bf16(y[b, n])^2
+ * (FP32 [batch, tile rows]), written by the blocks completing each tile row
+ * (dot2 launches) or by a small kernel after the product (MFMA launches).
+ * Same stream, allocation and ordering rules as se12_gemv. */
+int se12_gemv_rowss(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch, float* y_dev,
+                    float* row_ss_dev, const se12_launch* launch, void* stream);
+
 /* The product of the decoder's next normalised input, with the norm in the
  * product's head (no reference counterpart; same motivation as above): for
  * each batch row, from the previous product's FP32 output y_prev [batch,
@@ -204,9 +213,13 @@ int se12_gemv_rmsnorm(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_
  * + 4) bytes, every block of the product rebuilds h in LDS (sums of squares
  * over its threads) and block (0, 0) writes residual_out and h_out;
  * otherwise the norm runs as its own kernel (se12_step_rmsnorm mode 1)
- * before the product. Same stream, allocation and ordering rules as
+ * before the product. y_prev_ss: NULL, or the tile-row sums of squares of
+ * y_prev that se12_gemv_rowss wrote with it (FP32 [batch, ceil(cols / 16)]);
+ * the fused head then takes the first norm's mean from them instead of a
+ * pass over y_prev. Same stream, allocation and ordering rules as
  * se12_gemv. */
-int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y_prev_dev, int32_t batch,
+int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y_prev_dev, const float* y_prev_ss_dev,
+                      int32_t batch,
                       const uint16_t* w1_dev, const uint16_t* w2_dev, const uint16_t* residual_in_dev,
                       uint16_t* residual_out_dev, uint16_t* h_out_dev, float eps, float* const* y_dev,
                       uint16_t* gelu_out_dev, const se12_launch* launch, void* stream);

@@ -121,8 +121,11 @@ SIGNATURES = {
     ),
     "se12_gemv_prenorm": (
         c_i32,
-        [ctypes.POINTER(c_void_p), c_i32, c_void_p, c_i32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         ctypes.c_float, ctypes.POINTER(c_void_p), c_void_p, ctypes.POINTER(Launch), c_void_p],
+        [ctypes.POINTER(c_void_p), c_i32, c_void_p, c_void_p, c_i32, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, ctypes.c_float, ctypes.POINTER(c_void_p), c_void_p, ctypes.POINTER(Launch), c_void_p],
+    ),
+    "se12_gemv_rowss": (
+        c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, c_void_p, ctypes.POINTER(Launch), c_void_p],
     ),
     "se12_decode": (c_i32, [c_void_p, c_void_p, c_void_p]),
     "se12_decode_rows": (c_i32, [c_void_p, c_void_p, c_i64, c_void_p, c_void_p]),

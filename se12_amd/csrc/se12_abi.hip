@@ -553,6 +553,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         if (fuse_pro) {
             g.pro = *pro;
             g.pro.y_prev += (size_t)b0 * h0->K;
+            if (g.pro.y_prev_ss) g.pro.y_prev_ss += (size_t)b0 * ceil_div(h0->K, SE12_TILE_ROWS);
             g.pro.res_in += (size_t)b0 * h0->K;
             g.pro.res_out += (size_t)b0 * h0->K;
             g.pro.h_out += (size_t)b0 * h0->K;
@@ -561,8 +562,9 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         }
         if (fuse_epi) {
             g.epi = *epi;
-            g.epi.out += (size_t)b0 * h0->N;
+            if (g.epi.out) g.epi.out += (size_t)b0 * h0->N;
             if (g.epi.residual) g.epi.residual += (size_t)b0 * h0->N;
+            if (g.epi.row_ss) g.epi.row_ss += (size_t)b0 * h0->TR;
             if (epi->kind == kEpiRmsNorm) p.lds = std::max(p.lds, gemv_norm_lds_bytes(h0->N));
         }
         if ((int64_t)(p.lds + kLutBytes) > h0->lds_per_block)
@@ -573,11 +575,17 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     }
     if (epi && !fuse_epi) {
         // the step runs as its own kernel after the product
-        const int rc = epi->kind == kEpiGeluMul
-                           ? se12_step_gelu_mul(ys[0], ys[1], SE12_STEP_F32, h0->N, epi->out, batch, (int32_t)h0->N, st)
-                           : se12_step_rmsnorm(ys[0], SE12_STEP_F32, h0->N, epi->w1, epi->residual, epi->w2, epi->out,
-                                               batch, (int32_t)h0->N, epi->eps, 0.0f, 1, st);
-        if (rc != SE12_STEP_OK) return fail(SE12_E_HIP, "%s step: %s", fn, se12_step_last_error());
+        if (epi->row_ss) {
+            const hipError_t e = launch_row_sumsq(ys[0], h0->N, h0->TR, batch, epi->row_ss, st);
+            if (e != hipSuccess) return fail(SE12_E_HIP, "%s row sums: %s", fn, hipGetErrorString(e));
+        }
+        if (epi->kind != kEpiNone) {
+            const int rc = epi->kind == kEpiGeluMul
+                               ? se12_step_gelu_mul(ys[0], ys[1], SE12_STEP_F32, h0->N, epi->out, batch, (int32_t)h0->N, st)
+                               : se12_step_rmsnorm(ys[0], SE12_STEP_F32, h0->N, epi->w1, epi->residual, epi->w2,
+                                                   epi->out, batch, (int32_t)h0->N, epi->eps, 0.0f, 1, st);
+            if (rc != SE12_STEP_OK) return fail(SE12_E_HIP, "%s step: %s", fn, se12_step_last_error());
+        }
     }
     return SE12_OK;
 }
@@ -611,6 +619,17 @@ int se12_gemv_gelu_mul(se12_handle* const* gate_up, const void* x, int32_t x_dty
     return gemv_group("se12_gemv_gelu_mul", gate_up, 2, x, x_dtype, batch, y, launch, stream, &e);
 }
 
+int se12_gemv_rowss(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, float* row_ss,
+                    const se12_launch* launch, void* stream) {
+    if (!h || !y || !row_ss) return fail(SE12_E_INVALID, "se12_gemv_rowss: NULL handle, y or row_ss");
+    GemvEpilogue e{};
+    e.kind = kEpiNone;
+    e.row_ss = row_ss;
+    se12_handle* hs[1] = {h};
+    float* ys[1] = {y};
+    return gemv_group("se12_gemv_rowss", hs, 1, x, x_dtype, batch, ys, launch, stream, &e);
+}
+
 int se12_gemv_rmsnorm(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y, const uint16_t* w1,
                       const uint16_t* w2, uint16_t* residual, uint16_t* out, float eps, const se12_launch* launch,
                       void* stream) {
@@ -631,10 +650,10 @@ int se12_gemv_rmsnorm(se12_handle* h, const void* x, int32_t x_dtype, int32_t ba
     return gemv_group("se12_gemv_rmsnorm", hs, 1, x, x_dtype, batch, ys, launch, stream, &e);
 }
 
-int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y_prev, int32_t batch,
-                      const uint16_t* w1, const uint16_t* w2, const uint16_t* residual_in, uint16_t* residual_out,
-                      uint16_t* h_out, float eps, float* const* y, uint16_t* gelu_out, const se12_launch* launch,
-                      void* stream) {
+int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y_prev, const float* y_prev_ss,
+                      int32_t batch, const uint16_t* w1, const uint16_t* w2, const uint16_t* residual_in,
+                      uint16_t* residual_out, uint16_t* h_out, float eps, float* const* y, uint16_t* gelu_out,
+                      const se12_launch* launch, void* stream) {
     const char* fn = "se12_gemv_prenorm";
     if (!handles || !y || !y_prev || !w1 || !w2 || !residual_in || !residual_out || !h_out)
         return fail(SE12_E_INVALID, "%s: NULL handles, y, y_prev, weights, residuals or h_out", fn);
@@ -651,6 +670,7 @@ int se12_gemv_prenorm(se12_handle* const* handles, int32_t count, const float* y
         return fail(SE12_E_INVALID, "%s: residual_in and residual_out overlap without being the same tensor", fn);
     GemvPrologue pr{};
     pr.y_prev = y_prev;
+    pr.y_prev_ss = y_prev_ss;
     pr.w1 = w1;
     pr.w2 = w2;
     pr.res_in = residual_in;

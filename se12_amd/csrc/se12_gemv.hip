@@ -124,6 +124,16 @@ __device__ __forceinline__ void gemv_prologue_stage(const GemvPrologue& pr, int6
     stage_to_lds(pr.res_in, rs, B * k * 2, w, W, lane);
     stage_to_lds(pr.w1, w1s, k * 2, w, W, lane);
     stage_to_lds(pr.w2, w2s, k * 2, w, W, lane);
+    if (pr.y_prev_ss) {
+        // the producer's per-tile-row sums of squares, 4 bytes per lane
+        const int n = B * ((k + 15) / 16) * 4;
+        char* ss = w2s + (size_t)k * 2;
+        for (int c = w * 256; c < n; c += W * 256) {
+            const int off = c + (int)lane * 4;
+            if (off < n)
+                __builtin_amdgcn_global_load_lds(reinterpret_cast<const char*>(pr.y_prev_ss) + off, ss + c, 4, 0, 0);
+        }
+    }
 }
 
 // after the staged loads have landed (the caller waits and meets the block)
@@ -140,19 +150,31 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
     auto lo = [](uint32_t u) { return bf16_to_f(u & 0xFFFFu); };
     auto hi = [](uint32_t u) { return bf16_to_f(u >> 16); };
     auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
+    const int trp = (k + 15) / 16;
+    const float* row_ss = reinterpret_cast<const float*>(stage + (size_t)B * k * 6 + (size_t)k * 4);
     for (int b = 0; b < B; ++b) {
         const float4* yb = ys + (size_t)b * n4;
         const uint2* rb = rs + (size_t)b * n4;
-        float ss = 0.0f;
-        for (int g = tid; g < n4; g += nt) {
-            const float4 v = yb[g];
-            const float4 t = make_float4(round_bf16(v.x), round_bf16(v.y), round_bf16(v.z), round_bf16(v.w));
-            ss += t.x * t.x;
-            ss += t.y * t.y;
-            ss += t.z * t.z;
-            ss += t.w * t.w;
+        float inv;
+        if (pr.y_prev_ss) {
+            // from the producer's tile-row sums: lane l adds rows l, l + 64,
+            // ... in order, then the wave's DPP tree; every wave gets the
+            // same value, so no block barrier
+            float ss = 0.0f;
+            for (int i = (int)(tid & 63); i < trp; i += 64) ss += row_ss[b * trp + i];
+            inv = rms_inv(wave_sum(ss), k, pr.eps);
+        } else {
+            float ss = 0.0f;
+            for (int g = tid; g < n4; g += nt) {
+                const float4 v = yb[g];
+                const float4 t = make_float4(round_bf16(v.x), round_bf16(v.y), round_bf16(v.z), round_bf16(v.w));
+                ss += t.x * t.x;
+                ss += t.y * t.y;
+                ss += t.z * t.z;
+                ss += t.w * t.w;
+            }
+            inv = rms_inv(block_sum(ss, sh), k, pr.eps);
         }
-        const float inv = rms_inv(block_sum(ss, sh), k, pr.eps);
         // the new residual (BF16-exact) goes to x's place in LDS, where the
         // same thread turns it into x
         uint2* xb = reinterpret_cast<uint2*>(xs + (size_t)b * k);
@@ -581,7 +603,8 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
     // the arguments of the tail, loaded while the first tiles are in flight
     // (a scalar load issued at the tail would hold the last stores)
     const int epi_kind = ga.epi.kind;
-    asm volatile("" ::"s"(a.y), "s"(a.N), "s"(epi_kind));
+    float* const row_ss = ga.epi.row_ss;
+    asm volatile("" ::"s"(a.y), "s"(a.N), "s"(epi_kind), "s"(row_ss));
     if constexpr (PF) {
         int r = 0;
         while (true) {
@@ -649,6 +672,11 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         else
             a.y[(int64_t)b * a.N + n] = v;
     }
+    if (row_ss && tid < 64) {  // wave 0, all lanes: the 16-lane trees of the batch rows
+        const float t = (tid < 16 * B && n < a.N) ? se12step::round_bf16(v) : 0.0f;
+        const float q = row16_sum(t * t);
+        if (tid < 16 * B && (tid & 15) == 0) row_ss[(int64_t)b * a.TR + tr] = q;
+    }
     if (epi) gemv_epilogue<B>(ga, tr, red);
 }
 
@@ -678,6 +706,22 @@ hipError_t launch_b(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t strea
 }
 
 }  // namespace
+
+// row_ss of a product whose launch did not write it (the MFMA kernel): the
+// same 16-lane tree over bf16(y)^2 as the dot2 tail, so the values agree
+// wherever y does. Grid (tile rows, batch rows), one wave per block.
+__global__ __launch_bounds__(64) void row_sumsq_kernel(const float* y, int64_t N, int32_t TR, float* row_ss) {
+    const int tr = blockIdx.x, b = blockIdx.y, lane = threadIdx.x;
+    const int64_t n = (int64_t)tr * kTileRows + (lane & 15);
+    const float t = (lane < 16 && n < N) ? se12step::round_bf16(y[(int64_t)b * N + n]) : 0.0f;
+    const float q = row16_sum(t * t);
+    if (lane == 0) row_ss[(int64_t)b * TR + tr] = q;
+}
+
+hipError_t launch_row_sumsq(const float* y, int64_t N, int32_t TR, int32_t batch, float* row_ss, hipStream_t stream) {
+    hipLaunchKernelGGL(row_sumsq_kernel, dim3(TR, batch), dim3(64), 0, stream, y, N, TR, row_ss);
+    return hipGetLastError();
+}
 
 hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream) {
     switch (p.batch * 2 + (p.raw ? 1 : 0)) {

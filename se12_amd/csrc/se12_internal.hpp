@@ -51,6 +51,11 @@ struct GemvEpilogue {
     const uint16_t* w2;       // [N] BF16
     uint16_t* residual;       // [B, N] BF16
     uint16_t* out;            // [B, N] BF16
+    // any kind, single-matrix dot2 launches: when not NULL, the block that
+    // completes tile row t also writes row_ss[b, t] = the sum over its 16
+    // rows n < N of bf16(y[b, n])^2 (a 16-lane DPP tree), the first sum of
+    // squares of the decoder's next norm
+    float* row_ss;            // [B, TR]
 };
 
 // Decode-step work done at the head of a dot2 GEMV launch (the XN kernel
@@ -63,6 +68,7 @@ struct GemvEpilogue {
 // residual_in).
 struct GemvPrologue {
     const float* y_prev;      // [B, K]
+    const float* y_prev_ss;   // [B, ceil(K / 16)] row_ss of y_prev's product, or NULL
     const uint16_t* w1;       // [K] BF16
     const uint16_t* w2;       // [K] BF16
     const uint16_t* res_in;   // [B, K] BF16
@@ -93,7 +99,10 @@ inline int32_t group_grid_x(const GemvGroupArgs& a) {
 // per batch row, w1 and w2), and x of the batch rows (BF16).
 constexpr size_t lds_align16(size_t n) { return (n + 15) / 16 * 16; }
 constexpr size_t gemv_pro_x_bytes(int64_t k, int batch) { return (size_t)k * batch * 2; }
-constexpr size_t gemv_pro_stage_bytes(int64_t k, int batch) { return (size_t)k * (batch * 4 + batch * 2 + 4); }
+constexpr size_t gemv_pro_ss_bytes(int64_t k, int batch) { return lds_align16((size_t)batch * ((k + 15) / 16) * 4); }
+constexpr size_t gemv_pro_stage_bytes(int64_t k, int batch) {
+    return (size_t)k * (batch * 4 + batch * 2 + 4) + gemv_pro_ss_bytes(k, batch);
+}
 inline size_t gemv_xn_lds_bytes(int64_t k, int batch, int waves) {
     return lds_align16(gemv_pro_x_bytes(k, batch)) + lds_align16((size_t)waves * batch * 16 * sizeof(float)) +
            gemv_pro_stage_bytes(k, batch);
@@ -192,6 +201,7 @@ constexpr int gemv_waves_per_simd(int batch, bool raw, int g, int pf, bool gener
 inline size_t gemv_lds_bytes(int waves, int batch) { return (size_t)waves * batch * 16 * sizeof(float); }
 
 hipError_t launch_gemv(const GemvGroupArgs& a, const GemvPlan& p, hipStream_t stream);
+hipError_t launch_row_sumsq(const float* y, int64_t N, int32_t TR, int32_t batch, float* row_ss, hipStream_t stream);
 
 // Batched path (se12_gemm.hip): BF16 x with kGemmMinBatch..32 rows runs one
 // MFMA launch over all rows (one pass over the weights) instead of one

@@ -262,6 +262,10 @@ class Gemma2Decoder:
             # residual to the other buffer; `residual` is the current one
             # after a step
             self.x2 = buf(s.hidden, torch.bfloat16) if self.fused_tails else None
+            # tile-row sums of squares of o_proj's and down_proj's outputs,
+            # written by those products for the norms in the next heads
+            self.o_ss = buf((s.hidden + 15) // 16, torch.float32) if self.fused_tails else None
+            self.down_ss = buf((s.hidden + 15) // 16, torch.float32) if self.fused_tails else None
             self.residual = self.x
             self.h = buf(s.hidden, torch.bfloat16)          # normalised input of the next product
             self.emb = buf(s.hidden, torch.bfloat16)
@@ -437,16 +441,16 @@ class Gemma2Decoder:
                 multiply_grouped(qkv, self.h, outs=self.qkv)
             else:
                 multiply_prenorm(qkv, self.down_out, self.w.layers[li - 1]["post_ffw_norm"], lw["input_norm"], ra, rb,
-                                 self.h, s.eps, ys=self.qkv)
+                                 self.h, s.eps, ys=self.qkv, y_prev_ss=self.down_ss)
                 ra, rb = rb, ra
             q, k, v = self.qkv
             self._attention(li, q.data_ptr(), k.data_ptr(), v.data_ptr(), nat.STEP_F32, q.shape[1], k.shape[1])
-            ks["o"].multiply(self.attn, out=self.o_out)
+            ks["o"].multiply_rowss(self.attn, self.o_ss, y=self.o_out)
             multiply_prenorm([ks["gate"], ks["up"]], self.o_out, lw["post_attn_norm"], lw["pre_ffw_norm"], ra, rb, self.h,
-                             s.eps, ys=self.gu, gelu_out=self.m)
+                             s.eps, ys=self.gu, gelu_out=self.m, y_prev_ss=self.o_ss)
             ra, rb = rb, ra
             if li + 1 < s.layers:
-                ks["down"].multiply(self.m, out=self.down_out)
+                ks["down"].multiply_rowss(self.m, self.down_ss, y=self.down_out)
             else:
                 ks["down"].multiply_rmsnorm(self.m, lw["post_ffw_norm"], self.w.final_norm, ra, self.h, s.eps,
                                             y=self.down_out)

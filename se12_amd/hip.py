@@ -164,6 +164,23 @@ class _GemvBase:
                                               nat.stream_ptr()))
         return y
 
+    def multiply_rowss(self, activations: torch.Tensor, row_ss: torch.Tensor, y: torch.Tensor | None = None,
+                       launch: LaunchConfiguration | None = None) -> torch.Tensor:
+        """y = x . W^T with the tile-row sums of squares of the output
+        (se12_gemv_rowss): row_ss[b, t] = sum over tile row t's 16 rows of
+        bf16(y[b, n])^2, FP32 [B, ceil(rows / 16)], for a following
+        `multiply_prenorm(..., y_prev_ss=row_ss)`. Returns y."""
+        x, xd = _activations(activations, self.cols, self.device)
+        b = x.shape[0]
+        y = _fp32_out(y, b, self.rows, self.device)
+        tr = (self.rows + 15) // 16
+        if row_ss.dtype != torch.float32 or tuple(row_ss.shape) != (b, tr) or not row_ss.is_contiguous() \
+                or row_ss.device != self.device:
+            raise ValueError(f"row_ss must be a contiguous float32 [{b}, {tr}] tensor on {self.device}")
+        nat.check(nat.lib().se12_gemv_rowss(self.handle.raw, nat.ptr(x), xd, b, nat.ptr(y), nat.ptr(row_ss),
+                                            _launch_struct(launch), nat.stream_ptr()))
+        return y
+
 
 class Se12MatVecKernel(_GemvBase):
     """Fused SE12 decode + GEMV bound to one SE12 matrix (gemv.py:180-226).
@@ -254,14 +271,17 @@ def multiply_gelu_mul(gate, up, activations: torch.Tensor, out: torch.Tensor, ys
 
 def multiply_prenorm(kernels, y_prev: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, residual_in: torch.Tensor,
                      residual_out: torch.Tensor, h_out: torch.Tensor, eps: float, ys: list[torch.Tensor] | None = None,
-                     gelu_out: torch.Tensor | None = None, launch: LaunchConfiguration | None = None) -> list[torch.Tensor]:
+                     gelu_out: torch.Tensor | None = None, launch: LaunchConfiguration | None = None,
+                     y_prev_ss: torch.Tensor | None = None) -> list[torch.Tensor]:
     """The decoder's next normalised input and its products in one launch
     (se12_gemv_prenorm): per batch row of the previous product's FP32 output
     y_prev [B, K], r = bf16(residual_in + norm(bf16(y_prev)) * (1 + w1)),
     h = norm(r) * (1 + w2); residual_out = r, h_out = h, then y_i = h . W_i^T
     for up to 4 bound matrices with K columns (and, with gelu_out and two
     matrices, the MLP gate of `multiply_gelu_mul`). residual_in and
-    residual_out are the same tensor or disjoint. Returns the FP32 y_i."""
+    residual_out are the same tensor or disjoint. y_prev_ss: the row sums that
+    `multiply_rowss` wrote with y_prev (the first norm's mean then comes from
+    them). Returns the FP32 y_i."""
     kernels = list(kernels)
     if not 1 <= len(kernels) <= nat.MAX_GROUP:
         raise ValueError(f"1..{nat.MAX_GROUP} matrices per launch, got {len(kernels)}")
@@ -272,6 +292,11 @@ def multiply_prenorm(kernels, y_prev: torch.Tensor, w1: torch.Tensor, w2: torch.
     if y_prev.dtype != torch.float32 or y_prev.dim() != 2 or y_prev.shape[1] != k0.cols or not y_prev.is_contiguous():
         raise ValueError(f"y_prev must be a contiguous float32 [B, {k0.cols}] tensor")
     b = y_prev.shape[0]
+    if y_prev_ss is not None:
+        tr = (k0.cols + 15) // 16
+        if y_prev_ss.dtype != torch.float32 or tuple(y_prev_ss.shape) != (b, tr) or not y_prev_ss.is_contiguous() \
+                or y_prev_ss.device != k0.device:
+            raise ValueError(f"y_prev_ss must be a contiguous float32 [{b}, {tr}] tensor on {k0.device}")
     for t in (w1, w2):
         if t.dtype != torch.bfloat16 or tuple(t.shape) != (k0.cols,) or not t.is_contiguous() or t.device != k0.device:
             raise ValueError(f"norm weights must be contiguous bfloat16 [{k0.cols}] on {k0.device}")
@@ -288,7 +313,8 @@ def multiply_prenorm(kernels, y_prev: torch.Tensor, w1: torch.Tensor, w2: torch.
     n = len(kernels)
     hs = (ctypes.c_void_p * n)(*[k.handle.raw.value for k in kernels])
     yp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in ys])
-    nat.check(nat.lib().se12_gemv_prenorm(hs, n, nat.ptr(y_prev), b, nat.ptr(w1), nat.ptr(w2), nat.ptr(residual_in),
+    nat.check(nat.lib().se12_gemv_prenorm(hs, n, nat.ptr(y_prev),
+                                          None if y_prev_ss is None else nat.ptr(y_prev_ss), b, nat.ptr(w1), nat.ptr(w2), nat.ptr(residual_in),
                                           nat.ptr(residual_out), nat.ptr(h_out), float(eps), yp,
                                           None if gelu_out is None else nat.ptr(gelu_out), _launch_struct(launch),
                                           nat.stream_ptr()))

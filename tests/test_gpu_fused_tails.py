@@ -286,3 +286,113 @@ def test_prenorm_replays_in_a_graph(gpu):
         torch.cuda.synchronize()
         for a, b in zip(got, (ra, rb, h, m, *outs[0], *outs[1])):
             assert torch.equal(a, b), rep
+
+
+def _want_row_ss(y: torch.Tensor) -> torch.Tensor:
+    b, n = y.shape
+    tr = (n + 15) // 16
+    t = torch.zeros((b, tr * 16), dtype=torch.float32, device=y.device)
+    t[:, :n] = y.to(torch.bfloat16).float() ** 2
+    return t.view(b, tr, 16).sum(-1)
+
+
+@pytest.mark.parametrize("fmt", ["se12", "raw"])
+@pytest.mark.parametrize("rows,cols,batch,dtype", [
+    (2304, 2048, 1, torch.bfloat16),    # Gemma-2-2B o_proj
+    (2304, 9216, 1, torch.bfloat16),    # down_proj, split-K
+    (2304, 9216, 4, torch.bfloat16),
+    (300, 512, 3, torch.bfloat16),      # a partial last tile row
+    (256, 1024, 6, torch.bfloat16),     # MFMA product, row sums after it
+    (512, 768, 2, torch.float32),       # FP32 x
+])
+def test_rowss_sums_the_tile_rows_of_the_output(gpu, fmt, rows, cols, batch, dtype):
+    k = _kernel(rows, cols, 70, fmt, gpu)
+    tr = (rows + 15) // 16
+    for call in range(2):
+        x = _x(batch, cols, gpu, 71 + call, dtype)
+        ss = torch.full((batch, tr), float("nan"), device=gpu)
+        y = k.multiply_rowss(x, ss)
+        torch.cuda.synchronize()
+        assert torch.equal(y, k.multiply(x))
+        torch.testing.assert_close(ss, _want_row_ss(y), rtol=1e-5, atol=1e-30)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4])
+@pytest.mark.parametrize("consumer_rows", [(2048, 1024, 1024), (9216, 9216)])
+def test_prenorm_from_producer_row_sums(gpu, batch, consumer_rows):
+    """The norm's first mean from the producer's row sums gives the norm of
+    the separate step kernels (Gemma-2-2B o_proj -> gate/up, down -> q/k/v)."""
+    from se12_amd.hip import multiply_grouped, multiply_prenorm
+
+    producer = _kernel(2304, 2048, 80, "se12", gpu)
+    kernels = [_kernel(r, 2304, 81 + i, "se12", gpu) for i, r in enumerate(consumer_rows)]
+    x = _x(batch, 2048, gpu, 85)
+    ss = torch.empty((batch, 144), device=gpu)
+    y_prev = producer.multiply_rowss(x, ss)
+    w1, w2, res0 = _norm_inputs(batch, 2304, gpu, 86)
+    want_res, want_h = _separate_norm(y_prev, w1, w2, res0, 1e-6)
+    res_out, h = torch.full_like(res0, float("nan")), torch.full_like(res0, float("nan"))
+    ys = multiply_prenorm(kernels, y_prev, w1, w2, res0, res_out, h, 1e-6, y_prev_ss=ss)
+    torch.cuda.synchronize()
+    _norm_close(res_out, want_res)
+    _norm_close(h, want_h)
+    for got, want in zip(ys, multiply_grouped(kernels, h)):
+        assert torch.equal(got, want)
+
+
+def test_row_sums_replay_in_a_graph(gpu):
+    """o_proj with row sums, then gate/up with the norm from them, captured
+    once and replayed five times against eager calls."""
+    from se12_amd.hip import multiply_prenorm
+
+    o_k = _kernel(1024, 512, 90, "se12", gpu)
+    gu = [_kernel(2048, 1024, 91, "se12", gpu), _kernel(2048, 1024, 92, "se12", gpu)]
+    g = _gen(gpu, 93)
+    x = torch.randn((1, 512), generator=g, device=gpu).to(torch.bfloat16)
+    w = [(torch.randn(1024, generator=g, device=gpu) * 0.1).to(torch.bfloat16) for _ in range(2)]
+    r0 = torch.randn((1, 1024), generator=g, device=gpu).to(torch.bfloat16)
+    ra, rb, h = r0.clone(), torch.empty_like(r0), torch.empty_like(r0)
+    y_o, ss = torch.empty((1, 1024), device=gpu), torch.empty((1, 64), device=gpu)
+    m = torch.empty((1, 2048), dtype=torch.bfloat16, device=gpu)
+    outs = [torch.empty((1, 2048), device=gpu) for _ in gu]
+
+    def step():
+        o_k.multiply_rowss(x, ss, y=y_o)
+        multiply_prenorm(gu, y_o, w[0], w[1], ra, rb, h, 1e-6, ys=outs, gelu_out=m, y_prev_ss=ss)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        step()
+    torch.cuda.synchronize()
+    for rep in range(5):
+        ss.fill_(float("nan"))
+        gr.replay()
+        torch.cuda.synchronize()
+        got = [t.clone() for t in (ss, y_o, rb, h, m, *outs)]
+        ss.fill_(float("nan"))
+        step()
+        torch.cuda.synchronize()
+        for a, b in zip(got, (ss, y_o, rb, h, m, *outs)):
+            assert torch.equal(a, b), rep
+
+
+def test_row_sum_arguments_are_checked(gpu):
+    from se12_amd.hip import multiply_prenorm
+
+    k = _kernel(256, 512, 95, "se12", gpu)
+    x = _x(2, 512, gpu, 96)
+    with pytest.raises(ValueError):
+        k.multiply_rowss(x, torch.empty((2, 15), device=gpu))
+    with pytest.raises(ValueError):
+        k.multiply_rowss(x, torch.empty((2, 16), device=gpu, dtype=torch.float64))
+    c = _kernel(128, 256, 97, "se12", gpu)
+    y = torch.randn((1, 256), device=gpu)
+    w1, w2, r = _norm_inputs(1, 256, gpu, 98)
+    with pytest.raises(ValueError):
+        multiply_prenorm([c], y, w1, w2, r, torch.empty_like(r), torch.empty_like(r), 1e-6,
+                         y_prev_ss=torch.empty((1, 15), device=gpu))

@@ -69,6 +69,8 @@ def test_null_arguments_fail_with_a_message_and_no_gpu_call():
     assert "se12_gemv_gelu_mul" in nat.last_error()
     assert lib.se12_gemv_rmsnorm(None, None, 0, 1, None, None, None, None, None, 1e-6, None, None) == nat.SE12_E_INVALID
     assert "se12_gemv_rmsnorm" in nat.last_error()
+    assert lib.se12_gemv_rowss(None, None, 0, 1, None, None, None, None) == nat.SE12_E_INVALID
+    assert "se12_gemv_rowss" in nat.last_error()
 
 
 def test_bind_rejects_bad_shapes_before_touching_the_device():

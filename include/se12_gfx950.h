@@ -209,8 +209,9 @@ int se12_gemv_rowss(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t 
  * residual_in and residual_out are either the same tensor or disjoint.
  * Where the product runs the dot2 kernel with BF16 x (batch <= 4), whole K
  * tiles, distinct residuals, 16-byte aligned y_prev and 8-byte aligned
- * weights, residuals and h_out, and a block's LDS holds cols x (12 x batch
- * + 4) bytes, every block of the product rebuilds h in LDS (sums of squares
+ * weights, residuals and h_out, and a block's LDS holds about cols x (8 x
+ * batch + 4) bytes (staged y_prev, residual, weights and x) beside the
+ * product's own, every block of the product rebuilds h in LDS (sums of squares
  * over its threads) and block (0, 0) writes residual_out and h_out;
  * otherwise the norm runs as its own kernel (se12_step_rmsnorm mode 1)
  * before the product. y_prev_ss: NULL, or the tile-row sums of squares of

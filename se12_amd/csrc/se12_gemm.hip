@@ -28,9 +28,8 @@
 // for the part's two 32-column slices s (lane l: weight row l % 16, columns
 // 32 s + 8 (l / 16) .. + 7), so the decoded tile never goes through memory.
 // The B operand is the x slab (lane l: batch row 16 g + l % 16, the same
-// columns). 8 MFMAs per tile and group of 16 batch rows, FP32 accumulate:
-// the even slices in ascending order into one accumulator, the odd ones into
-// a second, the two added after the wave's last tile. Rows of the LDS x slabs are padded to 528 bytes so
+// columns). 8 MFMAs per tile and group of 16 batch rows, FP32 accumulate, in
+// ascending slice order. Rows of the LDS x slabs are padded to 528 bytes so
 // that the 16-byte reads of 8 lanes per cycle hit distinct banks. Batch rows
 // past the batch in a 16-row group read stale LDS: MFMA output column n
 // depends on B column n only, and those columns are not stored.
@@ -200,12 +199,10 @@ __device__ __forceinline__ void zero_past_k(uint32_t w[8], int c0, int lim) {
 }
 
 // The MFMAs of part p (slices 2p and 2p + 1) for every batch group, the x
-// slab (B operands) read from LDS. Even slices accumulate into acc[0], odd
-// ones into acc[1]: two independent chains per batch group, so an MFMA does
-// not wait for the one issued just before it.
+// slab (B operands) read from LDS.
 template <int BG>
 __device__ __forceinline__ void mfma_part(const bf16x8_t& a0, const bf16x8_t& a1, const char* xb, int p, uint32_t lane,
-                                          floatx4_t (&acc)[2][BG]) {
+                                          floatx4_t acc[BG]) {
     const int off = (int)(lane & 15u) * kRowBytes + 16 * (int)(lane >> 4);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -213,8 +210,8 @@ __device__ __forceinline__ void mfma_part(const bf16x8_t& a0, const bf16x8_t& a1
 #pragma unroll
         for (int g = 0; g < BG; ++g) {
             const uint4 bv = *reinterpret_cast<const uint4*>(xb + g * 16 * kRowBytes + off + 64 * s);
-            acc[h][g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h ? a1 : a0, __builtin_bit_cast(bf16x8_t, bv), acc[h][g],
-                                                                 0, 0, 0);
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(h ? a1 : a0, __builtin_bit_cast(bf16x8_t, bv), acc[g], 0, 0,
+                                                              0);
         }
     }
 }
@@ -259,9 +256,9 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     const int slab_bytes = x_slab_bytes<BG>();
     char* xbuf = gsm;  // [2 buffers][KG slabs]
 
-    floatx4_t chains[2][BG];
+    floatx4_t acc[BG];
 #pragma unroll
-    for (int g = 0; g < BG; ++g) chains[0][g] = chains[1][g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int g = 0; g < BG; ++g) acc[g] = floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
     auto load_tile_i = [&](GemmTile<RAW>& t, int i) {
         const int j = kg + KG * i;
@@ -282,7 +279,7 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
             if constexpr (GENERIC) zero_past_k(wv, row_layout_col(p, lane), lim);
             bf16x8_t a0, a1;
             rows_to_operands(wv, a0, a1);
-            mfma_part<BG>(a0, a1, xb, p, lane, chains);
+            mfma_part<BG>(a0, a1, xb, p, lane, acc);
         };
         if constexpr (RAW) {
 #pragma unroll
@@ -374,10 +371,6 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
             lds_barrier();
         }
     }
-    // the wave's sums: even slices + odd slices
-    floatx4_t acc[BG];
-#pragma unroll
-    for (int g = 0; g < BG; ++g) acc[g] = chains[0][g] + chains[1][g];
     // the K groups of a tile row: groups 1..KG-1 hand their sums to group 0
     // through LDS (the x slabs are no longer read: every wave passed the
     // last step's barrier), which adds them in ascending group order

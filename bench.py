@@ -78,6 +78,9 @@ def parse_args(argv=None):
     p.add_argument("--profile-down", action="store_true",
                    help="only the dominant kernel (26 down_proj launches per step) and a 256 MiB device copy of known "
                         "size, for hardware-counter runs")
+    p.add_argument("--profile-batch", type=int, default=None, metavar="B",
+                   help="only the batch sweep's 14336x3584 product at batch B (cold rotation of matrices), for "
+                        "hardware-counter runs of one kernel")
     p.add_argument("--profile-e2e", choices=("se12", "raw", "bf16"), default=None,
                    help="only the Gemma-2-2B decode of one backend: prefill 512, capture, a 0.5 s pause, 32 graph-"
                         "replayed steps (kernel traces of the decode step)")
@@ -143,6 +146,32 @@ def profile_down(args, device) -> int:
     print(json.dumps({"profile": "down_proj 2304x9216 fused GEMV", "us_per_launch": round(ms * 1e3 / len(down), 3),
                       "launches": len(down) * (args.steps + args.warmup + 2), "copy_bytes": src.numel() * 4,
                       "copies": 3}), flush=True)
+    return 0
+
+
+def profile_batch(args, device, batch: int) -> int:
+    """The batch sweep's product alone at one batch: 14336x3584 (a Gemma-2-9B
+    MLP shape), a rotation of distinct matrices over more than 1 GB so that
+    every launch streams from HBM, default launch."""
+    from se12_amd.hip import Se12MatVecKernel, encode_on_device
+
+    n, k = 14336, 3584
+    gen = torch.Generator(device=device)
+    kerns = []
+    for r in range(cold_rotation(int(n * k * 1.504))):
+        gen.manual_seed(r)
+        w = (torch.randn((n, k), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+        kerns.append(Se12MatVecKernel(encode_on_device(w), max_batch=batch))
+        del w
+    gen.manual_seed(99)
+    x = torch.randn((batch, k), generator=gen, device=device).to(torch.bfloat16)
+    y = torch.empty((batch, n), dtype=torch.float32, device=device)
+    g = capture(lambda: [kk.multiply(x, out=y) for kk in kerns])
+    ms = time_graph(g, args.steps, args.warmup)
+    launch = kerns[0].default_launch(batch)
+    print(json.dumps({"profile": f"fused SE12 product 14336x3584 at batch {batch}",
+                      "us_per_launch": round(ms * 1e3 / len(kerns), 3),
+                      "launch": [launch.threads_per_block.value, launch.blocks.value]}), flush=True)
     return 0
 
 
@@ -419,6 +448,10 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     if args.profile_down:
         return profile_down(args, dev)
+    if args.profile_batch is not None:
+        if not 1 <= args.profile_batch <= 32:
+            raise SystemExit("--profile-batch takes a batch in 1..32")
+        return profile_batch(args, dev, args.profile_batch)
     if args.profile_e2e:
         return profile_e2e(args.profile_e2e, dev)
     props = HipGpuProbe(0).properties()

@@ -197,9 +197,14 @@ def _prenorm_case(gpu, kernels, batch, seed, same_residual=False, launch=None):
     _norm_close(h, want_h)
     if not same_residual:
         assert torch.equal(res_in, res0)
-    # the products are those of the h the launch wrote
+    # the products are those of the h the launch wrote: bit for bit under one
+    # launch shape; the default launches of the two calls may differ (a head
+    # launch can take one wave fewer), which only reorders the FP32 K sums
     for got, want in zip(ys, multiply_grouped(kernels, h, launch=launch)):
-        assert torch.equal(got, want)
+        if launch is None:
+            torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+        else:
+            assert torch.equal(got, want)
     return ys, h
 
 
@@ -337,7 +342,7 @@ def test_prenorm_from_producer_row_sums(gpu, batch, consumer_rows):
     _norm_close(res_out, want_res)
     _norm_close(h, want_h)
     for got, want in zip(ys, multiply_grouped(kernels, h)):
-        assert torch.equal(got, want)
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
 def test_row_sums_replay_in_a_graph(gpu):

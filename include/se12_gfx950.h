@@ -92,6 +92,13 @@ typedef struct se12_device_info {
     int32_t memory_clock_khz;
     int32_t memory_bus_width_bits;
     int32_t max_threads_per_block;
+    int32_t pci_domain_id;
+    int32_t pci_bus_id;
+    int32_t pci_device_id;
+    int32_t ecc_enabled;         /* hipDeviceProp_t.ECCEnabled */
+    int32_t kernel_timeout;      /* hipDeviceProp_t.kernelExecTimeoutEnabled (a display watchdog) */
+    int32_t runtime_version;     /* hipRuntimeGetVersion */
+    int32_t driver_version;      /* hipDriverGetVersion */
 } se12_device_info;
 
 typedef struct se12_handle se12_handle;
@@ -131,6 +138,13 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
 /* The default launch for `batch` (the heuristic of
  * lws/domain/launch/heuristic.py:46-87 re-derived for 256 CUs of wave64). */
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out);
+
+/* Sets the compute-unit count the handle's default launches are derived for
+ * (bind takes hipDeviceProp_t.multiProcessorCount). Host only. Replaces the
+ * `sm_count` argument that Se12MatVecKernel / RawBf16MatVecKernel take at
+ * construction and hand to the default launch heuristic
+ * (lws/adapters/cuda/gemv.py:146,183,199). */
+int se12_set_compute_units(se12_handle* h, int32_t compute_units);
 
 /* y[b, n] = sum_k W[n, k] * x[b, k] for b < batch (1..32), FP32 accumulate.
  * x: [batch, cols] row-major, BF16 or FP32 (`x_dtype`); y: FP32 [batch, rows].

@@ -87,6 +87,13 @@ class DeviceInfo(ctypes.Structure):
         ("memory_clock_khz", c_i32),
         ("memory_bus_width_bits", c_i32),
         ("max_threads_per_block", c_i32),
+        ("pci_domain_id", c_i32),
+        ("pci_bus_id", c_i32),
+        ("pci_device_id", c_i32),
+        ("ecc_enabled", c_i32),
+        ("kernel_timeout", c_i32),
+        ("runtime_version", c_i32),
+        ("driver_version", c_i32),
     ]
 
 
@@ -104,6 +111,7 @@ SIGNATURES = {
         [c_void_p, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), ctypes.POINTER(c_i32)],
     ),
     "se12_default_launch": (c_i32, [c_void_p, c_i32, ctypes.POINTER(Launch)]),
+    "se12_set_compute_units": (c_i32, [c_void_p, c_i32]),
     "se12_gemv": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, ctypes.POINTER(Launch), c_void_p]),
     "se12_gemv_grouped": (
         c_i32,

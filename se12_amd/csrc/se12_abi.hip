@@ -116,6 +116,17 @@ int se12_device_info_get(int32_t device, se12_device_info* out) {
     out->memory_clock_khz = p.memoryClockRate;
     out->memory_bus_width_bits = p.memoryBusWidth;
     out->max_threads_per_block = p.maxThreadsPerBlock;
+    out->pci_domain_id = p.pciDomainID;
+    out->pci_bus_id = p.pciBusID;
+    out->pci_device_id = p.pciDeviceID;
+    out->ecc_enabled = p.ECCEnabled;
+    out->kernel_timeout = p.kernelExecTimeoutEnabled;
+    int v = 0;
+    SE12_HIP(hipRuntimeGetVersion(&v));
+    out->runtime_version = v;
+    v = 0;
+    SE12_HIP(hipDriverGetVersion(&v));
+    out->driver_version = v;
     return SE12_OK;
 }
 
@@ -373,6 +384,14 @@ static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t b
                                                                h0->TC / (3 * kg)}));
     *waves_out = (int32_t)(rows * kg);
     *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, (2 * m + kg) / (2 * kg)));
+}
+
+int se12_set_compute_units(se12_handle* h, int32_t compute_units) {
+    if (!h) return fail(SE12_E_INVALID, "se12_set_compute_units: NULL handle");
+    if (compute_units < 1 || compute_units > (1 << 16))
+        return fail(SE12_E_INVALID, "se12_set_compute_units: %d compute units", compute_units);
+    h->cu_count = compute_units;
+    return SE12_OK;
 }
 
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {

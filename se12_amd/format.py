@@ -248,6 +248,41 @@ def validate_streams(tensor: Any) -> None:
         raise ValueError(f"bitmap marks {nfb} fallback tiles but fallback_raw holds {raw.size // TILE_SIZE}")
 
 
+def validate_device_streams(dt: "Se12DeviceTensor") -> None:
+    """The device-side counterpart of `validate_streams`: every stream a torch
+    tensor on one GPU, contiguous, of the right dtype and size for the shape
+    (the library binds to these pointers and its kernels read every byte the
+    shape implies). The fallback count against the bitmap is checked by the
+    library at bind."""
+    import torch
+
+    if dt.rows <= 0 or dt.cols <= 0:
+        raise ValueError(f"shape must be positive, got [{dt.rows}, {dt.cols}]")
+    tr, tc = tile_grid(dt.rows, dt.cols)
+    t = tr * tc
+    expect = {
+        "sm": (dt.sm, torch.uint8, t * TILE_SIZE),
+        "ec": (dt.ec, torch.uint8, t * TILE_SIZE // 2),
+        "esc": (dt.esc, torch.uint8, t * ESCAPE_BUDGET),
+        "codebook": (dt.codebook, torch.uint8, CODEBOOK_SIZE),
+        "fallback_bitmap": (dt.fallback_bitmap, torch.uint8, bitmap_bytes(t)),
+    }
+    device = dt.sm.device if isinstance(dt.sm, torch.Tensor) else None
+    if device is None or device.type != "cuda":
+        raise ValueError(f"SE12 streams must be device tensors, sm is on {device}")
+    for name, (arr, dtype, size) in expect.items():
+        if not isinstance(arr, torch.Tensor) or arr.device != device:
+            raise ValueError(f"stream {name} must be a tensor on {device}")
+        if arr.dtype != dtype or arr.numel() != size or not arr.is_contiguous():
+            raise ValueError(f"stream {name}: expected {size} contiguous x {dtype}, got {arr.numel()} x {arr.dtype}")
+    raw = dt.fallback_raw
+    if not isinstance(raw, torch.Tensor) or raw.device != device or raw.dtype != torch.int16 \
+            or raw.numel() % TILE_SIZE != 0 or not raw.is_contiguous():
+        raise ValueError(f"stream fallback_raw must be whole contiguous int16 tiles on {device}")
+    if tuple(int(c) for c in dt.codebook_host) != tuple(int(c) for c in dt.codebook.cpu().tolist()):
+        raise ValueError("codebook_host differs from the device codebook")
+
+
 @dataclasses.dataclass
 class Se12DeviceTensor:
     """The SE12 streams resident on one GPU (torch tensors), plus metadata."""

@@ -36,6 +36,7 @@ from .format import (
     Se12DeviceTensor,
     bitmap_bytes,
     tile_grid,
+    validate_device_streams,
 )
 from .launch import BlockCount, LaunchConfiguration, ThreadsPerBlock
 
@@ -48,8 +49,25 @@ def _device_of(t: torch.Tensor) -> torch.device:
 
 def _as_device_tensor(tensor: Any, device=None) -> Se12DeviceTensor:
     if isinstance(tensor, Se12DeviceTensor):
+        validate_device_streams(tensor)
+        if device is not None and tensor.sm.device != torch.device(device):
+            raise ValueError(f"SE12 streams on {tensor.sm.device}, requested {device}")
         return tensor
     return Se12DeviceTensor.from_host(tensor, device=device)
+
+
+def _require(t: Any, name: str, dtype: torch.dtype, shape: tuple, device: torch.device) -> torch.Tensor:
+    """Checks a caller-supplied tensor before its pointer crosses into the
+    library: a host tensor, another device's memory or a short buffer would
+    otherwise reach a kernel as a bad address."""
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch tensor, got {type(t).__name__}")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, the weights on {device}")
+    if t.dtype != dtype or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous {dtype} {list(shape)} tensor, "
+                         f"got {t.dtype} {list(t.shape)}{'' if t.is_contiguous() else ' (not contiguous)'}")
+    return t
 
 
 class _Handle:
@@ -132,10 +150,7 @@ class _GemvBase:
             raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
         x = x.contiguous()
         b = x.shape[0]
-        if out is None:
-            out = torch.empty((b, self.rows), dtype=torch.float32, device=self.device)
-        elif out.shape != (b, self.rows) or out.dtype != torch.float32 or not out.is_contiguous():
-            raise ValueError("out must be a contiguous float32 [B, rows] tensor")
+        out = _fp32_out(out, b, self.rows, self.device)
         nat.check(nat.lib().se12_gemv(self.handle.raw, nat.ptr(x), xd, b, nat.ptr(out), _launch_struct(launch), nat.stream_ptr()))
         return out
 
@@ -152,13 +167,11 @@ class _GemvBase:
         residual / out: BF16 [B, rows] (updated / written); returns y."""
         x, xd = _activations(activations, self.cols, self.device)
         b = x.shape[0]
-        y = _fp32_out(y, b, self.rows, self.device)
-        for t in (w1, w2):
-            if t.dtype != torch.bfloat16 or tuple(t.shape) != (self.rows,) or not t.is_contiguous() or t.device != self.device:
-                raise ValueError(f"norm weights must be contiguous bfloat16 [{self.rows}] on {self.device}")
-        for t in (residual, out):
-            if t.dtype != torch.bfloat16 or tuple(t.shape) != (b, self.rows) or not t.is_contiguous() or t.device != self.device:
-                raise ValueError(f"residual and out must be contiguous bfloat16 [{b}, {self.rows}] on {self.device}")
+        y = _fp32_out(y, b, self.rows, self.device, "y")
+        for name, t in (("w1", w1), ("w2", w2)):
+            _require(t, name, torch.bfloat16, (self.rows,), self.device)
+        for name, t in (("residual", residual), ("out", out)):
+            _require(t, name, torch.bfloat16, (b, self.rows), self.device)
         nat.check(nat.lib().se12_gemv_rmsnorm(self.handle.raw, nat.ptr(x), xd, b, nat.ptr(y), nat.ptr(w1), nat.ptr(w2),
                                               nat.ptr(residual), nat.ptr(out), float(eps), _launch_struct(launch),
                                               nat.stream_ptr()))
@@ -172,11 +185,8 @@ class _GemvBase:
         `multiply_prenorm(..., y_prev_ss=row_ss)`. Returns y."""
         x, xd = _activations(activations, self.cols, self.device)
         b = x.shape[0]
-        y = _fp32_out(y, b, self.rows, self.device)
-        tr = (self.rows + 15) // 16
-        if row_ss.dtype != torch.float32 or tuple(row_ss.shape) != (b, tr) or not row_ss.is_contiguous() \
-                or row_ss.device != self.device:
-            raise ValueError(f"row_ss must be a contiguous float32 [{b}, {tr}] tensor on {self.device}")
+        y = _fp32_out(y, b, self.rows, self.device, "y")
+        _require(row_ss, "row_ss", torch.float32, (b, (self.rows + 15) // 16), self.device)
         nat.check(nat.lib().se12_gemv_rowss(self.handle.raw, nat.ptr(x), xd, b, nat.ptr(y), nat.ptr(row_ss),
                                             _launch_struct(launch), nat.stream_ptr()))
         return y
@@ -197,10 +207,7 @@ class Se12MatVecKernel(_GemvBase):
     def decode_into(self, out: torch.Tensor) -> torch.Tensor:
         """Decodes the whole matrix into `out` (row-major BF16 [rows, cols],
         e.g. a view of a scratch buffer shared by many layers)."""
-        if out.dtype != torch.bfloat16 or tuple(out.shape) != (self.rows, self.cols) or not out.is_contiguous():
-            raise ValueError(f"out must be a contiguous bfloat16 [{self.rows}, {self.cols}] tensor")
-        if out.device != self.device:
-            raise ValueError(f"out on {out.device}, weights on {self.device}")
+        _require(out, "out", torch.bfloat16, (self.rows, self.cols), self.device)
         nat.check(nat.lib().se12_decode(self.handle.raw, nat.ptr(out), nat.stream_ptr()))
         return out
 
@@ -210,10 +217,8 @@ class Se12MatVecKernel(_GemvBase):
         index outside [0, rows) gives a row of zeros (the kernel checks each
         index before reading)."""
         idx = rows.reshape(-1)
-        if idx.dtype != torch.int64 or idx.device != self.device or not idx.is_contiguous():
-            raise ValueError("rows must be a contiguous int64 tensor on the weights' device")
-        if out.dtype != torch.bfloat16 or tuple(out.shape) != (idx.numel(), self.cols) or not out.is_contiguous():
-            raise ValueError(f"out must be a contiguous bfloat16 [{idx.numel()}, {self.cols}] tensor")
+        _require(idx, "rows", torch.int64, (idx.numel(),), self.device)
+        _require(out, "out", torch.bfloat16, (idx.numel(), self.cols), self.device)
         nat.check(nat.lib().se12_decode_rows(self.handle.raw, nat.ptr(idx), idx.numel(), nat.ptr(out), nat.stream_ptr()))
         return out
 
@@ -241,12 +246,10 @@ def _activations(activations: torch.Tensor, cols: int, device) -> tuple[torch.Te
     raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
 
 
-def _fp32_out(out: torch.Tensor | None, b: int, rows: int, device) -> torch.Tensor:
+def _fp32_out(out: torch.Tensor | None, b: int, rows: int, device, name: str = "out") -> torch.Tensor:
     if out is None:
         return torch.empty((b, rows), dtype=torch.float32, device=device)
-    if out.shape != (b, rows) or out.dtype != torch.float32 or not out.is_contiguous():
-        raise ValueError("out must be a contiguous float32 [B, rows] tensor")
-    return out
+    return _require(out, name, torch.float32, (b, rows), device)
 
 
 def multiply_gelu_mul(gate, up, activations: torch.Tensor, out: torch.Tensor, ys: list[torch.Tensor] | None = None,
@@ -258,10 +261,10 @@ def multiply_gelu_mul(gate, up, activations: torch.Tensor, out: torch.Tensor, ys
         raise ValueError("gate and up need one shape, one device and one format")
     x, xd = _activations(activations, gate.cols, gate.device)
     b = x.shape[0]
-    ys = [_fp32_out(None, b, gate.rows, gate.device) for _ in range(2)] if ys is None else \
-        [_fp32_out(t, b, gate.rows, gate.device) for t in ys]
-    if out.dtype != torch.bfloat16 or tuple(out.shape) != (b, gate.rows) or not out.is_contiguous() or out.device != gate.device:
-        raise ValueError(f"out must be a contiguous bfloat16 [{b}, {gate.rows}] tensor on {gate.device}")
+    if ys is not None and len(ys) != 2:
+        raise ValueError(f"ys must hold two tensors, got {len(ys)}")
+    ys = [_fp32_out(None if ys is None else ys[i], b, gate.rows, gate.device, f"ys[{i}]") for i in range(2)]
+    _require(out, "out", torch.bfloat16, (b, gate.rows), gate.device)
     hs = (ctypes.c_void_p * 2)(gate.handle.raw.value, up.handle.raw.value)
     yp = (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr())
     nat.check(nat.lib().se12_gemv_gelu_mul(hs, nat.ptr(x), xd, b, yp, nat.ptr(out), _launch_struct(launch),
@@ -289,27 +292,23 @@ def multiply_prenorm(kernels, y_prev: torch.Tensor, w1: torch.Tensor, w2: torch.
     for k in kernels:
         if k.cols != k0.cols or k.device != k0.device or type(k) is not type(k0):
             raise ValueError("the matrices need one K, one device and one format")
-    if y_prev.dtype != torch.float32 or y_prev.dim() != 2 or y_prev.shape[1] != k0.cols or not y_prev.is_contiguous():
-        raise ValueError(f"y_prev must be a contiguous float32 [B, {k0.cols}] tensor")
+    if not isinstance(y_prev, torch.Tensor) or y_prev.dim() != 2:
+        raise ValueError(f"y_prev must be a 2-D float32 [B, {k0.cols}] tensor")
     b = y_prev.shape[0]
+    _require(y_prev, "y_prev", torch.float32, (b, k0.cols), k0.device)
     if y_prev_ss is not None:
-        tr = (k0.cols + 15) // 16
-        if y_prev_ss.dtype != torch.float32 or tuple(y_prev_ss.shape) != (b, tr) or not y_prev_ss.is_contiguous() \
-                or y_prev_ss.device != k0.device:
-            raise ValueError(f"y_prev_ss must be a contiguous float32 [{b}, {tr}] tensor on {k0.device}")
-    for t in (w1, w2):
-        if t.dtype != torch.bfloat16 or tuple(t.shape) != (k0.cols,) or not t.is_contiguous() or t.device != k0.device:
-            raise ValueError(f"norm weights must be contiguous bfloat16 [{k0.cols}] on {k0.device}")
-    for t in (residual_in, residual_out, h_out):
-        if t.dtype != torch.bfloat16 or tuple(t.shape) != (b, k0.cols) or not t.is_contiguous() or t.device != k0.device:
-            raise ValueError(f"residuals and h_out must be contiguous bfloat16 [{b}, {k0.cols}] on {k0.device}")
-    ys = [_fp32_out(None, b, k.rows, k0.device) for k in kernels] if ys is None else \
-        [_fp32_out(t, b, k.rows, k0.device) for k, t in zip(kernels, ys)]
+        _require(y_prev_ss, "y_prev_ss", torch.float32, (b, (k0.cols + 15) // 16), k0.device)
+    for name, t in (("w1", w1), ("w2", w2)):
+        _require(t, name, torch.bfloat16, (k0.cols,), k0.device)
+    for name, t in (("residual_in", residual_in), ("residual_out", residual_out), ("h_out", h_out)):
+        _require(t, name, torch.bfloat16, (b, k0.cols), k0.device)
+    if ys is not None and len(ys) != len(kernels):
+        raise ValueError(f"ys must hold {len(kernels)} tensors, got {len(ys)}")
+    ys = [_fp32_out(None if ys is None else ys[i], b, k.rows, k0.device, f"ys[{i}]") for i, k in enumerate(kernels)]
     if gelu_out is not None:
         if len(kernels) != 2 or kernels[0].rows != kernels[1].rows:
             raise ValueError("the MLP gate takes two matrices with the same rows")
-        if gelu_out.dtype != torch.bfloat16 or tuple(gelu_out.shape) != (b, k0.rows) or not gelu_out.is_contiguous():
-            raise ValueError(f"gelu_out must be a contiguous bfloat16 [{b}, {k0.rows}] tensor")
+        _require(gelu_out, "gelu_out", torch.bfloat16, (b, k0.rows), k0.device)
     n = len(kernels)
     hs = (ctypes.c_void_p * n)(*[k.handle.raw.value for k in kernels])
     yp = (ctypes.c_void_p * n)(*[t.data_ptr() for t in ys])
@@ -348,11 +347,10 @@ def multiply_grouped(kernels, activations: torch.Tensor, launch: LaunchConfigura
         raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
     x = x.contiguous()
     b = x.shape[0]
-    if outs is None:
-        outs = [torch.empty((b, k.rows), dtype=torch.float32, device=k0.device) for k in kernels]
-    for k, o in zip(kernels, outs):
-        if o.shape != (b, k.rows) or o.dtype != torch.float32 or not o.is_contiguous():
-            raise ValueError("each out must be a contiguous float32 [B, rows] tensor")
+    if outs is not None and len(outs) != len(kernels):
+        raise ValueError(f"outs must hold {len(kernels)} tensors, got {len(outs)}")
+    outs = [_fp32_out(None if outs is None else outs[i], b, k.rows, k0.device, f"outs[{i}]")
+            for i, k in enumerate(kernels)]
     n = len(kernels)
     hs = (ctypes.c_void_p * n)(*[k.handle.raw.value for k in kernels])
     ys = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])

@@ -127,6 +127,34 @@ def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int =
     return tpb // WAVE_SIZE, blocks // rows
 
 
+def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 1, float32_activations: bool = False,
+                                 aligned_x: bool = True) -> LaunchConfiguration:
+    """This kernel's configuration for a launch built with the reference's
+    meaning: one 32-lane warp per output element, `threads_per_block` in
+    32..1024, and `blocks` x warps per block covering rows x batch
+    (lws/domain/launch/heuristic.py:46-87; the tuner's candidates,
+    search_space.py:14-36). The translation keeps the block's threads
+    (rounded up to whole wave64s, and for the MFMA kernel to a multiple of the
+    batch's tile rows per block, within the variant's limit) and splits no K
+    tiles, as the reference kernel never does. A launch that leaves outputs
+    uncovered, which the reference kernel would leave unwritten, is refused."""
+    tpb = int(launch.threads_per_block.value)
+    blocks = int(launch.blocks.value)
+    if tpb % 32 or not 32 <= tpb <= 1024:
+        raise ValueError(f"threads_per_block {tpb} must be a multiple of 32 in [32, 1024]")
+    if blocks <= 0 or blocks * (tpb // 32) < output_rows * batch:
+        raise ValueError(f"{blocks} blocks of {tpb // 32} warps do not cover {output_rows} rows x batch {batch}")
+    mfma = uses_mfma(batch, float32_activations)
+    generic = runs_generic(output_rows, k, float32_activations) or not aligned_x
+    hi = max_waves_per_block(batch, float32_activations, generic)
+    waves = -(-tpb // WAVE_SIZE)
+    if mfma:
+        lo = mfma_min_waves(batch)
+        waves = -(-waves // lo) * lo
+        hi = hi // lo * lo
+    return configuration(min(waves, hi), 1, output_rows, batch, float32_activations)
+
+
 def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_activations: bool = False) -> tuple[LaunchConfiguration, ...]:
     """Every (waves, splits) worth timing: waves per block up to the batch's
     limit (valid for the fused kernel and its raw twin alike), K splits up to

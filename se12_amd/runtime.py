@@ -318,6 +318,30 @@ def _contiguous_eager_attention(module, query, key, value, attention_mask, dropo
     return out.transpose(1, 2).contiguous(), weights
 
 
+# Attention implementations refused on a HIP device: transformers' eager
+# attention multiplies BF16 query [B, H, S, D] by key.transpose(2, 3), a view
+# with strides (H*S*D, S*D, 1, D); BF16 batched products whose right operand
+# is such a view have faulted MI355X GPUs (torch 2.10.0+rocm7.0 on ROCm 7.2).
+_FAULTING_ATTENTION = ("eager",)
+
+
+def resolve_attention(attn_implementation: str | None, device: torch.device) -> str | None:
+    """The attention implementation a model is built with: on a HIP device
+    the contiguous-key eager attention ("se12_eager") unless the caller names
+    another one, and never transformers' own "eager"."""
+    if device.type != "cuda":
+        return attn_implementation
+    if attn_implementation is None:
+        attn_implementation = CONTIGUOUS_EAGER
+    if attn_implementation in _FAULTING_ATTENTION:
+        raise ValueError(f"attn_implementation={attn_implementation!r} runs a BF16 batched product on a transposed "
+                         f"key view, which has faulted MI355X GPUs; use {CONTIGUOUS_EAGER!r} (the same computation "
+                         "with a contiguous key) or leave it None")
+    if attn_implementation == CONTIGUOUS_EAGER:
+        register_attention()
+    return attn_implementation
+
+
 def register_attention() -> str:
     """Registers the attention above with transformers as "se12_eager"; pass
     that name as `attn_implementation` to the original and the packed model
@@ -418,8 +442,7 @@ def load_packed(packed: Any, mode: str = "auto", order: str | None = None, devic
     if launch_lookup is None and mode != "exact" and kernel_factory is None:
         launch_lookup = tuned_lookup(dev, "order_matched" if order == "matched" else "fused", tuning_dir)
     make_kernel = kernel_factory or _default_kernel
-    if attn_implementation == CONTIGUOUS_EAGER:
-        register_attention()
+    attn_implementation = resolve_attention(attn_implementation, dev)
     extra = {"attn_implementation": attn_implementation} if attn_implementation else {}
     with torch.device("meta"):
         model = AutoModelForCausalLM.from_config(config, dtype=torch.bfloat16, **extra)
@@ -500,11 +523,13 @@ def load_reference(model_dir, device=None, order: str | None = "matched",
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     if launch_lookup is None:
         launch_lookup = tuned_lookup(dev, "order_matched" if order == "matched" else "raw", tuning_dir)
-    if attn_implementation == CONTIGUOUS_EAGER:
-        register_attention()
+    attn_implementation = resolve_attention(attn_implementation, dev)
     if model is None:
         extra = {"attn_implementation": attn_implementation} if attn_implementation else {}
         model = AutoModelForCausalLM.from_pretrained(str(model_dir), dtype=torch.bfloat16, **extra)
+    elif dev.type == "cuda" and getattr(model.config, "_attn_implementation", None) in _FAULTING_ATTENTION:
+        raise ValueError(f"the model was built with attn_implementation={model.config._attn_implementation!r}, which "
+                         f"faults MI355X GPUs; build it with {CONTIGUOUS_EAGER!r} (runtime.register_attention())")
     model = model.to(dev)
     for name, mod in list(model.named_modules()):
         if isinstance(mod, nn.Linear) and is_eligible(mod.weight):

@@ -1,0 +1,169 @@
+"""Parity at the full sizes of the measured workloads (the reference holds no
+fixtures for them: its fused-GEMV GPU tests are skip stubs,
+tests/test_spec_fused_gemv.py:135-180):
+
+- Gemma-2-9B gate_proj 14336x3584, N(0, 0.02) from numpy seed 0: the GPU
+  encoder's streams byte-identical to the oracle's; products at B = 1, 2, 4,
+  8, 16, 32 under the default launch within REL_TOL of the oracle's decode +
+  float32 matmul; the raw twin bit-identical to each.
+- Heavy-tailed (Student-t(3), std 0.02, 0.1% at +-8 sigma) Gemma-2-27B
+  down_proj 4608x36864: GPU encode byte-identical to the oracle's encode,
+  GPU decode equal to the input bits, the product within REL_TOL of the
+  oracle, the raw twin bit-identical under the default launch.
+- Heavy-tailed tied LM head 256000x2304: GPU encode then decode equal to the
+  input bits; the oracle decodes the GPU encoder's streams of three tile-row
+  slices (first, middle, last) back to the input and its product of each
+  slice matches the GPU's rows; fused and raw twin bit-identical under the
+  default launch.
+- The 26-layer Gemma-2-2B (hidden 2304, 8 / 4 heads of 256, intermediate
+  9216, vocab 256000, random init) after a 512-token prompt: 24
+  graph-replayed greedy steps in which the SE12 backend and the raw-BF16
+  twin give identical logits at every step and identical tokens.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import REL_TOL, bf16_tensor, heavy_tailed_bf16_device, max_rel_error
+from oracle import se12_codec as o
+
+pytestmark = pytest.mark.gpu
+
+BATCHES = (1, 2, 4, 8, 16, 32)
+
+
+def _host_streams(dt) -> dict:
+    return {"sm": dt.sm.cpu().numpy(), "ec": dt.ec.cpu().numpy(), "esc": dt.esc.cpu().numpy().reshape(-1, 16),
+            "fallback_bitmap": dt.fallback_bitmap.cpu().numpy(), "fallback_raw": dt.fallback_raw.cpu().numpy(),
+            "codebook": np.asarray(dt.codebook_host, dtype=np.uint8), "shape": (dt.rows, dt.cols)}
+
+
+def _assert_same_streams(got: dict, want: dict) -> None:
+    for name in ("sm", "ec", "esc", "fallback_bitmap", "fallback_raw", "codebook"):
+        a = np.asarray(got[name]).reshape(-1)
+        b = np.asarray(want[name]).reshape(-1)
+        assert a.dtype == b.dtype and np.array_equal(a, b), name
+
+
+def _tile_row_slice(dt, tr0: int, tr1: int) -> dict:
+    """The GPU encoder's streams of tile rows [tr0, tr1) as an encoding of
+    their own (tile-major streams are contiguous per tile row; the bitmap
+    bits and raw tiles of the range re-based to the slice)."""
+    tr, tc = dt.tile_grid
+    t0, t1 = tr0 * tc, tr1 * tc
+    bits = np.unpackbits(dt.fallback_bitmap.cpu().numpy(), count=tr * tc)
+    ranks = np.cumsum(bits.astype(np.int64)) - 1
+    fb = bits[t0:t1].astype(bool)
+    raw = dt.fallback_raw.cpu().numpy().reshape(-1, o.TILE_SIZE)[ranks[t0:t1][fb]].reshape(-1)
+    return {"sm": dt.sm[t0 * 4096:t1 * 4096].cpu().numpy(), "ec": dt.ec[t0 * 2048:t1 * 2048].cpu().numpy(),
+            "esc": dt.esc[t0 * 16:t1 * 16].cpu().numpy().reshape(-1, 16), "fallback_bitmap": np.packbits(fb),
+            "fallback_raw": raw.astype(np.int16), "codebook": np.asarray(dt.codebook_host, dtype=np.uint8),
+            "shape": (min(dt.rows, tr1 * 16) - tr0 * 16, dt.cols)}
+
+
+@pytest.fixture(scope="module")
+def gate_9b(gpu):
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+
+    rows, cols = 14336, 3584
+    bits = o.normal_bf16(rows, cols, seed=0, std=0.02)
+    w = bf16_tensor(bits, gpu)
+    dt = encode_on_device(w)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    _assert_same_streams(_host_streams(dt), enc)
+    # every batch's activations stacked: one oracle product covers them all
+    xs = {b: o.normal_bf16(b, cols, seed=1000 + b, std=1.0) for b in BATCHES}
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(np.concatenate([xs[b] for b in BATCHES])))
+    refs, r0 = {}, 0
+    for b in BATCHES:
+        refs[b] = ref[r0:r0 + b]
+        r0 += b
+    return Se12MatVecKernel(dt), RawBf16MatVecKernel(w), xs, refs
+
+
+@pytest.mark.parametrize("batch", BATCHES)
+def test_gate_9b_batch_sweep_default_launch(gpu, gate_9b, batch):
+    fused, raw, xs, refs = gate_9b
+    x = bf16_tensor(xs[batch], gpu)
+    y = fused.multiply(x)
+    yr = raw.multiply(x)
+    torch.cuda.synchronize()
+    assert max_rel_error(y, refs[batch]) <= REL_TOL
+    assert torch.equal(y, yr)
+
+
+def test_down_27b_heavy_tailed_full_size(gpu):
+    from se12_amd.hip import HipSe12WeightDecoder, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+
+    rows, cols = 4608, 36864
+    w = heavy_tailed_bf16_device(rows, cols, seed=27, device=gpu)
+    dt = encode_on_device(w)
+    assert torch.equal(HipSe12WeightDecoder().decode_to_device(dt), w)
+    bits = w.view(torch.int16).cpu().numpy()
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    _assert_same_streams(_host_streams(dt), enc)
+    assert int((o.unpack_codes(enc["ec"]) == o.ESCAPE_CODE).sum()) > 0   # the escape path is exercised
+    xb = o.normal_bf16(1, cols, seed=28, std=1.0)
+    x = bf16_tensor(xb, gpu)
+    y = Se12MatVecKernel(dt).multiply(x)
+    yr = RawBf16MatVecKernel(w).multiply(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, yr)
+    assert max_rel_error(y, o.gemv_reference(enc, o.bf16_bits_to_f32(xb))) <= REL_TOL
+
+
+def test_lm_head_heavy_tailed_full_size(gpu):
+    from se12_amd.hip import HipSe12WeightDecoder, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+
+    rows, cols = 256000, 2304
+    w = heavy_tailed_bf16_device(rows, cols, seed=256, device=gpu)
+    dt = encode_on_device(w)
+    assert torch.equal(HipSe12WeightDecoder().decode_to_device(dt), w)
+    xb = o.normal_bf16(1, cols, seed=257, std=1.0)
+    x = bf16_tensor(xb, gpu)
+    fused = Se12MatVecKernel(dt)
+    y = fused.multiply(x)
+    yr = RawBf16MatVecKernel(w).multiply(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, yr)
+    tr = dt.tile_grid[0]
+    escapes = 0
+    for tr0 in (0, tr // 2, tr - 8):
+        enc = _tile_row_slice(dt, tr0, tr0 + 8)
+        r0, r1 = tr0 * 16, tr0 * 16 + enc["shape"][0]
+        assert np.array_equal(o.decode(enc), w[r0:r1].view(torch.int16).cpu().numpy())
+        ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+        assert max_rel_error(y[:, r0:r1], ref) <= REL_TOL
+        escapes += int((o.unpack_codes(enc["ec"]) == o.ESCAPE_CODE).sum())
+    assert escapes > 0   # the slices exercise the escape path
+
+
+def test_gemma2_2b_full_decode_se12_equals_raw_twin(gpu):
+    from se12_amd.gemma2 import GEMMA2_2B, PROJECTIONS, Gemma2Decoder, Gemma2Weights
+    from se12_amd.hip import encode_on_device
+
+    w = Gemma2Weights.random(GEMMA2_2B, gpu, seed=0)
+    enc = {(li, n): encode_on_device(lw[n]) for li, lw in enumerate(w.layers) for n in PROJECTIONS}
+    enc["embed"] = encode_on_device(w.embed)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(5)
+    prompt = torch.randint(0, GEMMA2_2B.vocab, (1, 512), generator=g, device=gpu)
+    steps = 24
+    out = {}
+    for backend in ("se12", "raw"):
+        d = Gemma2Decoder(w, backend, 1, max_len=512 + steps + 8, encoded=enc)
+        d.prefill(prompt)
+        d.capture()
+        logits = []
+        for _ in range(steps):
+            d.decode(1)
+            logits.append(d.last_logits.clone())
+        torch.cuda.synchronize()
+        out[backend] = (d.tokens[:, :steps + 1].clone(), torch.stack(logits))
+        del d
+    assert torch.equal(out["se12"][1], out["raw"][1])
+    assert torch.equal(out["se12"][0], out["raw"][0])
+    assert torch.isfinite(out["se12"][1].float()).all()

@@ -32,6 +32,7 @@ tokens) whose decode tokens/s is the `decode_tok_s` field.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -74,6 +75,10 @@ def parse_args(argv=None):
     p.add_argument("--no-batch-sweep", action="store_true")
     p.add_argument("--no-stress", action="store_true")
     p.add_argument("--no-e2e", action="store_true", help="skip the Gemma-2-2B greedy decode")
+    p.add_argument("--no-micro", action="store_true", help="skip the microbenchmark / verdict files")
+    p.add_argument("--no-model", action="store_true", help="skip the roofline model's calibration")
+    p.add_argument("--reports", default=os.environ.get("LWS_VERDICT_DIR", "reports"),
+                   help="directory for micro-<slug>.json and verdict-<slug>.json")
     p.add_argument("--only-fused", action="store_true", help="skip the BF16 and raw-twin comparisons (profiling)")
     p.add_argument("--profile-down", action="store_true",
                    help="only the dominant kernel (26 down_proj launches per step) and a 256 MiB device copy of known "
@@ -222,21 +227,44 @@ def evict_caches(buf: torch.Tensor) -> None:
     torch.sum(buf)
 
 
-def time_graph(g, steps: int, warmup: int, flush=None) -> float:
-    """Mean ms per replay over `steps` replays, events on the replay stream."""
+class Timing(float):
+    """Mean ms per replay (the float value), with the median, p10 and p90 of
+    the per-replay times (the reference's statistics,
+    lws/domain/benchmark/statistics.py:46-53)."""
+
+    def __new__(cls, samples_ms):
+        import numpy as np
+
+        arr = np.asarray(samples_ms, dtype=np.float64)
+        obj = super().__new__(cls, float(arr.mean()))
+        obj.median = float(np.median(arr))
+        obj.p10 = float(np.percentile(arr, 10))
+        obj.p90 = float(np.percentile(arr, 90))
+        return obj
+
+    def stats_us(self, per: int = 1) -> dict:
+        """Median / p10 / p90 in microseconds per launch (`per` launches per replay)."""
+        return {"median_us": round(self.median * 1e3 / per, 3), "p10_us": round(self.p10 * 1e3 / per, 3),
+                "p90_us": round(self.p90 * 1e3 / per, 3)}
+
+
+def time_graph(g, steps: int, warmup: int, flush=None) -> Timing:
+    """ms per replay over `steps` replays, events on the replay stream. Without
+    a flush the replays run back to back between one pair of
+    synchronizations, an event between consecutive replays; with one, the
+    flush runs before each replay, outside its event pair."""
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
     if flush is None:
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(steps):
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record()
+        for i in range(steps):
             g.replay()
-        end.record()
-        end.synchronize()
-        return start.elapsed_time(end) / steps
-    total = 0.0
+            ev[i + 1].record()
+        ev[-1].synchronize()
+        return Timing([ev[i].elapsed_time(ev[i + 1]) for i in range(steps)])
+    samples = []
     for _ in range(steps):
         flush()
         start = torch.cuda.Event(enable_timing=True)
@@ -245,8 +273,8 @@ def time_graph(g, steps: int, warmup: int, flush=None) -> float:
         g.replay()
         end.record()
         end.synchronize()
-        total += start.elapsed_time(end)
-    return total / steps
+        samples.append(start.elapsed_time(end))
+    return Timing(samples)
 
 
 def cold_rotation(nbytes: int) -> int:
@@ -314,35 +342,45 @@ def heavy_tailed(n: int, k: int, seed: int, device) -> torch.Tensor:
 def stress(device) -> dict:
     """Batch-1 products at the tied LM head 256000x2304 and the Gemma-2-27B
     down_proj 4608x36864 with heavy-tailed weights (escape and fallback
-    paths), against hipBLASLt BF16; the cache is flushed before each launch."""
-    from se12_amd.hip import Se12MatVecKernel, encode_on_device
+    paths), against hipBLASLt BF16 and the raw twin: each timed over a
+    rotation of cold copies in one graph (at least 8 launches per replay, so
+    the replay's fixed cost of ~10 us spreads; HipBenchmarkTimer.
+    time_cold_rotation), median / p10 / p90 per launch."""
+    from se12_amd.hip import HipBenchmarkTimer, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+    from se12_amd.micro import cold_copies
 
-    flush_buf = torch.zeros(1 << 28, dtype=torch.float32, device=device)
+    timer = HipBenchmarkTimer(device.index)
     out = {}
     for name, n, k, seed in (("lm_head", 256000, 2304, 11), ("down_27b", 4608, 36864, 12)):
         w = heavy_tailed(n, k, seed, device)
         enc = encode_on_device(w)
-        kern = Se12MatVecKernel(enc, max_batch=1)
+        copies = cold_copies(2 * n * k)
+        ws = [w] + [w.clone() for _ in range(copies - 1)]
+        kerns = [Se12MatVecKernel(e, max_batch=1) for e in [enc] + [enc.clone() for _ in range(copies - 1)]]
         gen = torch.Generator(device=device)
         gen.manual_seed(seed + 100)
         x = torch.randn((1, k), generator=gen, device=device).to(torch.bfloat16)
-        y = torch.empty((1, n), dtype=torch.float32, device=device)
-        g = capture(lambda: kern.multiply(x, out=y))
-        us = time_graph(g, 10, 3, flush=lambda: evict_caches(flush_buf)) * 1e3
-        gb = capture(lambda: torch.nn.functional.linear(x, w))
-        us_b = time_graph(gb, 10, 3, flush=lambda: evict_caches(flush_buf)) * 1e3
-        lc = kern.default_launch(1)
-        out[name] = {"shape": [n, k], "us": round(us, 3), "se12_bytes": enc.byte_size(),
+        ys = [torch.empty((1, n), dtype=torch.float32, device=device) for _ in range(copies)]
+        st = timer.time_cold_rotation([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(kerns, ys)], 3, 10)
+        del kerns
+        st_b = timer.time_cold_rotation([lambda m=m: torch.nn.functional.linear(x, m) for m in ws], 3, 10)
+        raws = [RawBf16MatVecKernel(m, max_batch=1) for m in ws]
+        st_r = timer.time_cold_rotation([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(raws, ys)], 3, 10)
+        del raws
+        us, us_b, us_r = st.median_us, st_b.median_us, st_r.median_us
+        lc = Se12MatVecKernel(enc, max_batch=1).default_launch(1)
+        out[name] = {"shape": [n, k], "us": round(us, 3), "p10_us": round(st.p10_us, 3), "p90_us": round(st.p90_us, 3),
+                     "cold_copies": copies, "se12_bytes": enc.byte_size(),
                      "bytes_per_weight": round(enc.byte_size() / (n * k), 4),
                      "se12_gbps": round(enc.byte_size() / (us * 1e-6) / 1e9, 1),
                      "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
-                     "bf16_hipblaslt_us": round(us_b, 3), "speedup_of_se12": round(us_b / us, 4),
+                     "bf16_hipblaslt_us": round(us_b, 3), "raw_twin_us": round(us_r, 3),
+                     "speedup_of_se12": round(us_b / us, 4), "speedup_vs_faster_baseline": round(min(us_b, us_r) / us, 4),
                      "fallback_tiles": enc.fallback_tiles, "tiles": enc.tile_grid[0] * enc.tile_grid[1],
                      "launch": [lc.threads_per_block.value, lc.blocks.value]}
         log(f"[bench] stress {name}: {out[name]}")
-        del g, gb, kern, enc, w
+        del ws, enc, w, ys
         torch.cuda.empty_cache()
-    del flush_buf
     return out
 
 
@@ -402,12 +440,74 @@ def e2e_decode(device, prompt_len: int = 512, new_tokens: int = 128) -> dict:
     return out
 
 
+def roofline_model(device, props, per_shape: dict) -> dict:
+    """The reference's performance model (lws/domain/performance/roofline.py:
+    52-146) fed by this device: peak from hipDeviceProp (memory clock x bus
+    width), bandwidths and the graph launch cost measured here, each
+    kernel's cost per weight from cache-resident launches (a 2304x2304
+    matrix, 32 back-to-back launches in one graph), eta fitted from the raw
+    twin's cold latency at the 2304x9216 down_proj shape, and the predicted
+    fused / raw ratio against the measured one at every Gemma-2-2B shape."""
+    from se12_amd import roofline as rl
+    from se12_amd.hip import HipBenchmarkTimer, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+
+    timer = HipBenchmarkTimer(device.index)
+    facts = rl.DeviceFacts(hbm_peak_gbps=props.hbm_peak_gbps, copy_gbps=timer.measure_peak_copy_bandwidth(),
+                           stream_read_gbps=timer.measure_stream_read_bandwidth(),
+                           launch_us=timer.measure_graph_launch_us())
+    gen = torch.Generator(device=device)
+    gen.manual_seed(77)
+    hot = {"raw": [], "se12": []}
+    for n, k in rl.CALIBRATION_SHAPES:
+        w = (torch.randn((n, k), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+        x = torch.randn((1, k), generator=gen, device=device).to(torch.bfloat16)
+        y = torch.empty((1, n), dtype=torch.float32, device=device)
+        for name, kern in (("raw", RawBf16MatVecKernel(w, max_batch=1)),
+                           ("se12", Se12MatVecKernel(encode_on_device(w), max_batch=1))):
+            g = capture(lambda kern=kern: [kern.multiply(x, out=y) for _ in range(32)])
+            hot[name].append(time_graph(g, 20, 5).median * 1e3 / 32)
+            del g
+    cal = rl.calibrate(facts.copy_gbps, tuple(hot["raw"]), tuple(hot["se12"]), facts.launch_us)
+    fit = per_shape["down"]
+    eta = rl.fit_eta_from_raw(fit["raw_twin_us"], *fit["shape"], cal)
+    shapes = {}
+    for name, e in per_shape.items():
+        rep = rl.shape_report(*e["shape"], cal, eta, e["us"], e["raw_twin_us"])
+        shapes[name] = {kk: round(v, 4) for kk, v in rep.items()}
+        shapes[name]["launch_floor_us"] = round(rl.launch_floor_us(*e["shape"], facts), 3)
+    out = {"facts": {kk: round(v, 3) for kk, v in dataclasses.asdict(facts).items()},
+           "hbm_peak_published_gbps": rl.HBM_PEAK_PUBLISHED_GBPS,
+           "calibration": {"shapes": [list(sh) for sh in rl.CALIBRATION_SHAPES], "batch": 1,
+                           "raw_hot_us": [round(v, 3) for v in hot["raw"]],
+                           "se12_hot_us": [round(v, 3) for v in hot["se12"]], "launch_us": round(cal.launch_us, 3),
+                           "bandwidth_gbps": round(cal.bandwidth_gbps, 1),
+                           "raw_cost_ps_per_weight": round(cal.raw_cost_us_per_weight * 1e6, 4),
+                           "se12_cost_ps_per_weight": round(cal.se12_cost_us_per_weight * 1e6, 4)},
+           "eta": round(eta, 4), "eta_fit": "raw twin, 2304x9216 (down_proj), cold",
+           "per_shape": shapes}
+    log(f"[bench] model: {out['facts']} eta {eta:.3f}")
+    return out
+
+
+def cpu_model() -> str | None:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     """The oracle's numpy decode + float32 matmul of one 2304x9216 GEMV (the
-    Gemma-2-2B down_proj shape, N(0, 0.02) seed 0) on the host, BLAS limited
-    to one thread; median over repeated runs within the time budget."""
+    Gemma-2-2B down_proj shape, N(0, 0.02) seed 0) on the host: decode alone
+    and decode + matmul, each timed with the BLAS pool limited to one thread
+    (the value) and with every core the process may use; medians of at
+    least 5 runs within the time budget."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    from threadpoolctl import threadpool_info, threadpool_limits
 
     from oracle import se12_codec as o
 
@@ -415,20 +515,39 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     bits = o.normal_bf16(n, k, seed=0, std=0.02)
     enc = o.encode(bits.reshape(-1), n, k)
     x = o.bf16_bits_to_f32(o.normal_bf16(1, k, seed=1, std=1.0))
-    times = []
-    with threadpool_limits(limits=1):
-        t_end = time.perf_counter() + budget_s
-        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 30):
+    cores = len(os.sched_getaffinity(0))
+
+    def med(fn, budget):
+        times, t_end = [], time.perf_counter() + budget
+        while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 30):
             t0 = time.perf_counter()
-            o.gemv_reference(enc, x)
+            fn()
             times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+        return float(np.median(times)), len(times)
+
+    with threadpool_limits(limits=1):
+        dec_s, n_dec = med(lambda: o.decode(enc), budget_s / 4)
+        gemv_s, n_gemv = med(lambda: o.gemv_reference(enc, x), budget_s / 2)
+    with threadpool_limits(limits=cores):
+        gemv_mt_s, n_mt = med(lambda: o.gemv_reference(enc, x), budget_s / 4)
+    blas = [{"api": d.get("internal_api"), "version": d.get("version"), "threads": d.get("num_threads")}
+            for d in threadpool_info() if d.get("user_api") == "blas"]
     return {
-        "value": round(2.0 * n * k / med / 1e9, 4),
+        "value": round(2.0 * n * k / gemv_s / 1e9, 4),
         "unit": "GB/s",
         "cores": 1,
         "kind": "port",
-        "sample": f"one 2304x9216 GEMV at batch 1 (numpy decode + float32 matmul, 1 thread), median of {len(times)} runs, {med * 1e3:.1f} ms each",
+        "sample": f"one 2304x9216 GEMV at batch 1 (numpy decode + float32 matmul, 1 thread), median of {n_gemv} runs, "
+                  f"{gemv_s * 1e3:.1f} ms each",
+        "decode_only_ms": round(dec_s * 1e3, 3),
+        "decode_only_runs": n_dec,
+        "decode_gemv_ms": round(gemv_s * 1e3, 3),
+        "decode_gemv_all_cores_ms": round(gemv_mt_s * 1e3, 3),
+        "decode_gemv_all_cores_runs": n_mt,
+        "decode_gemv_all_cores_gbps": round(2.0 * n * k / gemv_mt_s / 1e9, 4),
+        "affinity_cores": cores,
+        "cpu_model": cpu_model(),
+        "blas": blas,
     }
 
 
@@ -504,6 +623,9 @@ def main(argv=None) -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "ms_per_step_median": round(ms.median, 4),
+        "ms_per_step_p10": round(ms.p10, 4),
+        "ms_per_step_p90": round(ms.p90, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -548,6 +670,10 @@ def main(argv=None) -> int:
         "shape": [down[0]["n"], down[0]["k"]],
         "launch": {"threads_per_block": launch.threads_per_block.value, "blocks": launch.blocks.value},
         "avg_launch_us": round(us_launch, 3),
+        "launch_stats": ms_down.stats_us(len(down)),
+        "peak_published": HBM_PEAK_GBPS,
+        "peak_from_device": round(props.hbm_peak_gbps, 1),
+        "frac_of_device_peak": round(achieved / props.hbm_peak_gbps, 4),
         "algorithmic_bytes_per_launch": bytes_launch,
         "bf16_equiv_gbps": round(2 * down[0]["n"] * down[0]["k"] / (us_launch * 1e-6) / 1e9, 1),
     }
@@ -610,13 +736,23 @@ def main(argv=None) -> int:
             per_shape[name] = {"shape": [n, k], "us": round(us, 3), "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
                                "se12_gbps": round(col[0]["enc"].byte_size() / (us * 1e-6) / 1e9, 1),
                                "launch": [lc.threads_per_block.value, lc.blocks.value]}
+            per_shape[name].update(ms_s.stats_us(len(col)))
             if not args.only_fused:
                 gb = capture(lambda col=col: [torch.nn.functional.linear(e["x"], e["w"]) for e in col])
                 us_b = time_graph(gb, 10, 3, flush=flush) * 1e3 / len(col)
+                rk = [RawBf16MatVecKernel(e["w"], max_batch=1) for e in col]
+                yr = [torch.empty_like(e["y"]) for e in col]
+                gr = capture(lambda col=col, rk=rk, yr=yr: [r.multiply(e["x"], out=y) for r, e, y in zip(rk, col, yr)])
+                us_r = time_graph(gr, 10, 3, flush=flush) * 1e3 / len(col)
+                del gb, gr, rk, yr
                 per_shape[name]["bf16_hipblaslt_us"] = round(us_b, 3)
+                per_shape[name]["raw_twin_us"] = round(us_r, 3)
+                per_shape[name]["speedup_vs_faster_baseline"] = round(min(us_b, us_r) / us, 4)
             log(f"[bench] {name} {n}x{k}: {per_shape[name]}")
         result["per_shape"] = per_shape
         del flush_buf
+        if not args.only_fused and not args.no_model:
+            result["model"] = roofline_model(dev, props, per_shape)
 
     if not args.no_batch_sweep:
         del stack, flat
@@ -629,6 +765,24 @@ def main(argv=None) -> int:
         result["e2e"] = e2e_decode(dev)
         result["decode_tok_s"] = result["e2e"]["se12"]["decode_tok_s"]
 
+    if not args.no_micro:
+        from se12_amd import micro
+
+        m, v = micro.run(device=dev, log=log)
+        paths = micro.write_reports(m, v, args.reports)
+        result["micro"] = {
+            "verdict": v["verdict"], "per_batch": {b: e["verdict"] for b, e in v["per_batch"].items()},
+            "peak_copy_bandwidth_gbps": round(v["peak_copy_bandwidth_gbps"], 1),
+            "rows": [{"shape": row["shape"], "batch": row["batch_size"],
+                      **{n: r.get("median_microseconds") and round(r["median_microseconds"], 3)
+                         for n, r in row["results"].items()},
+                      **({"ratio": round(row["shape_verdict"]["ratio"], 4),
+                          "baseline": row["shape_verdict"]["baseline"],
+                          "baseline_fraction_of_peak": round(row["shape_verdict"]["baseline_fraction_of_peak"], 3),
+                          "verdict": row["shape_verdict"]["verdict"]} if row["shape_verdict"] else {})}
+                     for row in m["results"]],
+            "files": [str(x) for x in paths],
+        }
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline()

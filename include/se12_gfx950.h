@@ -139,6 +139,15 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
  * lws/domain/launch/heuristic.py:46-87 re-derived for 256 CUs of wave64). */
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out);
 
+/* Reads `bytes` (16-byte aligned, whole 16-byte words counted) of device
+ * memory as a streaming read, the traffic of one pass over a weight matrix,
+ * for bandwidth measurement; the kernel writes to out (>= 8 words per compute
+ * unit) only in the rare case its XOR of the data equals a fixed constant.
+ * No reference counterpart: the reference measures a device copy only
+ * (lws/adapters/cuda/benchmark_timer.py:50-66); the roofline here also wants
+ * the read-only rate. Same stream rules as se12_gemv. */
+int se12_read_probe(const void* buf_dev, int64_t bytes, uint32_t* out_dev, int64_t out_elems, void* stream);
+
 /* Sets the compute-unit count the handle's default launches are derived for
  * (bind takes hipDeviceProp_t.multiProcessorCount). Host only. Replaces the
  * `sm_count` argument that Se12MatVecKernel / RawBf16MatVecKernel take at

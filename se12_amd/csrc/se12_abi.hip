@@ -386,6 +386,21 @@ static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t b
     *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, (2 * m + kg) / (2 * kg)));
 }
 
+int se12_read_probe(const void* buf_dev, int64_t bytes, uint32_t* out_dev, int64_t out_elems, void* stream) {
+    if (!buf_dev || !out_dev) return fail(SE12_E_INVALID, "se12_read_probe: NULL argument");
+    if (bytes < 16 || !aligned16(buf_dev))
+        return fail(SE12_E_INVALID, "se12_read_probe: needs a 16-byte aligned buffer of at least 16 bytes");
+    int dev = 0, cus = 0;
+    SE12_HIP(hipGetDevice(&dev));
+    SE12_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    const int64_t blocks = read_probe_blocks(cus);
+    if (out_elems < blocks)
+        return fail(SE12_E_CAPACITY, "se12_read_probe: out holds %lld words, the grid needs %lld", (long long)out_elems,
+                    (long long)blocks);
+    SE12_HIP(launch_read_probe(buf_dev, bytes / 16, out_dev, blocks, static_cast<hipStream_t>(stream)));
+    return SE12_OK;
+}
+
 int se12_set_compute_units(se12_handle* h, int32_t compute_units) {
     if (!h) return fail(SE12_E_INVALID, "se12_set_compute_units: NULL handle");
     if (compute_units < 1 || compute_units > (1 << 16))

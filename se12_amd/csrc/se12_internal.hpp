@@ -235,5 +235,8 @@ hipError_t launch_encode_histogram(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_count(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_scan(const EncodeArgs& a, hipStream_t stream);
 hipError_t launch_encode_write(const EncodeArgs& a, hipStream_t stream);
+// Streaming-read probe (se12_probe.hip): its grid for a device and the launch.
+int64_t read_probe_blocks(int32_t compute_units);
+hipError_t launch_read_probe(const void* buf, int64_t n16, uint32_t* out, int64_t blocks, hipStream_t stream);
 
 }  // namespace se12

@@ -309,6 +309,12 @@ class Se12DeviceTensor:
         """Algorithmic bytes of one pass (every stream + the codebook)."""
         return packed_byte_size(self.rows, self.cols, self.fallback_tiles)
 
+    def clone(self) -> "Se12DeviceTensor":
+        """A copy of every stream in new device memory."""
+        return dataclasses.replace(self, sm=self.sm.clone(), ec=self.ec.clone(), esc=self.esc.clone(),
+                                   codebook=self.codebook.clone(), fallback_bitmap=self.fallback_bitmap.clone(),
+                                   fallback_raw=self.fallback_raw.clone())
+
     @classmethod
     def from_host(cls, tensor: Any, device=None) -> "Se12DeviceTensor":
         """Uploads a host `Se12Tensor` (the reference container layout)."""

@@ -459,6 +459,9 @@ def codebook_from_histogram(counts) -> tuple[int, ...]:
 # ---------------------------------------------------------------------------
 
 
+HBM_TRANSFERS_PER_CLOCK = 4
+
+
 @dataclasses.dataclass(frozen=True)
 class DeviceProperties:
     """hipDeviceProp_t facts the roofline and the launch heuristic use."""
@@ -474,6 +477,26 @@ class DeviceProperties:
     clock_khz: int
     memory_clock_khz: int
     memory_bus_width_bits: int
+    pci_domain_id: int = 0
+    pci_bus_id: int = 0
+    pci_device_id: int = 0
+    ecc_enabled: bool = False
+    kernel_timeout: bool = False
+    runtime_version: int = 0
+    driver_version: int = 0
+
+    @property
+    def pci_address(self) -> str:
+        """"dddd:bb:dd.0", the device's PCI location (sysfs naming)."""
+        return f"{self.pci_domain_id:04x}:{self.pci_bus_id:02x}:{self.pci_device_id:02x}.0"
+
+    @property
+    def hbm_peak_gbps(self) -> float:
+        """Peak HBM bandwidth from hipDeviceProp's memory clock and bus width.
+        HBM3 / HBM3E move HBM_TRANSFERS_PER_CLOCK data words per pin per
+        reported clock: MI355X reports 2.0 GHz on an 8192-bit interface,
+        i.e. 8 Gb/s per pin, 8,192 GB/s (the published peak is 8.0 TB/s)."""
+        return self.memory_clock_khz * 1e3 * HBM_TRANSFERS_PER_CLOCK * self.memory_bus_width_bits / 8.0 / 1e9
 
     @property
     def slug(self) -> str:
@@ -498,7 +521,10 @@ class HipGpuProbe:
             wavefront_size=info.wavefront_size, l2_bytes=info.l2_bytes, lds_bytes_per_cu=info.lds_bytes_per_cu,
             lds_bytes_per_block=info.lds_bytes_per_block, total_memory_bytes=info.total_memory_bytes,
             clock_khz=info.clock_khz, memory_clock_khz=info.memory_clock_khz,
-            memory_bus_width_bits=info.memory_bus_width_bits,
+            memory_bus_width_bits=info.memory_bus_width_bits, pci_domain_id=info.pci_domain_id,
+            pci_bus_id=info.pci_bus_id, pci_device_id=info.pci_device_id, ecc_enabled=bool(info.ecc_enabled),
+            kernel_timeout=bool(info.kernel_timeout), runtime_version=info.runtime_version,
+            driver_version=info.driver_version,
         )
 
     def software_versions(self) -> dict:
@@ -547,9 +573,30 @@ class HipBenchmarkTimer:
         dirty lines whose write-back competes with the timed operation."""
         torch.sum(self.flush_buffer)
 
-    def time_operation(self, operation: Callable[[], Any], warmup: int = 25, timed: int = 100, flush: bool = True) -> LatencyStats:
+    def time_operation(self, operation: Callable[[], Any], warmup: int = 25, timed: int = 100, flush: bool = True,
+                       graph: bool = False) -> LatencyStats:
+        """Microseconds per call, one event pair per sample on the current
+        stream. `graph=True` captures the operation once in a HIP graph and
+        times its replays, as a decode runtime issues it: without the ~2 us a
+        host-side dispatch adds to every eager launch."""
+        run = operation
+        if graph:
+            for _ in range(3):
+                operation()
+            cur = torch.cuda.current_stream()
+            side = torch.cuda.Stream()
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                operation()
+            cur.wait_stream(side)
+            torch.cuda.synchronize(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                operation()
+            torch.cuda.synchronize(self.device)
+            run = g.replay
         for _ in range(warmup):
-            operation()
+            run()
         torch.cuda.synchronize(self.device)
         out = []
         for _ in range(timed):
@@ -558,11 +605,79 @@ class HipBenchmarkTimer:
             s = torch.cuda.Event(enable_timing=True)
             e = torch.cuda.Event(enable_timing=True)
             s.record()
-            operation()
+            run()
             e.record()
             e.synchronize()
             out.append(s.elapsed_time(e) * 1000.0)
         return latency_stats(out)
+
+    def time_cold_rotation(self, operations, warmup: int = 25, timed: int = 100) -> LatencyStats:
+        """Microseconds per launch of `operations`, each reading its own copy
+        of the data (together several times L2 + Infinity Cache, so every
+        launch reads HBM), captured back to back in one HIP graph: each sample
+        is one replay divided by the launches in it. This is how a decode
+        step issues its products; a graph of a single launch instead carries
+        a per-replay cost of ~10 us on this GPU, and an eager launch ~2 us of
+        host dispatch."""
+        ops = list(operations)
+
+        def seq():
+            for op in ops:
+                op()
+
+        seq()
+        cur = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            seq()
+        cur.wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            seq()
+        torch.cuda.synchronize(self.device)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize(self.device)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(timed + 1)]
+        ev[0].record()
+        for i in range(timed):
+            g.replay()
+            ev[i + 1].record()
+        ev[-1].synchronize()
+        out = latency_stats([ev[i].elapsed_time(ev[i + 1]) * 1000.0 / len(ops) for i in range(timed)])
+        del g
+        return out
+
+    def measure_stream_read_bandwidth(self, nbytes: int = 1 << 30, copies: int = 4) -> float:
+        """GB/s of the library's streaming-read probe over `copies` buffers of
+        `nbytes` (each over 4x L2 + Infinity Cache), one launch per buffer in
+        one graph: the read-only traffic of a weight pass."""
+        dev = f"cuda:{self.device}"
+        bufs = [torch.zeros(nbytes, dtype=torch.uint8, device=dev) for _ in range(copies)]
+        sink = torch.zeros(1 << 16, dtype=torch.int32, device=dev)
+        lib = nat.lib()
+
+        def probe(b):
+            return lambda: nat.check(lib.se12_read_probe(nat.ptr(b), b.numel(), nat.ptr(sink), sink.numel(),
+                                                         nat.stream_ptr()))
+
+        st = self.time_cold_rotation([probe(b) for b in bufs], warmup=3, timed=10)
+        del bufs
+        return nbytes / (st.median_us * 1e-6) / 1e9
+
+    def measure_graph_launch_us(self, launches: int = 64) -> float:
+        """Microseconds per node of a HIP graph of `launches` dependent
+        one-element kernels: the fixed cost a launch adds to a decode step."""
+        t = torch.zeros(1, dtype=torch.float32, device=f"cuda:{self.device}")
+
+        def chain():
+            for _ in range(launches):
+                t.add_(1.0)
+
+        st = self.time_operation(chain, warmup=5, timed=20, flush=False, graph=True)
+        return st.median_us / launches
 
     def measure_peak_copy_bandwidth(self, nbytes: int = 1 << 30) -> float:
         """GB/s of a device-to-device copy of `nbytes` (read + write counted),

@@ -50,6 +50,9 @@ from .packed import PackedModel, is_eligible, read_packed, write_packed_file
 
 VERDICT_BATCHES = (1, 4, 16)
 GO_RATIO_THRESHOLD = 0.95
+# a comparison is valid only where the baseline reaches this fraction of the
+# measured copy bandwidth (lws/domain/benchmark/verdict.py:12,40-50)
+PEAK_BANDWIDTH_FRACTION = 0.70
 MODES = ("exact", "fused", "auto")
 
 
@@ -76,7 +79,12 @@ class FusedPolicy:
                 "fused_batches": {b: self.fused_for(b) for b in (1, 2, 4, 8, 16, 17)}}
 
 
-def shape_verdict(ratio: float) -> str:
+def shape_verdict(ratio: float, baseline_fraction_of_peak: float | None = None) -> str:
+    """GO when the fused median is at most 0.95 x the faster lossless
+    baseline's, NO-GO otherwise; INCONCLUSIVE when that baseline reaches less
+    than 70% of the measured copy bandwidth (verdict.py:40-62)."""
+    if baseline_fraction_of_peak is not None and baseline_fraction_of_peak < PEAK_BANDWIDTH_FRACTION:
+        return "INCONCLUSIVE"
     return "GO" if ratio <= GO_RATIO_THRESHOLD else "NO-GO"
 
 
@@ -87,15 +95,25 @@ def aggregate_verdict(verdicts) -> str:
     return "GO" if all(v == "GO" for v in verdicts) else "NO-GO"
 
 
-def verdict_payload(gpu_slug: str, arch: str, ratios: dict[int, list[tuple[Any, float]]]) -> dict:
+def verdict_payload(gpu_slug: str, arch: str, ratios: dict[int, list[tuple]]) -> dict:
     """The verdict file for one GPU from fused/baseline median ratios per
-    batch size: {batch: [(shape, ratio), ...]}."""
+    batch size: {batch: [(shape, ratio) or (shape, ratio, baseline fraction
+    of the measured copy peak), ...]}."""
     per_batch = {}
     for b, items in sorted(ratios.items()):
-        per_shape = [{"shape": list(shape), "ratio": float(r), "verdict": shape_verdict(float(r))} for shape, r in items]
+        per_shape = []
+        for item in items:
+            shape, r = item[0], float(item[1])
+            frac = float(item[2]) if len(item) > 2 and item[2] is not None else None
+            entry = {"shape": list(shape), "ratio": r, "verdict": shape_verdict(r, frac)}
+            if frac is not None:
+                entry["baseline_fraction_of_peak"] = frac
+            per_shape.append(entry)
         per_batch[str(b)] = {"verdict": aggregate_verdict(p["verdict"] for p in per_shape), "per_shape": per_shape}
     one = per_batch.get("1", {"verdict": "INCONCLUSIVE", "per_shape": []})
-    return {"gpu_slug": gpu_slug, "arch": arch, "verdict": one["verdict"],
+    # compute_capability: the reference's field name (micro.py:215-228),
+    # holding the gfx architecture here
+    return {"gpu_slug": gpu_slug, "arch": arch, "compute_capability": arch, "verdict": one["verdict"],
             "per_shape": [{"ratio": p["ratio"], "verdict": p["verdict"]} for p in one["per_shape"]],
             "per_batch": per_batch}
 

@@ -114,6 +114,7 @@ SIGNATURES = {
     "se12_set_compute_units": (c_i32, [c_void_p, c_i32]),
     "se12_read_probe": (c_i32, [c_void_p, c_i64, c_void_p, c_i64, c_void_p]),
     "se12_gemv": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, ctypes.POINTER(Launch), c_void_p]),
+    "se12_gemv_noalloc": (c_i32, [c_void_p, c_void_p, c_i32, c_i32, c_void_p, ctypes.POINTER(Launch), c_void_p]),
     "se12_gemv_grouped": (
         c_i32,
         [ctypes.POINTER(c_void_p), c_i32, c_void_p, c_i32, c_i32, ctypes.POINTER(c_void_p), ctypes.POINTER(Launch), c_void_p],

@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -463,9 +464,21 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // The launches of one product over `count` handles that share x (a single
 // matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped): one MFMA
 // launch for all rows, or one dot2 launch per 4 rows.
+// Device memory the kernels of one product use beyond inputs and outputs:
+// split-K partial sums and arrival counters (zero between launches: the last
+// block to arrive resets its counter). By default each handle's own,
+// allocated at bind; se12_gemv_noalloc passes the library's static scratch.
+struct Workspace {
+    float* partial;
+    int64_t partial_elems;
+    int32_t* counters;
+    int64_t counter_elems;
+};
+
 static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, const void* x, int32_t x_dtype,
                       int32_t batch, float* const* ys, const se12_launch* launch, void* stream,
-                      const GemvEpilogue* epi = nullptr, const GemvPrologue* pro = nullptr) {
+                      const GemvEpilogue* epi = nullptr, const GemvPrologue* pro = nullptr,
+                      const Workspace* ws = nullptr) {
     if (count < 1 || count > kMaxGroup) return fail(SE12_E_INVALID, "%s: %d matrices, expected 1..%d", fn, count, kMaxGroup);
     if (!x) return fail(SE12_E_INVALID, "%s: NULL x", fn);
     if (x_dtype != SE12_X_BF16 && x_dtype != SE12_X_F32) return fail(SE12_E_INVALID, "%s: unknown x_dtype %d", fn, x_dtype);
@@ -532,11 +545,21 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     DeviceScope ds;
     SE12_HIP(ds.enter(h0->device));
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (splits > 1)
+    if (ws) {
+        if (count != 1 || epi || pro) return fail(SE12_E_INVALID, "%s: a workspace serves one plain product", fn);
+        if (gemv_counter_count(h0->TR) > ws->counter_elems)
+            return fail(SE12_E_CAPACITY, "%s: %d tile rows need %lld arrival counters, the scratch holds %lld", fn,
+                        h0->TR, (long long)gemv_counter_count(h0->TR), (long long)ws->counter_elems);
+        if (splits > 1 && (int64_t)splits * b_first * h0->Np > ws->partial_elems)
+            return fail(SE12_E_CAPACITY, "%s: %d K splits x %d batch rows x %lld rows need %lld partial sums, the "
+                        "scratch holds %lld", fn, splits, b_first, (long long)h0->Np,
+                        (long long)splits * b_first * h0->Np, (long long)ws->partial_elems);
+    } else if (splits > 1) {
         for (int32_t i = 0; i < count; ++i)
             if ((int64_t)splits * b_first * hs[i]->Np > hs[i]->partial_elems)
                 return fail(SE12_E_CAPACITY, "%s: %d K splits at batch %d exceed handle %d's split-K workspace", fn,
                             splits, batch, i);
+    }
     // the x prologue runs in the dot2 kernel when its rows fit the block's
     // LDS; the caller has checked the rest
     const bool fuse_pro = pro && !mfma && !generic &&
@@ -575,8 +598,8 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.wraw = h->wraw;
             a.x = static_cast<const char*>(x) + (size_t)b0 * h->K * esize;
             a.y = ys[i] + (size_t)b0 * h->N;
-            a.partial = h->partial;
-            a.counters = h->counters;
+            a.partial = ws ? ws->partial : h->partial;
+            a.counters = ws ? ws->counters : h->counters;
             a.N = h->N;
             a.K = h->K;
             a.Np = h->Np;
@@ -637,6 +660,74 @@ int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, flo
     se12_handle* hs[1] = {h};
     float* ys[1] = {y};
     return gemv_group("se12_gemv", hs, 1, x, x_dtype, batch, ys, launch, stream);
+}
+
+}  // extern "C"
+
+// The zero-allocation product's scratch: one array per device (each GPU the
+// library runs on holds its own copy until the process ends), arrival
+// counters first, split-K partial sums after them. In host code `scratch`
+// names a host-side stand-in, not device memory: only the address
+// hipGetSymbolAddress returns for the current device may reach a kernel or
+// any HIP call.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+constexpr size_t kScratchCounterBytes = size_t(256) << 10;
+static_assert(kScratchCounterBytes % 256 == 0 && kScratchCounterBytes < kScratchBytes, "scratch layout");
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kScratchMaxDevices = 64;
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[kScratchMaxDevices] = {};
+
+__global__ void scratch_clear_kernel(uint32_t* p, int64_t words) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+// The device address of `scratch` on `device` (current), set up on the
+// first call there: hipGetSymbolAddress, then the counters cleared by a
+// kernel on `stream` (a fill kernel, so that a caller capturing the call
+// records no memset node).
+int scratch_for_device(int device, hipStream_t stream, uint8_t** out) {
+    if (device < 0 || device >= kScratchMaxDevices)
+        return fail(SE12_E_DEVICE, "se12_gemv_noalloc: device %d beyond the %d the scratch table serves", device,
+                    kScratchMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* p = nullptr;
+        SE12_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(SE12_E_HIP, "se12_gemv_noalloc: hipGetSymbolAddress gave NULL");
+        hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint32_t*>(p),
+                           (int64_t)(kScratchCounterBytes / sizeof(uint32_t)));
+        SE12_HIP(hipGetLastError());
+        g_scratch_ptr[device] = static_cast<uint8_t*>(p);
+    }
+    *out = g_scratch_ptr[device];
+    return SE12_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int se12_gemv_noalloc(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, float* y,
+                      const se12_launch* launch, void* stream) {
+    if (!h) return fail(SE12_E_INVALID, "se12_gemv_noalloc: NULL handle");
+    if (!x || !y) return fail(SE12_E_INVALID, "se12_gemv_noalloc: NULL x or y");
+    uint8_t* base = nullptr;
+    {
+        DeviceScope ds;
+        SE12_HIP(ds.enter(h->device));
+        if (int rc = scratch_for_device(h->device, static_cast<hipStream_t>(stream), &base)) return rc;
+    }
+    Workspace ws{reinterpret_cast<float*>(base + kScratchCounterBytes),
+                 (int64_t)((kScratchBytes - kScratchCounterBytes) / sizeof(float)), reinterpret_cast<int32_t*>(base),
+                 (int64_t)(kScratchCounterBytes / sizeof(int32_t))};
+    se12_handle* hs[1] = {h};
+    float* ys[1] = {y};
+    return gemv_group("se12_gemv_noalloc", hs, 1, x, x_dtype, batch, ys, launch, stream, nullptr, nullptr, &ws);
 }
 
 int se12_gemv_grouped(se12_handle* const* handles, int32_t count, const void* x, int32_t x_dtype, int32_t batch,

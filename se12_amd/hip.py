@@ -157,6 +157,17 @@ class _GemvBase:
     def default_launch(self, batch: int) -> LaunchConfiguration:
         return self.handle.default_launch(batch)
 
+    def multiply_noalloc(self, activations: torch.Tensor, out: torch.Tensor,
+                         launch: LaunchConfiguration | None = None) -> torch.Tensor:
+        """`multiply` through se12_gemv_noalloc: the library allocates nothing
+        (its split-K scratch is a static per-GPU array shared by every such
+        call on the GPU, so overlapping calls race); `out` is required."""
+        x, xd = _activations(activations, self.cols, self.device)
+        out = _require(out, "out", torch.float32, (x.shape[0], self.rows), self.device)
+        nat.check(nat.lib().se12_gemv_noalloc(self.handle.raw, nat.ptr(x), xd, x.shape[0], nat.ptr(out),
+                                              _launch_struct(launch), nat.stream_ptr()))
+        return out
+
     def multiply_rmsnorm(self, activations: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, residual: torch.Tensor,
                          out: torch.Tensor, eps: float, y: torch.Tensor | None = None,
                          launch: LaunchConfiguration | None = None) -> torch.Tensor:

@@ -22,7 +22,7 @@ INCLUDE = ROOT / "include"
 LIBDIR = PKG / "_lib"
 LIBNAME = "libse12_gfx950.so"
 SOURCES = ("se12_abi.hip", "se12_gemv.hip", "se12_gemm.hip", "se12_decode.hip", "se12_encode.hip", "se12_step.hip",
-           "se12_probe.hip")
+           "se12_probe.hip", "se12_gemm_rx.hip")
 ARCH = "gfx950"
 
 # Packed-FP32 VALU forms are disabled for every HIP unit (hipcc's host pass

@@ -304,6 +304,9 @@ int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_
 // launch, one pass over the weights); FP32 activations and smaller batches
 // the dot2 kernel, 4 rows per launch.
 static bool uses_mfma(int32_t batch, bool xf32) { return !xf32 && batch >= kGemmMinBatch; }
+static bool rx_fits(se12_handle* const* hs, int32_t count, int32_t batch);
+static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
+                              int32_t* blocks_out);
 
 static int max_threads_for(int32_t bl, bool xf32, bool generic) {
     return std::min(gemv_max_threads(bl, xf32, false, 1, 0, generic), gemv_max_threads(bl, xf32, true, 1, 0, generic));
@@ -417,6 +420,13 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
     const bool generic = h->K % SE12_TILE_COLS != 0 ||
                          (h->format == SE12_FORMAT_RAW_BF16 && h->N % SE12_TILE_ROWS != 0);
     se12_handle* hs[1] = {const_cast<se12_handle*>(h)};
+    if (uses_mfma(batch, false) && !generic && rx_fits(hs, 1, batch)) {
+        int32_t blocks;
+        rx_default_launch(hs, 1, batch, &waves, &blocks);
+        out->threads_per_block = waves * 64;
+        out->blocks = blocks;
+        return SE12_OK;
+    }
     if (uses_mfma(batch, false)) {
         gemm_default_launch(hs, 1, batch, generic, &waves, &splits);
         out->threads_per_block = waves * 64;
@@ -464,6 +474,57 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // The launches of one product over `count` handles that share x (a single
 // matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped): one MFMA
 // launch for all rows, or one dot2 launch per 4 rows.
+// The resident-x batched kernel serves FAST launches of BF16 x with
+// kRxMinBatch or more rows, or kGemmMinBatch or more over at least
+// kRxMinTiles tiles, whose x fits a block's LDS beside the pair table, on
+// matrices of whole tile rows (both formats alike, so that a fused kernel and
+// its raw twin always run the same kernel and stay bit-identical). Below
+// those sizes the x-slab kernel measured as fast or faster (14336 x 3584 at 8
+// rows: 20.8 against 22.3 us; 4096 x 14336 at 5 rows: 29.5 against 26.6).
+constexpr int32_t kRxMinBatch = 9;
+constexpr int64_t kRxMinTiles = 14336;
+
+static bool rx_fits(se12_handle* const* hs, int32_t count, int32_t batch) {
+    int64_t tiles = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (hs[i]->N % SE12_TILE_ROWS != 0) return false;
+        tiles += (int64_t)hs[i]->TR * hs[i]->TC;
+    }
+    if (batch < kRxMinBatch && tiles < kRxMinTiles) return false;
+    return (int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= hs[0]->lds_per_block;
+}
+
+static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
+    int64_t tr = 1;
+    for (int32_t i = 0; i < count; ++i) tr = std::max<int64_t>(tr, hs[i]->TR);
+    return tr;
+}
+
+// Default launch of the resident-x kernel: 12 waves per block (3 per SIMD,
+// the kernel's register limit) and one block per CU, fewer where a matrix
+// has fewer tile rows than its share of the CUs. Where rows are few, the K
+// groups (rx_kgroups) put several waves on each row.
+static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
+                              int32_t* blocks_out) {
+    (void)batch;
+    const int64_t cus = std::max<int32_t>(1, hs[0]->cu_count);
+    const int64_t per_matrix = std::max<int64_t>(1, std::min<int64_t>(rx_max_blocks(hs, count), ceil_div(cus, count)));
+    *waves_out = kRxMaxThreads / 64;
+    *blocks_out = (int32_t)(per_matrix * count);
+}
+
+static GemvPlan plan_rx(bool raw, int32_t batch, int32_t waves, int32_t blocks, int64_t k, size_t lds) {
+    GemvPlan p{};
+    p.batch = batch;
+    p.raw = raw;
+    p.waves = waves;
+    p.blocks = blocks;
+    p.lds = std::max(lds, rx_lds_bytes(k, batch));
+    p.g = 1;
+    p.pf = 1;
+    return p;
+}
+
 // Device memory the kernels of one product use beyond inputs and outputs:
 // split-K partial sums and arrival counters (zero between launches: the last
 // block to arrive resets its counter). By default each handle's own,
@@ -503,11 +564,29 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     for (int32_t i = 0; i < count; ++i)
         generic = generic || (raw && (hs[i]->N % SE12_TILE_ROWS != 0 || !aligned16(hs[i]->wraw)));
     const bool mfma = uses_mfma(batch, xf32);
+    const bool rx = mfma && !generic && rx_fits(hs, count, batch);
     const int32_t step = mfma ? batch : kGemvMaxBatchPerLaunch;
     const int32_t b_first = std::min<int32_t>(batch, step);
     int32_t waves, splits;
+    int32_t rx_blocks = 0;
     int64_t grid_rows = tr_total;  // grid rows per split: tile rows, or row blocks (MFMA)
-    if (launch) {
+    if (rx) {
+        splits = 1;
+        if (launch) {
+            if (launch->threads_per_block < 64 || launch->threads_per_block > kRxMaxThreads ||
+                launch->threads_per_block % 64 != 0)
+                return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d",
+                            fn, launch->threads_per_block, kRxMaxThreads, batch);
+            if (launch->blocks <= 0 || launch->blocks % count != 0 || launch->blocks / count > rx_max_blocks(hs, count))
+                return fail(SE12_E_INVALID, "%s: blocks %d must be %d x 1..%lld (blocks per matrix, at most its tile "
+                            "rows)", fn, launch->blocks, count, (long long)rx_max_blocks(hs, count));
+            waves = launch->threads_per_block / 64;
+            rx_blocks = launch->blocks;
+        } else {
+            rx_default_launch(hs, count, batch, &waves, &rx_blocks);
+        }
+        grid_rows = rx_blocks;
+    } else if (launch) {
         const int max_threads = mfma ? (generic ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
                                      : max_threads_for(b_first, xf32, generic);
         const int min_threads = mfma ? 64 * gemm_min_waves(batch) : 64;
@@ -586,6 +665,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         g.count = count;
         g.rows_per_block = mfma ? gemm_min_waves(bl) : 1;
         int32_t start = 0;
+        size_t rx_lds = 0;
         for (int32_t i = 0; i < count; ++i) {
             const se12_handle* h = hs[i];
             GemvArgs& a = g.m[i];
@@ -605,14 +685,16 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.Np = h->Np;
             a.TR = h->TR;
             a.TC = h->TC;
-            a.S = splits;
+            a.S = rx ? rx_kgroups(h->TR, h->TC, waves, rx_blocks / count) : splits;
+            rx_lds = std::max(rx_lds, rx ? rx_lds_total(h->K, bl, waves, a.S) : 0);
             g.tr_start[i] = start;
             start += mfma ? (int32_t)ceil_div(h->TR, gemm_min_waves(bl)) : h->TR;
         }
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);
-        GemvPlan p = mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
-                          : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
+        GemvPlan p = rx     ? plan_rx(raw, bl, waves, rx_blocks, h0->K, rx_lds)
+                     : mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
+                            : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
         if (fuse_pro) {
             g.pro = *pro;
             g.pro.y_prev += (size_t)b0 * h0->K;
@@ -633,7 +715,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         if ((int64_t)(p.lds + kLutBytes) > h0->lds_per_block)
             return fail(SE12_E_CAPACITY, "%s: launch needs %zu bytes of LDS, the device allows %lld", fn, p.lds,
                         (long long)h0->lds_per_block);
-        hipError_t e = mfma ? launch_gemm(g, bl, p, st) : launch_gemv(g, p, st);
+        hipError_t e = rx ? launch_gemm_rx(g, bl, p, st) : mfma ? launch_gemm(g, bl, p, st) : launch_gemv(g, p, st);
         if (e != hipSuccess) return fail(SE12_E_HIP, "%s launch: %s", fn, hipGetErrorString(e));
     }
     if (epi && !fuse_epi) {

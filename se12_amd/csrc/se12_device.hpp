@@ -290,21 +290,28 @@ __device__ __forceinline__ void or_pattern_word(uint32_t pat[4][8], uint32_t wor
 // Patches the n (1..kListedEscapes) listed escapes of a tile: escape k sits
 // at pos_k = row * 256 + col and takes esc slot k. Everything but the final
 // OR is wave-uniform (scalar), so an escape costs a few instructions.
-// Two lane layouts of a tile's 16 x 256 weights, 16 per lane in each of 4
-// parts (pat[part][word], word = pair of columns):
+// Three lane layouts of a tile's 16 x 256 weights, 16 consecutive columns
+// of one row (a column block, col / 16) per lane in each of 4 parts
+// (pat[part][word], word = pair of columns):
 //   chunk layout (dot2, decode): part j = rows 4j..4j+3, lane 16 (row % 4) +
-//     col / 16 holds 16 consecutive columns of its row;
-//   row layout (MFMA): part p = columns 64p..64p+63, lane row + 16 ((col %
-//     64) / 16) holds 16 consecutive columns of its row.
-template <bool ROWS>
+//     block;
+//   row layout (se12_gemm.hip): part p = columns 64p..64p+63, lane row + 16
+//     (block % 4);
+//   block layout (se12_gemm_rx.hip): part = block % 4, lane row + 16 (block
+//     / 4).
+enum TileLayout { kChunkLayout, kRowLayout, kBlockLayout };
+
+template <int LAYOUT>
 __device__ __forceinline__ void patch_listed_escapes(uint32_t pat[4][8], uint4 pos, uint4 esc, uint32_t n,
                                                      uint32_t lane) {
     for (uint32_t k = 0; k < n; ++k) {
         const uint32_t w = k < 4u ? (k < 2u ? pos.x : pos.y) : (k < 6u ? pos.z : pos.w);
         const uint32_t p = (k & 1u) ? (w >> 16) : (w & 0xFFFFu);
-        const uint32_t row = (p >> 8) & 15u, col = p & 255u;
-        const uint32_t owner = ROWS ? (row | (((col >> 4) & 3u) << 4)) : (((row & 3u) << 4) | (col >> 4));
-        const uint32_t part = ROWS ? (col >> 6) : (row >> 2);
+        const uint32_t row = (p >> 8) & 15u, col = p & 255u, block = col >> 4;
+        const uint32_t owner = LAYOUT == kChunkLayout ? (((row & 3u) << 4) | block)
+                               : LAYOUT == kRowLayout ? (row | ((block & 3u) << 4))
+                                                      : (row | ((block >> 2) << 4));
+        const uint32_t part = LAYOUT == kChunkLayout ? (row >> 2) : LAYOUT == kRowLayout ? (block >> 2) : (block & 3u);
         const uint32_t word = (part << 3) | ((col & 15u) >> 1);
         const uint32_t v = esc_byte(esc, k) << ((col & 1u) ? 23u : 7u);
         or_pattern_word(pat, word, lane == owner ? v : 0u);
@@ -313,11 +320,11 @@ __device__ __forceinline__ void patch_listed_escapes(uint32_t pat[4][8], uint4 p
 
 // The escapes of a tile read through the pair table (at most
 // kListedEscapes: bind turns tiles with more into raw tiles).
-template <bool ROWS = false>
+template <int LAYOUT = kChunkLayout>
 __device__ __forceinline__ void patch_tile_escapes(uint32_t pat[4][8], uint32_t info, const TileSide& side, int g,
                                                    uint32_t lane) {
     const uint32_t n = info_escapes(info);
-    if (n != 0u) patch_listed_escapes<ROWS>(pat, side_pos(side, g), side_esc(side, g), n, lane);
+    if (n != 0u) patch_listed_escapes<LAYOUT>(pat, side_pos(side, g), side_esc(side, g), n, lane);
 }
 
 // The raw BF16 of a tile that bind marked raw: the format's fallback tiles,

@@ -301,7 +301,7 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
             } else {
                 uint32_t pat[4][8];
                 lookup_tile(lut, t.t, pat);
-                patch_tile_escapes<true>(pat, info, t.side, 0, lane);
+                patch_tile_escapes<kRowLayout>(pat, info, t.side, 0, lane);
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
                     uint32_t wv[8];

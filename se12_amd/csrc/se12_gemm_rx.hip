@@ -1,0 +1,413 @@
+// Batched fused SE12 decode + matrix product for gfx950 with x resident in
+// LDS: Y[b, n] = sum_k W[n, k] X[b, k] for up to 32 BF16 batch rows in one
+// pass over the weights. Same semantics as the reference kernel
+// lws/adapters/cuda/kernels/gemv_se12.cu:50-142 at batch B (one warp per
+// (row, batch) element, W read B times there).
+//
+// For shapes whose x fits a block's LDS (batch x K x 2 bytes): every block
+// first copies all of x into LDS with direct-to-LDS loads (no registers
+// held); then its waves run without a barrier. A block of W waves holds
+// W / KG row slots times KG K groups: slot j of the launch (j = slot * P +
+// block, P blocks) takes tile rows j, j + P W / KG, ... (the rows in flight
+// at a time are adjacent, so the chip reads a moving window of the
+// tile-major streams, and where rows are fewer than slots they spread over
+// all blocks), and K group g of the slot takes the K tiles g, g + KG, ... of
+// each row, in ascending order. A wave keeps its next kRxDepth tiles
+// in flight in a ring of registers, across row boundaries. With one K group
+// a wave stores each row as soon as its last K tile is done; with KG > 1
+// (the host picks it where rows are few, and then no slot holds more than
+// one row) the groups' sums meet once at the end, through LDS, and are added
+// in ascending group order. The launch shape (W, P) fixes KG and so every
+// sum; the raw-BF16 twin (same kernel, RAW) is bit-identical to the fused
+// kernel under one shape.
+//
+// Per tile: each 1 KB of sm (512 B of ec) holding 4 tile rows is read whole
+// by one load instruction (full cache lines in order; a layout with one row
+// per lane measured 2 us slower at 14336 x 3584), then two DPP exchanges
+// between the 4 parts and lane bits 3 and 2 bring the tile into the block
+// layout: lane l holds, in part p, the 16 columns 16 (4 (l / 16) + p) .. +
+// 15 of row l % 16. It is rebuilt through the pair table with listed
+// escapes and raw tiles, and each part's first and second 8 columns are the
+// A operands of two v_mfma_f32_16x16x32_bf16 (MFMA row = tile row l % 16).
+// Their K positions differ between lane groups, and the B operands (lane l:
+// batch row 16 g + l % 16) read the same 8 x columns from the resident x.
+// x rows are stored as 16-byte pieces, piece q of row b at piece index b *
+// (K / 8) + (q ^ (b & 7)): the 16 rows an MFMA reads at one column land in 8
+// distinct 4-bank groups per 8 lanes (no bank conflicts; rows would
+// otherwise be a multiple of 512 bytes apart, all in one bank).
+// Batch rows past the batch in a 16-row group read row 0: MFMA output
+// column n depends on B column n only, and those columns are not stored.
+//
+// FAST only: K % 256 == 0, 16-byte aligned x rows, and for the raw twin
+// N % 16 == 0 and an aligned W (the other cases run se12_gemm.hip).
+#include "se12_device.hpp"
+#include "se12_internal.hpp"
+
+namespace se12 {
+
+typedef __bf16 rx_bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float rx_floatx4_t __attribute__((ext_vector_type(4)));
+
+namespace {
+
+// One tile's loads: sm / ec in the block layout once transposed (below), or
+// raw BF16 column blocks for the twin; the side record of the tile.
+template <bool RAW>
+struct RxTile {
+    TileSide side;
+    TileLoads t;
+    uint4 r[RAW ? 4 : 1][2];
+};
+
+// Part p of a tile's sm (ec) is its contiguous kilobyte (512 bytes) of rows
+// 4p..4p+3, loaded whole by one instruction: lane l takes column block l / 4
+// of row 4p + l % 4. Full cache lines, in order, per load.
+// A wave-uniform pointer in scalar registers: loads from it plus a 32-bit
+// per-lane offset need one VGPR for the address instead of two.
+template <typename T>
+__device__ __forceinline__ const T* rx_uniform(const T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+    return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ void rx_load_chunks(TileLoads& t, TileSide& side, const uint8_t* sm, const uint8_t* ec,
+                                               const uint32_t* sd, int64_t tile, uint32_t lane) {
+    const uint32_t off = (lane & 3u) * kTileCols + 16u * (lane >> 2);
+    const uint8_t* smt = rx_uniform(sm + tile * kTile);
+    const uint8_t* ect = rx_uniform(ec + tile * (kTile / 2));
+    const uint32_t* sdt = rx_uniform(sd + tile * kSideWords);
+    side.rec = sdt[lane & 15u];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        t.sm[p] = *reinterpret_cast<const uint4*>(smt + off + 1024 * p);
+        t.ec[p] = *reinterpret_cast<const uint2*>(ect + off / 2 + 512 * p);
+    }
+}
+
+// Exchanges part bit B with lane bit B + 2 between parts x (bit clear) and
+// y (bit set): lanes with the lane bit set take y from the lane 2^(B+2)
+// below, and the others x from the lane 2^(B+2) above. One DPP row shift
+// each, written only to the lanes that take it: a DPP bank is 4 lanes of a
+// 16-lane row, so lane bits 2 and 3 select banks.
+template <int B>
+__device__ __forceinline__ void rx_swap(uint32_t& x, uint32_t& y) {
+    constexpr int n = 4 << B;
+    constexpr int hi_banks = B == 1 ? 0xC : 0xA;
+    const uint32_t nx = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)y, 0x110 + n, 0xF, hi_banks, false);
+    y = (uint32_t)__builtin_amdgcn_update_dpp((int)y, (int)x, 0x100 + n, 0xF, hi_banks ^ 0xF, false);
+    x = nx;
+}
+
+// the swaps of W word pairs; the scheduler may not gather the copies of all
+// of them up front (each swap keeps one old word until its second move)
+template <int B, int W>
+__device__ __forceinline__ void rx_swap_words(uint32_t (&x)[W], uint32_t (&y)[W]) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) rx_swap<B>(x[i], y[i]);
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Chunk-order loads -> block layout: after the loads lane l holds (row 4p +
+// l % 4, block l / 4) in part p, i.e. row bits 3..2 in the part and row bits
+// 1..0 in lane bits 1..0; exchanging part bit 1 with lane bit 3 and part bit
+// 0 with lane bit 2 leaves lane l with row l % 16 and block 4 (l / 16) + p.
+__device__ __forceinline__ void rx_to_blocks(TileLoads& t) {
+    uint32_t s[4][4], e[4][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        s[p][0] = t.sm[p].x; s[p][1] = t.sm[p].y; s[p][2] = t.sm[p].z; s[p][3] = t.sm[p].w;
+        e[p][0] = t.ec[p].x; e[p][1] = t.ec[p].y;
+    }
+    rx_swap_words<1>(s[0], s[2]);
+    rx_swap_words<1>(s[1], s[3]);
+    rx_swap_words<1>(e[0], e[2]);
+    rx_swap_words<1>(e[1], e[3]);
+    rx_swap_words<0>(s[0], s[1]);
+    rx_swap_words<0>(s[2], s[3]);
+    rx_swap_words<0>(e[0], e[1]);
+    rx_swap_words<0>(e[2], e[3]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        t.sm[p] = make_uint4(s[p][0], s[p][1], s[p][2], s[p][3]);
+        t.ec[p] = make_uint2(e[p][0], e[p][1]);
+    }
+}
+
+// raw BF16 twin: lane l, part p = row l % 16, block 4 (l / 16) + p
+__device__ __forceinline__ void rx_load_raw_blocks(uint4 r[4][2], const uint16_t* wraw, int64_t K, int tr, int kt,
+                                                   uint32_t lane) {
+    const uint16_t* p = wraw + ((int64_t)tr * kTileRows + (lane & 15u)) * K + (int64_t)kt * kTileCols + 64 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        r[j][0] = reinterpret_cast<const uint4*>(p + 16 * j)[0];
+        r[j][1] = reinterpret_cast<const uint4*>(p + 16 * j)[1];
+    }
+}
+
+// a raw tile (fallback or overflow) in the block layout
+__device__ __forceinline__ void rx_raw_part(const int16_t* tile_raw, int p, uint32_t lane, uint32_t w[8]) {
+    const uint4* q = reinterpret_cast<const uint4*>(tile_raw + (lane & 15u) * kTileCols + 64 * (lane >> 4) + 16 * p);
+    const uint4 a = q[0], b = q[1];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+}  // namespace
+
+// byte offset in the resident x of piece q (8 columns) of batch row b
+__device__ __forceinline__ int rx_piece(int b, int q, int pieces_per_row) {
+    return (b * pieces_per_row + (q ^ (b & 7))) * 16;
+}
+
+template <int BG, bool RAW>
+__global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3))) void gemm_rx_kernel(
+    GemvGroupArgs ga, int batch) {
+    SE12_DECLARE_LUT(lut);
+    extern __shared__ __attribute__((aligned(16))) char xs[];
+    const GemvArgs a = ga.m[blockIdx.z];
+    const int threads = blockDim.x;
+    asm volatile("" ::"s"(a.sm), "s"(a.ec), "s"(a.lut), "s"(a.side), "s"(a.wraw), "s"(a.x), "s"(a.y), "s"(a.K),
+                 "s"(a.N), "s"(a.TR), "s"(a.TC), "s"(a.S), "s"(threads), "s"(batch));
+    const int W = threads >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int TC = a.TC;
+    // K groups: the host sets KG (in S) so that it divides W, every wave has
+    // K tiles, and with KG > 1 every row slot holds at most one row
+    const int KG = a.S;
+    const int RW = W / KG;                                     // row slots per block
+    const int kg = w / RW, rw = w - kg * RW;
+    const int nw = (int)gridDim.x * RW;                        // row slots of this matrix
+    const int j0 = rw * (int)gridDim.x + (int)blockIdx.x;      // this slot's first row
+    const int rows = a.TR > j0 ? (a.TR - 1 - j0) / nw + 1 : 0; // rows j0, j0 + nw, ...
+    const int ppr = (int)(a.K >> 3);                           // 16-byte pieces per x row
+    // this group's K tiles: kb, kb + ks, ... below ke
+    const int kb = kg, ks = KG, ke = TC;
+
+    // The wave's tiles in order: its slot's r-th row (j0 + r nw), its K
+    // tiles in ascending order. A cursor (r, kt) walks them and stops past
+    // the wave's last tile, where loads are no longer issued (a wave without
+    // rows loads nothing).
+    struct Cursor {
+        int r, kt;
+    };
+    auto advance = [&](Cursor& c) {
+        if (c.r >= rows) return;
+        c.kt += ks;
+        if (c.kt >= ke) {
+            c.kt = kb;
+            ++c.r;
+        }
+    };
+    auto row_of = [&](const Cursor& c) { return j0 + c.r * nw; };
+    auto load = [&](RxTile<RAW>& t, const Cursor& c) {
+        if (c.r >= rows) return;
+        const int tr = row_of(c), kt = c.kt;
+        if constexpr (RAW) {
+            rx_load_raw_blocks(t.r, a.wraw, a.K, tr, kt, lane);
+        } else {
+            rx_load_chunks(t.t, t.side, a.sm, a.ec, a.side, (int64_t)tr * TC + kt, lane);
+        }
+    };
+
+    // the first kRxDepth tiles, then the pair table and all of x (direct to LDS)
+    RxTile<RAW> ring[kRxDepth]{};
+    Cursor ld{0, kb};
+#pragma unroll
+    for (int d = 0; d < kRxDepth; ++d) {
+        load(ring[d], ld);
+        advance(ld);
+    }
+    uint4 lutv;
+    if constexpr (!RAW) lutv = reinterpret_cast<const uint4*>(a.lut)[lane];
+    {
+        // x in rounds of one piece per thread; block b starts at round
+        // b mod rounds, so that the blocks, which all read the same x from
+        // L2 at the same time, spread over its channels
+        const int total = batch * ppr;                         // pieces of x
+        const int rounds = (total + threads - 1) / threads;
+        const uint16_t* x = static_cast<const uint16_t*>(a.x);
+        int r = (int)(blockIdx.x % (unsigned)rounds);
+        for (int i = 0; i < rounds; ++i) {
+            const int base = r * threads + w * 64;
+            if (base < total) {
+                const int p = min(base + (int)lane, total - 1);  // a lane past the end re-loads the last piece
+                const int b = p / ppr, e = p - b * ppr;
+                const int q = e ^ (b & 7);                       // LDS piece p holds x piece q of row b
+                __builtin_amdgcn_global_load_lds(x + (int64_t)b * a.K + 8 * q, xs + 16 * base, 16, 0, 0);
+            }
+            r = r + 1 == rounds ? 0 : r + 1;
+        }
+    }
+    if constexpr (!RAW) store_block_lut(lut, lutv, lane);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    rx_floatx4_t acc[BG];
+#pragma unroll
+    for (int g = 0; g < BG; ++g) acc[g] = rx_floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    // B-operand row of this lane in each batch group (rows past the batch
+    // read row 0; their outputs are never stored)
+    int xrow[BG];
+#pragma unroll
+    for (int g = 0; g < BG; ++g) {
+        const int b = 16 * g + (int)(lane & 15u);
+        xrow[g] = b < batch ? b : 0;
+    }
+    // y as 16-byte pieces: N % 16 == 0 on this path, so a 16-byte aligned y
+    // keeps every batch row aligned
+    const bool y_vec = (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0u;
+
+    // The row's outputs: lane l holds D[4 (l / 16) + e][l % 16] of each batch
+    // group (tile row 4 (l / 16) + e, batch row 16 g + l % 16). Lane l takes
+    // those of lane 16 (l % 4) + l / 4, i.e. batch row 16 g + l / 4, tile
+    // rows 4 (l % 4) .. + 3, and stores them as one 16-byte piece: each
+    // batch row's 16 outputs are 64 contiguous bytes from 4 lanes.
+    auto store_row = [&](int tr) {
+        const int src = (int)((((lane & 3u) << 4) | (lane >> 2)) << 2);
+#pragma unroll
+        for (int g = 0; g < BG; ++g) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[e] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(acc[g][e])));
+            const int b = 16 * g + (int)(lane >> 2);
+            if (b < batch) {
+                float* yp = a.y + (int64_t)b * a.N + (int64_t)tr * kTileRows + 4 * (int)(lane & 3u);
+                if (y_vec) {
+                    *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) yp[e] = v[e];
+                }
+            }
+        }
+    };
+
+    // part p of a tile in the block layout: lane l holds columns 16 (4 (l /
+    // 16) + p) .. + 15 of row l % 16, as 8 BF16 pairs; its first and second
+    // 8 columns are the A operands of two MFMAs, whose B operands are the x
+    // pieces (8 columns) 2 (4 (l / 16) + p) and the next
+    auto mfma_part = [&](const uint32_t wv[8], int kt, int p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const rx_bf16x8_t av =
+                __builtin_bit_cast(rx_bf16x8_t, make_uint4(wv[4 * h], wv[4 * h + 1], wv[4 * h + 2], wv[4 * h + 3]));
+            const int q = 32 * kt + 8 * (int)(lane >> 4) + 2 * p + h;
+#pragma unroll
+            for (int g = 0; g < BG; ++g) {
+                const uint4 bv = *reinterpret_cast<const uint4*>(xs + rx_piece(xrow[g], q, ppr));
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(rx_bf16x8_t, bv), acc[g], 0, 0, 0);
+            }
+        }
+    };
+    auto use = [&](RxTile<RAW>& t, const Cursor& c) {
+        const int kt = c.kt;
+        if constexpr (RAW) {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const uint32_t wv[8] = {t.r[p][0].x, t.r[p][0].y, t.r[p][0].z, t.r[p][0].w,
+                                        t.r[p][1].x, t.r[p][1].y, t.r[p][1].z, t.r[p][1].w};
+                mfma_part(wv, kt, p);
+            }
+        } else {
+            const uint32_t info = side_info(t.side, 0);
+            if (info_is_fallback(info)) {
+                const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t wv[8];
+                    rx_raw_part(raw, p, lane, wv);
+                    mfma_part(wv, kt, p);
+                }
+            } else {
+                rx_to_blocks(t.t);  // in place: the slot is reloaded next
+                // each part's patterns merged with its sm bytes as soon as
+                // looked up; escapes only set exponent bits, which the merge
+                // takes from the patterns, so they patch the merged words
+                uint32_t wv[4][8];
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t pat[8];
+                    lookup_chunk(lut, t.t.ec[p], pat);
+                    merge_chunk(pat, t.t.sm[p], wv[p]);
+                }
+                patch_tile_escapes<kBlockLayout>(wv, info, t.side, 0, lane);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p);
+            }
+        }
+        // the row's last K tile of this wave: with one K group the row is
+        // done; with more, its single row waits for the combine below
+        if (KG == 1 && kt + ks >= ke) {
+            store_row(row_of(c));
+#pragma unroll
+            for (int g = 0; g < BG; ++g) acc[g] = rx_floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    };
+    // the ring: a step uses one slot, then reloads it with the tile
+    // kRxDepth ahead; the body holds kRxDepth steps so that every slot index
+    // is a constant, and leaves after the wave's last tile
+    Cursor cu{0, kb};
+    if (rows > 0 && kb < ke) {
+        bool more = true;
+        while (more) {
+#pragma unroll
+            for (int d = 0; d < kRxDepth; ++d) {
+                if (more) {
+                    use(ring[d], cu);
+                    // the slot's next loads after its use: hoisted above it,
+                    // they would hold a third tile's registers
+                    __builtin_amdgcn_sched_barrier(0);
+                    load(ring[d], ld);
+                    advance(ld);
+                    advance(cu);
+                    more = cu.r < rows;
+                }
+            }
+        }
+    }
+    if (KG == 1) return;
+    // K groups: every wave is past its last MFMA (x is no longer read), the
+    // groups 1.. of each slot leave their sums in LDS over x, and group 0
+    // adds them in ascending group order and stores the row
+    __syncthreads();
+    const bool has_row = rows > 0 && kb < ke;
+    rx_floatx4_t* part = reinterpret_cast<rx_floatx4_t*>(xs);  // [KG - 1][RW][64 lanes][BG]
+    if (kg > 0) {
+#pragma unroll
+        for (int g = 0; g < BG; ++g)
+            part[(((kg - 1) * RW + rw) * 64 + (int)lane) * BG + g] =
+                has_row ? acc[g] : rx_floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    __syncthreads();
+    if (kg > 0 || rows == 0) return;
+    for (int k = 1; k < KG; ++k)
+#pragma unroll
+        for (int g = 0; g < BG; ++g) acc[g] += part[(((k - 1) * RW + rw) * 64 + (int)lane) * BG + g];
+    store_row(j0);
+}
+
+namespace {
+
+template <int BG, bool RAW>
+hipError_t rx_go(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
+    const dim3 grid(p.blocks / a.count, 1, a.count), block(p.waves * 64);
+    hipLaunchKernelGGL((gemm_rx_kernel<BG, RAW>), grid, block, p.lds, stream, a, batch);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm_rx(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
+    if (batch < 1 || batch > 32 || p.waves < 1 || p.waves * 64 > kRxMaxThreads || p.blocks % a.count != 0)
+        return hipErrorInvalidValue;
+    for (int i = 0; i < a.count; ++i)
+        if (a.m[i].S < 1 || p.waves % a.m[i].S != 0) return hipErrorInvalidValue;
+    if (batch > 16) return p.raw ? rx_go<2, true>(a, batch, p, stream) : rx_go<2, false>(a, batch, p, stream);
+    return p.raw ? rx_go<1, true>(a, batch, p, stream) : rx_go<1, false>(a, batch, p, stream);
+}
+
+}  // namespace se12

@@ -222,6 +222,35 @@ constexpr int kGemmXPieces = 4;
 constexpr int gemm_min_waves(int batch) { return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces); }
 size_t gemm_lds_bytes(int waves, int batch);
 hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
+
+// Resident-x batched path (se12_gemm_rx.hip): BF16 x with up to 32 rows on
+// FAST shapes whose x (batch x K BF16, in whole 64-piece loads of 16 bytes)
+// fits a block's LDS beside the pair table (se12_abi.hip's rx_fits). Blocks
+// of 1..12 waves, any block count per matrix (blocks = that count x
+// matrices); each row's K groups (GemvArgs::S holds them on this path) are
+// fixed by the launch shape
+// (rx_kgroups). kRxDepth tiles in flight per wave, up to 3 waves per SIMD
+// (168 VGPRs: the decode, a tile in flight and the transposed tile in use).
+constexpr int kRxMaxThreads = 768;
+constexpr int kRxDepth = 2;
+// K groups of the resident-x kernel for one matrix: the largest power of two
+// that divides the waves per block, leaves each group at least two K tiles,
+// and keeps every row slot (blocks x waves / KG of them) to at most one row.
+constexpr int rx_kgroups(int64_t tile_rows, int32_t tile_cols, int32_t waves, int64_t blocks) {
+    int kg = 1;
+    while (waves % (2 * kg) == 0 && tile_cols >= 4 * kg && blocks * (waves / (2 * kg)) >= tile_rows) kg *= 2;
+    return kg;
+}
+constexpr size_t rx_lds_bytes(int64_t k, int batch) {
+    return (size_t)(((int64_t)batch * (k / 8) + 63) / 64 * 64) * 16;
+}
+// dynamic LDS: x, or (the same memory, after the main loop) the K groups'
+// sums, whichever is larger
+constexpr size_t rx_lds_total(int64_t k, int batch, int waves, int kgroups) {
+    const size_t sums = kgroups > 1 ? (size_t)(waves - waves / kgroups) * (batch > 16 ? 2 : 1) * 1024 : 0;
+    return rx_lds_bytes(k, batch) > sums ? rx_lds_bytes(k, batch) : sums;
+}
+hipError_t launch_gemm_rx(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream);
 // Bind-time sidecar: one word per tile (fallback rank, or the chunks holding
 // escape codes) and the fallback tile count.

@@ -30,6 +30,18 @@ MFMA_MIN_BATCH = 5
 MFMA_MAX_K_SPLITS = 16
 MFMA_MAX_WAVES = 8
 MFMA_MAX_WAVES_GENERIC = 4   # the edge-handling MFMA variants (K % 256 != 0 or unaligned x)
+# The resident-x MFMA kernel: BF16 batches of RX_MIN_BATCH rows or more (or
+# MFMA_MIN_BATCH or more on matrices of RX_MIN_TILES tiles or more) on FAST
+# shapes whose x (batch x K BF16, in whole 1 KiB loads) fits a block's LDS
+# (gfx950: 160 KiB) beside the 1 KiB pair table. Its launch is (waves per
+# block 1..12, blocks per matrix 1..tile rows); the launch fixes the K groups
+# (rx_kgroups) and with them the order of every sum.
+RX_MAX_WAVES = 12
+RX_MIN_BATCH = 9
+RX_MIN_TILES = 14336
+LDS_PER_BLOCK = 160 * 1024
+LUT_BYTES = 1024
+RX_BLOCK_CANDIDATES = (32, 64, 128, 192, 256, 384, 512, 768, 1024)
 
 
 @dataclasses.dataclass(frozen=True)
@@ -68,6 +80,34 @@ def uses_mfma(batch: int, float32_activations: bool = False) -> bool:
 
 def mfma_min_waves(batch: int) -> int:
     return -(-batch // 8)
+
+
+def rx_lds_bytes(k: int, batch: int) -> int:
+    """LDS of the resident x: batch x K BF16 in whole 64-piece loads of 16 bytes."""
+    return -(-(batch * (k // 8)) // 64) * 64 * 16
+
+
+def uses_rx(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True) -> bool:
+    """Whether a launch runs the resident-x MFMA kernel (the library's rule)."""
+    return (uses_mfma(batch, float32_activations) and aligned_x
+            and not runs_generic(output_rows, k, float32_activations)
+            and (batch >= RX_MIN_BATCH or tile_rows(output_rows) * k_tiles(k) >= RX_MIN_TILES)
+            and rx_lds_bytes(k, batch) + LUT_BYTES <= LDS_PER_BLOCK)
+
+
+def rx_kgroups(output_rows: int, k: int, waves: int, blocks_per_matrix: int) -> int:
+    """K groups of a resident-x launch (the library's rule): the largest power
+    of two that divides the waves per block, leaves every group at least two
+    K tiles and keeps each row slot (blocks x waves / groups) to one row."""
+    tr, tc, kg = tile_rows(output_rows), k_tiles(k), 1
+    while waves % (2 * kg) == 0 and tc >= 4 * kg and blocks_per_matrix * (waves // (2 * kg)) >= tr:
+        kg *= 2
+    return kg
+
+
+def rx_configuration(waves: int, blocks_per_matrix: int, matrices: int = 1) -> LaunchConfiguration:
+    return LaunchConfiguration(threads_per_block=ThreadsPerBlock(waves * WAVE_SIZE),
+                               blocks=BlockCount(blocks_per_matrix * matrices))
 
 
 def grid_rows(output_rows: int, waves: int, batch: int = 1, float32_activations: bool = False) -> int:
@@ -111,9 +151,17 @@ def max_waves_per_block(batch: int, float32_activations: bool = False, generic: 
 
 def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int = 1, k: int | None = None,
                      float32_activations: bool = False) -> tuple[int, int]:
-    """(waves per block, K splits) of a configuration for a matrix with `output_rows` rows."""
+    """(waves per block, K splits) of a configuration for a matrix with
+    `output_rows` rows; for the resident-x kernel (K given), (waves per
+    block, blocks), which never split K."""
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
+    if k is not None and uses_rx(output_rows, k, batch, float32_activations):
+        if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= WAVE_SIZE * RX_MAX_WAVES:
+            raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {WAVE_SIZE * RX_MAX_WAVES}]")
+        if not 1 <= blocks <= tile_rows(output_rows):
+            raise ValueError(f"blocks {blocks} must be in [1, {tile_rows(output_rows)}]")
+        return tpb // WAVE_SIZE, blocks
     generic = runs_generic(output_rows, k, float32_activations) if k is not None else float32_activations
     hi = WAVE_SIZE * max_waves_per_block(batch, float32_activations, generic)
     lo = WAVE_SIZE * (mfma_min_waves(batch) if uses_mfma(batch, float32_activations) else 1)
@@ -144,6 +192,9 @@ def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 
         raise ValueError(f"threads_per_block {tpb} must be a multiple of 32 in [32, 1024]")
     if blocks <= 0 or blocks * (tpb // 32) < output_rows * batch:
         raise ValueError(f"{blocks} blocks of {tpb // 32} warps do not cover {output_rows} rows x batch {batch}")
+    if uses_rx(output_rows, k, batch, float32_activations, aligned_x):
+        waves = min(-(-tpb // WAVE_SIZE), RX_MAX_WAVES)
+        return rx_configuration(waves, -(-tile_rows(output_rows) // waves))
     mfma = uses_mfma(batch, float32_activations)
     generic = runs_generic(output_rows, k, float32_activations) or not aligned_x
     hi = max_waves_per_block(batch, float32_activations, generic)
@@ -161,6 +212,13 @@ def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_a
     the K tiles; for the dot2 kernel never more waves than tiles per split
     (search_space.py:17-19 enumerates threads per block the same way)."""
     tc = k_tiles(k)
+    if uses_rx(output_rows, k, batch, float32_activations):
+        tr = tile_rows(output_rows)
+        out = []
+        for waves in (1, 2, 3, 4, 6, 8, 12):
+            for p in sorted({b for b in RX_BLOCK_CANDIDATES if b <= tr} | {-(-tr // waves)}):
+                out.append(rx_configuration(waves, p))
+        return tuple(out)
     mfma = uses_mfma(batch, float32_activations)
     mw = max_waves_per_block(batch, float32_activations, runs_generic(output_rows, k, float32_activations))
     lo = mfma_min_waves(batch) if mfma else 1

@@ -269,7 +269,8 @@ def test_grouped_launch_equals_separate_launches(gpu):
     launches under the same waves per block and K splits, and within the
     tolerance of the oracle under the default launch."""
     from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped
-    from se12_amd.launch import BlockCount, LaunchConfiguration, ThreadsPerBlock, configuration, grid_rows
+    from se12_amd.launch import (BlockCount, LaunchConfiguration, ThreadsPerBlock, configuration, grid_rows,
+                                 rx_configuration, rx_kgroups, uses_rx)
 
     cols = 2304
     shapes = [(272, cols), (128, cols), (48, cols)]
@@ -284,6 +285,29 @@ def test_grouped_launch_equals_separate_launches(gpu):
         for y, e in zip(ys, encs):
             ref = o.gemv_reference(e, o.bf16_bits_to_f32(xb))
             assert max_rel_error(y, ref) <= REL_TOL
+        if uses_rx(272, cols, batch):
+            # the resident-x kernel: (waves, blocks per matrix), which fix each
+            # matrix's K groups; the same groups give the same sums, grouped or
+            # single, whichever blocks hold the rows
+            for waves, per in ((3, 1), (8, 17), (4, 5), (1, 3), (12, 3), (12, 17), (8, 1)):
+                ys = multiply_grouped(kerns, x, launch=rx_configuration(waves, per, len(shapes)))
+                ysr = multiply_grouped(raws, x, launch=rx_configuration(waves, per, len(shapes)))
+                for k, r, y, yr, (rows, _), e in zip(kerns, raws, ys, ysr, shapes, encs):
+                    tr = -(-rows // 16)
+                    kg = rx_kgroups(rows, cols, waves, per)
+                    assert kg == rx_kgroups(rows, cols, waves, min(per, tr))
+                    assert torch.equal(y, k.multiply(x, launch=rx_configuration(waves, min(per, tr)))), (batch, waves, per)
+                    assert torch.equal(yr, y), (batch, waves, per)
+                    ref = o.gemv_reference(e, o.bf16_bits_to_f32(xb))
+                    assert max_rel_error(y, ref) <= REL_TOL, (batch, waves, per, kg)
+                    # another block count with the same K groups: the rows move
+                    # to other blocks, the sums stay
+                    for other in range(1, tr + 1):
+                        if other != min(per, tr) and rx_kgroups(rows, cols, waves, other) == kg:
+                            assert torch.equal(y, k.multiply(x, launch=rx_configuration(waves, other))), \
+                                (batch, waves, per, other)
+                            break
+            continue
         for waves, splits in ((3, 1), (9, 1), (4, 3), (6, 2)):
             if batch >= 4 and waves > 8:
                 continue

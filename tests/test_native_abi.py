@@ -117,11 +117,43 @@ def test_launch_candidates_respect_each_kernels_limits():
     assert all(waves_and_splits(c, 2304, batch=24, k=9216)[0] % 3 == 0 for c in candidate_configurations(2304, 9216, batch=24))
     assert min(waves_and_splits(c, 2304, batch=32, k=9216)[0] for c in candidate_configurations(2304, 9216, batch=32)) == 4
     assert max_waves_per_block(1) == 16 and max_waves_per_block(6) == 8
-    for batch, f32, max_s in ((1, False, 36), (6, False, 16), (32, False, 16), (6, True, 36)):
+    for batch, f32, max_s in ((1, False, 36), (32, False, 16), (6, True, 36)):
         cfgs = candidate_configurations(2304, 9216, batch=batch, float32_activations=f32)
         pairs = [waves_and_splits(c, 2304, batch=batch, k=9216, float32_activations=f32) for c in cfgs]
         assert max(s for _, s in pairs) == max_s
         assert max(w for w, _ in pairs) == max_waves_per_block(batch, f32)
+    # 9 or more BF16 rows of x that fit a block's LDS (9 x 2304: 41 KiB), or
+    # 5..8 rows over 14336 tiles or more: the resident-x kernel, (waves
+    # 1..12, blocks 1..tile rows); 9 rows at K = 9216 (162 KiB) do not fit
+    from se12_amd.launch import rx_lds_bytes, uses_rx
+
+    assert uses_rx(2304, 2304, 9) and not uses_rx(2304, 9216, 9) and not uses_rx(2304, 2304, 9, float32_activations=True)
+    assert not uses_rx(2304, 9216, 6) and uses_rx(4096, 14336, 5) and uses_rx(256000, 2304, 5)
+    assert not uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and not uses_rx(14336, 3584, 24)
+    assert not uses_rx(2304, 2300, 9) and not uses_rx(2300, 2304, 9) and not uses_rx(256000, 2304, 4)
+    assert rx_lds_bytes(9216, 6) == 6 * 1152 * 16 and rx_lds_bytes(2304, 5) == 1472 * 16
+    pairs = [waves_and_splits(c, 2304, batch=9, k=2304) for c in candidate_configurations(2304, 2304, batch=9)]
+    assert max(w for w, _ in pairs) == 12 and max(b for _, b in pairs) == 144 and min(b for _, b in pairs) >= 1
+
+
+def test_resident_x_kgroups_rule():
+    """K groups of the resident-x kernel: powers of two dividing the waves,
+    at least two K tiles per group, at most one row per row slot."""
+    from se12_amd.launch import rx_kgroups
+
+    assert rx_kgroups(2304, 9216, 8, 144) == 8         # 144 tile rows, 36 K tiles: one row per block
+    assert rx_kgroups(2304, 9216, 8, 72) == 4
+    assert rx_kgroups(14336, 3584, 8, 256) == 2        # 896 rows over 256 blocks x 4 slots; 14 K tiles
+    assert rx_kgroups(14336, 3584, 8, 512) == 4
+    assert rx_kgroups(9216, 2304, 8, 256) == 2
+    assert rx_kgroups(9216, 2304, 8, 576) == 4         # 9 K tiles: groups of 2..3 tiles
+    assert rx_kgroups(256000, 2304, 8, 256) == 1       # rows far beyond the slots
+    assert rx_kgroups(2304, 9216, 12, 144) == 4        # 12 waves: 4 divides, 8 does not
+    assert rx_kgroups(2304, 9216, 3, 144) == 1
+    for rows, k, w, p in ((2304, 9216, 12, 144), (14336, 3584, 8, 512), (9216, 2304, 8, 576), (272, 2304, 8, 17)):
+        kg = rx_kgroups(rows, k, w, p)
+        assert w % kg == 0 and -(-k // 256) >= 2 * kg
+        assert kg == 1 or p * (w // kg) >= -(-rows // 16)
 
 
 def test_step_kernels_reject_invalid_arguments():

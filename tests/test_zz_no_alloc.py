@@ -38,17 +38,21 @@ def _both(kern, x, launch):
 
 def test_noalloc_equals_the_allocating_product_twice_in_a_row(gpu):
     from se12_amd.hip import Se12MatVecKernel
-    from se12_amd.launch import configuration
+    from se12_amd.launch import configuration, rx_configuration, uses_rx
 
+    assert not uses_rx(4608, 9216, 16) and not uses_rx(1040, 9216, 9) and uses_rx(1040, 2304, 9)
     big_bits, big_enc = normal_case(4608, 9216, seed=41)
     small_bits, small_enc = normal_case(1040, 2304, seed=42)
+    long_bits, long_enc = normal_case(1040, 9216, seed=43)
     big = Se12MatVecKernel(to_device(big_enc, gpu))
     small = Se12MatVecKernel(to_device(small_enc, gpu))
+    long = Se12MatVecKernel(to_device(long_enc, gpu))
     cases = [
         (big, big_enc, 4, configuration(4, 9, 4608, 4)),       # dot2, 9 K splits over 4 batch rows
         (small, small_enc, 2, configuration(3, 3, 1040, 2)),   # a smaller input after it
-        (big, big_enc, 16, configuration(4, 3, 4608, 16)),     # MFMA, 3 K splits
-        (small, small_enc, 9, configuration(2, 3, 1040, 9)),   # smaller again, MFMA
+        (big, big_enc, 16, configuration(4, 3, 4608, 16)),     # MFMA (x over a block's LDS), 3 K splits
+        (long, long_enc, 9, configuration(2, 3, 1040, 9)),     # smaller again, MFMA, 3 K splits
+        (small, small_enc, 9, rx_configuration(4, 7)),         # resident-x kernel (no split-K scratch)
         (small, small_enc, 1, None),                            # the default launch
         (big, big_enc, 1, None),
     ]

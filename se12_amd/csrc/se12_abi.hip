@@ -347,8 +347,11 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         waves = std::min<int64_t>(3, tc);
     } else if (tiles <= 64 * cus) {
         // 2 rows and more per launch: 2 waves (14336x3584, B = 2..4: 17.8 us
-        // against 19.5 with tc / 2 = 7 waves, 19.8 against 26.9 at B = 4)
-        waves = bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, std::max<int64_t>(2, tc / 2)));
+        // against 19.5 with tc / 2 = 7 waves, 19.8 against 26.9 at B = 4);
+        // one row: about half the K tiles, rounded up to an even count
+        // (14336x3584: 8 waves 16.2 us, 7 waves 16.8)
+        const int64_t half = std::max<int64_t>(2, tc / 2);
+        waves = bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, half + (half & 1)));
     } else {
         // 2..4 rows per launch hold more registers per lane: 3 waves
         // (256000x2304 at B = 4: 154 us against 209 with 6 waves)

@@ -62,79 +62,6 @@ struct RxTile {
 // Part p of a tile's sm (ec) is its contiguous kilobyte (512 bytes) of rows
 // 4p..4p+3, loaded whole by one instruction: lane l takes column block l / 4
 // of row 4p + l % 4. Full cache lines, in order, per load.
-// A wave-uniform pointer in scalar registers: loads from it plus a 32-bit
-// per-lane offset need one VGPR for the address instead of two.
-template <typename T>
-__device__ __forceinline__ const T* rx_uniform(const T* p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-    return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
-}
-
-__device__ __forceinline__ void rx_load_chunks(TileLoads& t, TileSide& side, const uint8_t* sm, const uint8_t* ec,
-                                               const uint32_t* sd, int64_t tile, uint32_t lane) {
-    const uint32_t off = (lane & 3u) * kTileCols + 16u * (lane >> 2);
-    const uint8_t* smt = rx_uniform(sm + tile * kTile);
-    const uint8_t* ect = rx_uniform(ec + tile * (kTile / 2));
-    const uint32_t* sdt = rx_uniform(sd + tile * kSideWords);
-    side.rec = sdt[lane & 15u];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        t.sm[p] = *reinterpret_cast<const uint4*>(smt + off + 1024 * p);
-        t.ec[p] = *reinterpret_cast<const uint2*>(ect + off / 2 + 512 * p);
-    }
-}
-
-// Exchanges part bit B with lane bit B + 2 between parts x (bit clear) and
-// y (bit set): lanes with the lane bit set take y from the lane 2^(B+2)
-// below, and the others x from the lane 2^(B+2) above. One DPP row shift
-// each, written only to the lanes that take it: a DPP bank is 4 lanes of a
-// 16-lane row, so lane bits 2 and 3 select banks.
-template <int B>
-__device__ __forceinline__ void rx_swap(uint32_t& x, uint32_t& y) {
-    constexpr int n = 4 << B;
-    constexpr int hi_banks = B == 1 ? 0xC : 0xA;
-    const uint32_t nx = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)y, 0x110 + n, 0xF, hi_banks, false);
-    y = (uint32_t)__builtin_amdgcn_update_dpp((int)y, (int)x, 0x100 + n, 0xF, hi_banks ^ 0xF, false);
-    x = nx;
-}
-
-// the swaps of W word pairs; the scheduler may not gather the copies of all
-// of them up front (each swap keeps one old word until its second move)
-template <int B, int W>
-__device__ __forceinline__ void rx_swap_words(uint32_t (&x)[W], uint32_t (&y)[W]) {
-#pragma unroll
-    for (int i = 0; i < W; ++i) rx_swap<B>(x[i], y[i]);
-    __builtin_amdgcn_sched_barrier(0);
-}
-
-// Chunk-order loads -> block layout: after the loads lane l holds (row 4p +
-// l % 4, block l / 4) in part p, i.e. row bits 3..2 in the part and row bits
-// 1..0 in lane bits 1..0; exchanging part bit 1 with lane bit 3 and part bit
-// 0 with lane bit 2 leaves lane l with row l % 16 and block 4 (l / 16) + p.
-__device__ __forceinline__ void rx_to_blocks(TileLoads& t) {
-    uint32_t s[4][4], e[4][2];
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        s[p][0] = t.sm[p].x; s[p][1] = t.sm[p].y; s[p][2] = t.sm[p].z; s[p][3] = t.sm[p].w;
-        e[p][0] = t.ec[p].x; e[p][1] = t.ec[p].y;
-    }
-    rx_swap_words<1>(s[0], s[2]);
-    rx_swap_words<1>(s[1], s[3]);
-    rx_swap_words<1>(e[0], e[2]);
-    rx_swap_words<1>(e[1], e[3]);
-    rx_swap_words<0>(s[0], s[1]);
-    rx_swap_words<0>(s[2], s[3]);
-    rx_swap_words<0>(e[0], e[1]);
-    rx_swap_words<0>(e[2], e[3]);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        t.sm[p] = make_uint4(s[p][0], s[p][1], s[p][2], s[p][3]);
-        t.ec[p] = make_uint2(e[p][0], e[p][1]);
-    }
-}
-
 // raw BF16 twin: lane l, part p = row l % 16, block 4 (l / 16) + p
 __device__ __forceinline__ void rx_load_raw_blocks(uint4 r[4][2], const uint16_t* wraw, int64_t K, int tr, int kt,
                                                    uint32_t lane) {
@@ -208,7 +135,7 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
         if constexpr (RAW) {
             rx_load_raw_blocks(t.r, a.wraw, a.K, tr, kt, lane);
         } else {
-            rx_load_chunks(t.t, t.side, a.sm, a.ec, a.side, (int64_t)tr * TC + kt, lane);
+            load_tile_block_order(t.t, t.side, a.sm, a.ec, a.side, (int64_t)tr * TC + kt, lane);
         }
     };
 
@@ -323,7 +250,7 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
                     mfma_part(wv, kt, p);
                 }
             } else {
-                rx_to_blocks(t.t);  // in place: the slot is reloaded next
+                chunks_to_blocks(t.t);  // in place: the slot is reloaded next
                 // each part's patterns merged with its sm bytes as soon as
                 // looked up; escapes only set exponent bits, which the merge
                 // takes from the patterns, so they patch the merged words

@@ -122,23 +122,31 @@ def test_lm_head_heavy_tailed_full_size(gpu):
     w = heavy_tailed_bf16_device(rows, cols, seed=256, device=gpu)
     dt = encode_on_device(w)
     assert torch.equal(HipSe12WeightDecoder().decode_to_device(dt), w)
-    xb = o.normal_bf16(1, cols, seed=257, std=1.0)
-    x = bf16_tensor(xb, gpu)
     fused = Se12MatVecKernel(dt)
-    y = fused.multiply(x)
-    yr = RawBf16MatVecKernel(w).multiply(x)
-    torch.cuda.synchronize()
-    assert torch.equal(y, yr)
+    raw = RawBf16MatVecKernel(w)
     tr = dt.tile_grid[0]
+    slices = [_tile_row_slice(dt, tr0, tr0 + 8) for tr0 in (0, tr // 2, tr - 8)]
     escapes = 0
-    for tr0 in (0, tr // 2, tr - 8):
-        enc = _tile_row_slice(dt, tr0, tr0 + 8)
+    for tr0, enc in zip((0, tr // 2, tr - 8), slices):
         r0, r1 = tr0 * 16, tr0 * 16 + enc["shape"][0]
         assert np.array_equal(o.decode(enc), w[r0:r1].view(torch.int16).cpu().numpy())
-        ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
-        assert max_rel_error(y[:, r0:r1], ref) <= REL_TOL
         escapes += int((o.unpack_codes(enc["ec"]) == o.ESCAPE_CODE).sum())
     assert escapes > 0   # the slices exercise the escape path
+    # batch 1 (dot2 kernel), 8, 16 and 32 (the resident-x MFMA kernel: 144,000 tiles)
+    from se12_amd.launch import uses_rx
+
+    assert all(uses_rx(rows, cols, b) for b in (8, 16, 32))
+    for batch in (1, 8, 16, 32):
+        xb = o.normal_bf16(batch, cols, seed=257 + batch, std=1.0)
+        x = bf16_tensor(xb, gpu)
+        y = fused.multiply(x)
+        yr = raw.multiply(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y, yr), batch
+        for tr0, enc in zip((0, tr // 2, tr - 8), slices):
+            r0, r1 = tr0 * 16, tr0 * 16 + enc["shape"][0]
+            ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+            assert max_rel_error(y[:, r0:r1], ref) <= REL_TOL, (batch, tr0)
 
 
 def test_gemma2_2b_full_decode_se12_equals_raw_twin(gpu):

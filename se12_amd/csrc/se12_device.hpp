@@ -341,27 +341,37 @@ __device__ __forceinline__ void load_raw_chunk(const int16_t* tile_raw, int j, u
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
 }
 
-// A wave-uniform pointer in scalar registers: loads from it plus a 32-bit
-// per-lane offset need one VGPR for the address instead of two.
+// A wave-uniform global pointer in scalar registers: loads from it plus a
+// 32-bit per-lane offset need one VGPR for the address instead of two. The
+// result is typed as global memory: a pointer rebuilt from integers would
+// otherwise be a flat one, whose loads also count as LDS operations (a wait
+// for the pair-table lookups would then wait for the tile loads in flight).
 template <typename T>
-__device__ __forceinline__ const T* wave_uniform(const T* p) {
+using global_ptr = const __attribute__((address_space(1))) T*;
+
+template <typename T>
+__device__ __forceinline__ global_ptr<T> wave_uniform(const T* p) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
-    return reinterpret_cast<const T*>(((uint64_t)hi << 32) | lo);
+    return reinterpret_cast<global_ptr<T>>(((uint64_t)hi << 32) | lo);
 }
 
 __device__ __forceinline__ void load_tile_block_order(TileLoads& t, TileSide& side, const uint8_t* sm, const uint8_t* ec,
                                                const uint32_t* sd, int64_t tile, uint32_t lane) {
     const uint32_t off = (lane & 3u) * kTileCols + 16u * (lane >> 2);
-    const uint8_t* smt = wave_uniform(sm + tile * kTile);
-    const uint8_t* ect = wave_uniform(ec + tile * (kTile / 2));
-    const uint32_t* sdt = wave_uniform(sd + tile * kSideWords);
+    const global_ptr<uint8_t> smt = wave_uniform(sm + tile * kTile);
+    const global_ptr<uint8_t> ect = wave_uniform(ec + tile * (kTile / 2));
+    const global_ptr<uint32_t> sdt = wave_uniform(sd + tile * kSideWords);
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     side.rec = sdt[lane & 15u];
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
-        t.sm[p] = *reinterpret_cast<const uint4*>(smt + off + 1024 * p);
-        t.ec[p] = *reinterpret_cast<const uint2*>(ect + off / 2 + 512 * p);
+        const u32x4 s4 = *reinterpret_cast<global_ptr<u32x4>>(smt + off + 1024 * p);
+        const u32x2 e2 = *reinterpret_cast<global_ptr<u32x2>>(ect + off / 2 + 512 * p);
+        t.sm[p] = make_uint4(s4[0], s4[1], s4[2], s4[3]);
+        t.ec[p] = make_uint2(e2[0], e2[1]);
     }
 }
 

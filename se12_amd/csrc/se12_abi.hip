@@ -339,8 +339,13 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         waves = tc <= 16 ? tc : 8;
         if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
     } else if (tc > 32) {
-        waves = 8;
+        // long rows on many tile rows (4608x36864): one wave per block and
+        // splits of ~36 K tiles (B = 1: 48.2 us against 49.8 with 8 waves),
+        // half again as many from 3 rows per launch (B = 2: 48.5 against
+        // 58.3; B = 4: 51.3 against 65.9)
+        waves = 1;
         splits = std::max<int64_t>(1, (tc + 18) / 36);
+        if (bl >= 3) splits = splits * 3 / 2;
     } else if (tiles <= 10 * cus) {
         waves = std::min<int64_t>(16, tc);
     } else if (tiles <= 32 * cus) {
@@ -353,9 +358,15 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         const int64_t half = std::max<int64_t>(2, tc / 2);
         waves = bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, half + (half & 1)));
     } else {
-        // 2..4 rows per launch hold more registers per lane: 3 waves
-        // (256000x2304 at B = 4: 154 us against 209 with 6 waves)
-        waves = std::min<int64_t>(bl >= 2 ? 3 : 6, tc);
+        // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1
+        // and 3 at B = 2..4 (B = 4: 154 us against 209 with 6); rows over
+        // 12 K tiles (36864x4608) 4 waves at B = 1..2 (45.0 / 45.4 us against
+        // 46.2 / 47.1) and 8 at B = 3..4 (49.7 against 52.9)
+        if (tc <= 12)
+            waves = bl >= 2 ? 3 : 6;
+        else
+            waves = bl >= 3 ? 8 : 4;
+        waves = std::min<int64_t>(waves, tc);
     }
     waves = std::max<int64_t>(1, std::min(waves, mw));
     *waves_out = (int32_t)waves;

@@ -336,7 +336,9 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     const int64_t tiles = tr * tc;
     int64_t waves, splits = 1;
     if (tr < cus) {
-        waves = tc <= 16 ? tc : 8;
+        // one wave per K tile up to 9 (Gemma-2 2B), else 8 (2048x3584: 5.4 us
+        // against 14 waves' slower launch; 3584x4096: 6.3 against 7.4 with 16)
+        waves = tc <= 9 ? tc : 8;
         if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
     } else if (tc > 32) {
         // long rows on many tile rows (4608x36864): one wave per block and
@@ -349,7 +351,11 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     } else if (tiles <= 10 * cus) {
         waves = std::min<int64_t>(16, tc);
     } else if (tiles <= 32 * cus) {
-        waves = std::min<int64_t>(3, tc);
+        // 3 waves for 9 K tiles (9216x2304); longer rows 8 waves at 1..2 rows
+        // per launch (4096x3584: 6.3 us against 7.2 with 3; 4096x4608: 7.3
+        // against 8.3) and 4 at 3..4 (7.95 / 9.0 against 8.2 / 9.2)
+        waves = tc <= 9 ? 3 : (bl >= 3 ? 4 : 8);
+        waves = std::min<int64_t>(waves, tc);
     } else if (tiles <= 64 * cus) {
         // 2 rows and more per launch: 2 waves (14336x3584, B = 2..4: 17.8 us
         // against 19.5 with tc / 2 = 7 waves, 19.8 against 26.9 at B = 4);

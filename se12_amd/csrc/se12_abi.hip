@@ -352,9 +352,11 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         waves = std::min<int64_t>(16, tc);
     } else if (tiles <= 32 * cus) {
         // 3 waves for 9 K tiles (9216x2304); longer rows 8 waves at 1..2 rows
-        // per launch (4096x3584: 6.3 us against 7.2 with 3; 4096x4608: 7.3
-        // against 8.3) and 4 at 3..4 (7.95 / 9.0 against 8.2 / 9.2)
-        waves = tc <= 9 ? 3 : (bl >= 3 ? 4 : 8);
+        // per launch when the tile rows fill the CUs once (4096x3584: 6.3 us
+        // against 7.2 with 3; 4096x4608: 7.3 against 8.3), 4 where some CUs
+        // take two blocks (4608x4096: 8.6 against 9.0 with 8) and at 3..4
+        // rows (7.95 / 9.0 against 8.2 / 9.2)
+        waves = tc <= 9 ? 3 : (bl >= 3 || tr > cus ? 4 : 8);
         waves = std::min<int64_t>(waves, tc);
     } else if (tiles <= 64 * cus) {
         // 2 rows and more per launch: 2 waves (14336x3584, B = 2..4: 17.8 us

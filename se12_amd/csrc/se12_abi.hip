@@ -388,14 +388,20 @@ static int64_t gemm_row_blocks(se12_handle* const* hs, int32_t count, int32_t ro
     return rb;
 }
 
-// Default launch of the MFMA kernel, fitted to sweeps of (K groups, K splits)
-// on MI355X over the Gemma-2 2B/9B shapes at B = 5..32: rows per block fixed
-// by the batch (the fewest waves whose threads load an x slab, batch / 8
-// rounded up); then about 3.4 waves per CU in all (tile rows x K groups x
-// splits: 864 on 256 CUs), K groups first (up to 6 with one row per block,
-// 2 with more; at least 2 K tiles per wave), splits for the rest (at least 3
-// K tiles per wave). 14336x3584: 1 x 1; 2304x9216: 6 x 1 at B <= 8, 2 x 3 at
-// B = 9..24; 4096x2304: 3 x 1 at B <= 8.
+// Default launch of the x-slab MFMA kernel: rows per block fixed by the
+// batch (R = the fewest waves whose threads load an x slab, batch / 8
+// rounded up, 4 in place of 3); then m waves of K parallelism per tile row, m = 1 on
+// matrices of 2 or more tile rows per CU, else about 3.4 waves per CU in
+// all (864 on 256 CUs) and at least one per 24 K tiles; split between K
+// groups (up to 6 with one row per block, 2 with more, 2+ K tiles per wave)
+// and K splits (3+ K tiles per wave, at most 16) so that the blocks spread
+// most evenly over the CUs (the fewest blocks on the busiest CU relative to
+// the mean), then closest to m, then more K groups. Sweeps on MI355X:
+// 4608x36864 B = 8/16/32 (1, 6) 64.2 / (4, 3) 70.9 / (8, 3) 74.9 us against
+// 88.0 / 95.3 / 99.5 for the previous rule (K groups first), 3584x14336
+// B = 32 (4, 4) 34.4 against 46.2, 4096x3584 B = 32 (4, 3) 19.7 against
+// 21.8, 4608x4096 B = 8 (1, 3) 14.8 against 16.2, 9216x2304 B = 8 (1, 1)
+// 13.2 against 14.1; 2304x9216 B = 8 (2, 3) 17.1 against 16.8.
 static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, bool generic, int32_t* waves_out,
                                 int32_t* splits_out) {
     const se12_handle* h0 = hs[0];
@@ -403,15 +409,30 @@ static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t b
     for (int32_t i = 0; i < count; ++i) tr += hs[i]->TR;
     const int64_t cus = std::max<int32_t>(1, h0->cu_count);
     const int64_t rows = gemm_min_waves(batch);
+    const int64_t row_blocks = gemm_row_blocks(hs, count, (int32_t)rows);
     const int64_t target = 27 * cus / 8;
-    const int64_t m = std::max<int64_t>(1, (2 * target + tr) / (2 * tr));  // K groups x splits
+    const int64_t m =
+        tr >= 2 * cus ? 1 : std::max<int64_t>({1, (2 * target + tr) / (2 * tr), ceil_div(h0->TC, 24)});
     const int64_t max_waves = (generic ? kGemmMaxThreadsGeneric : kGemmMaxThreads) / 64;
     const int64_t kg_max = std::max<int64_t>(1, std::min<int64_t>({max_waves / rows, rows == 1 ? 6 : 2, h0->TC / 2}));
-    const int64_t kg = std::min(m, kg_max);
-    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kGemmMaxSplits, (int64_t)h0->s_cap,
-                                                               h0->TC / (3 * kg)}));
-    *waves_out = (int32_t)(rows * kg);
-    *splits_out = (int32_t)std::max<int64_t>(1, std::min<int64_t>(cap, (2 * m + kg) / (2 * kg)));
+    int64_t best_kg = 1, best_s = 1, best_dev = 0;
+    double best_imb = 0.0;
+    for (int64_t kg = 1; kg <= kg_max; ++kg) {
+        const int64_t cap = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kGemmMaxSplits, (int64_t)h0->s_cap,
+                                                                   h0->TC / (3 * kg)}));
+        const int64_t s = std::max<int64_t>(1, std::min<int64_t>(cap, (2 * m + kg) / (2 * kg)));
+        const int64_t blocks = row_blocks * s;
+        const double imb = (double)ceil_div(blocks, cus) * (double)cus / (double)blocks;
+        const int64_t dev = std::abs(kg * s - m);
+        if (kg == 1 || imb < best_imb - 1e-9 || (imb < best_imb + 1e-9 && dev <= best_dev)) {
+            best_kg = kg;
+            best_s = s;
+            best_imb = imb;
+            best_dev = dev;
+        }
+    }
+    *waves_out = (int32_t)(rows * best_kg);
+    *splits_out = (int32_t)best_s;
 }
 
 int se12_read_probe(const void* buf_dev, int64_t bytes, uint32_t* out_dev, int64_t out_elems, void* stream) {

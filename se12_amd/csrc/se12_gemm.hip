@@ -5,7 +5,7 @@
 // lws/adapters/cuda/kernels/gemv_se12.cu:50-142 at batch B, which runs one
 // warp per (row, batch) element and reads W B times.
 //
-// Grid: block = R x KG wave64s: R consecutive tile rows (R = ceil(batch / 8),
+// Grid: block = R x KG wave64s: R consecutive tile rows (R = ceil(batch / 8), 4 in place of 3,
 // the fewest waves whose threads load an x slab in one go) times KG K groups;
 // wave w owns tile row R * row_block + w % R and, of the split's K tiles, the
 // ones of K group w / R (every KG-th tile). blockIdx.y = K split s covering

@@ -219,7 +219,15 @@ constexpr int kGemmMaxThreadsGeneric = 256;
 
 constexpr int kGemmMaxSplits = 16;
 constexpr int kGemmXPieces = 4;
-constexpr int gemm_min_waves(int batch) { return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces); }
+// tile rows per block: the fewest waves whose threads load a batch x 256 x
+// slab (batch / 8, rounded up), rounded up to a power of two (3 waves leave a
+// SIMD of the CU without a row: 14336x3584 at B = 24 took 32.4 us with 3,
+// B = 32 26.2 with 4)
+constexpr int gemm_min_waves(int batch) {
+    return (batch * 32 + 64 * kGemmXPieces - 1) / (64 * kGemmXPieces) == 3 ? 4
+                                                                            : (batch * 32 + 64 * kGemmXPieces - 1) /
+                                                                                  (64 * kGemmXPieces);
+}
 size_t gemm_lds_bytes(int waves, int batch);
 hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
 

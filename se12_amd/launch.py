@@ -9,7 +9,7 @@ cut into `k_splits` contiguous ranges (the last block of a tile row to finish
 adds the splits in order). BF16 batches of MFMA_MIN_BATCH or more rows run
 the batched MFMA kernel instead, whose block is 1..8 wave64s each owning one
 tile row: there `blocks` = ceil(tile_rows / waves) x k_splits, and a block
-needs at least batch / 8 waves (each thread loads at most 4 x pieces per K
+needs batch / 8 waves, 4 in place of 3 (each thread loads at most 4 x pieces per K
 tile). The launch shape fixes the order of every sum, so the fused kernel and
 its raw twin agree bit for bit under one configuration. The default
 configuration itself is computed by the library (se12_default_launch) from
@@ -79,7 +79,10 @@ def uses_mfma(batch: int, float32_activations: bool = False) -> bool:
 
 
 def mfma_min_waves(batch: int) -> int:
-    return -(-batch // 8)
+    """Tile rows (waves) per block of the x-slab MFMA kernel: batch / 8
+    rounded up, and 4 in place of 3."""
+    r = -(-batch // 8)
+    return 4 if r == 3 else r
 
 
 def rx_lds_bytes(k: int, batch: int) -> int:

@@ -107,9 +107,10 @@ def test_translation_keeps_the_block_and_refuses_uncovered_launches():
     assert launch.waves_and_splits(cfg, 2304, 1, 9216) == (4, 1)
     cfg = launch.from_reference_configuration(RefLaunch(RefThreads(32), RefBlocks(2304)), 2304, 9216, 1)
     assert launch.waves_and_splits(cfg, 2304, 1, 9216) == (1, 1)
-    # B = 24 on the MFMA kernel: 3 tile rows per block, 512 threads -> 6 waves
-    cfg = launch.from_reference_configuration(RefLaunch(RefThreads(512), RefBlocks(3456)), 2304, 9216, 24)
-    assert launch.waves_and_splits(cfg, 2304, 24, 9216) == (6, 1)
+    # B = 24 on the x-slab MFMA kernel: 4 tile rows per block, 448 threads
+    # (7 waves) -> 8 waves
+    cfg = launch.from_reference_configuration(RefLaunch(RefThreads(448), RefBlocks(4000)), 2304, 9216, 24)
+    assert launch.waves_and_splits(cfg, 2304, 24, 9216) == (8, 1)
     with pytest.raises(ValueError, match="do not cover"):
         launch.from_reference_configuration(RefLaunch(RefThreads(256), RefBlocks(287)), 2304, 9216, 1)
     for t in (0, 16, 48 + 1, 2048):

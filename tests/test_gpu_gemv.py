@@ -270,7 +270,7 @@ def test_grouped_launch_equals_separate_launches(gpu):
     tolerance of the oracle under the default launch."""
     from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped
     from se12_amd.launch import (BlockCount, LaunchConfiguration, ThreadsPerBlock, configuration, grid_rows,
-                                 rx_configuration, rx_kgroups, uses_rx)
+                                 mfma_min_waves, rx_configuration, rx_kgroups, uses_rx)
 
     cols = 2304
     shapes = [(272, cols), (128, cols), (48, cols)]
@@ -311,7 +311,7 @@ def test_grouped_launch_equals_separate_launches(gpu):
         for waves, splits in ((3, 1), (9, 1), (4, 3), (6, 2)):
             if batch >= 4 and waves > 8:
                 continue
-            if batch >= 5 and waves % -(-batch // 8):  # MFMA: tile rows per block (batch / 8) x K groups
+            if batch >= 5 and waves % mfma_min_waves(batch):  # MFMA: tile rows per block x K groups
                 continue
             rows_total = sum(grid_rows(r, waves, batch) for r, _ in shapes)
             grouped = LaunchConfiguration(ThreadsPerBlock(64 * waves), BlockCount(rows_total * splits))

@@ -106,15 +106,20 @@ def test_launch_candidates_respect_each_kernels_limits():
                                  waves_and_splits)
 
     assert not uses_mfma(4) and uses_mfma(5) and not uses_mfma(32, float32_activations=True)
-    # MFMA blocks count row blocks of batch / 8 tile rows (rounded up); a
-    # block's waves are those rows times K groups
+    # MFMA blocks count row blocks of batch / 8 tile rows (rounded up, 4 in
+    # place of 3); a block's waves are those rows times K groups
+    from se12_amd.launch import mfma_min_waves
+
+    assert [mfma_min_waves(b) for b in (5, 8, 9, 16, 17, 24, 25, 32)] == [1, 1, 2, 2, 4, 4, 4, 4]
     assert configuration(4, 3, 2304, batch=8).blocks.value == 144 * 3
     assert configuration(4, 3, 2304, batch=32).blocks.value == 36 * 3
-    assert configuration(8, 1, 2304, batch=17).blocks.value == 48
+    assert configuration(8, 1, 2304, batch=17).blocks.value == 36
     assert configuration(4, 3, 2304, batch=4).blocks.value == 144 * 3
-    with pytest.raises(ValueError, match="multiple of 3"):
-        waves_and_splits(configuration(4, 1, 2304, batch=17), 2304, batch=17)
-    assert all(waves_and_splits(c, 2304, batch=24, k=9216)[0] % 3 == 0 for c in candidate_configurations(2304, 9216, batch=24))
+    with pytest.raises(ValueError, match="multiple of 4"):
+        waves_and_splits(configuration(6, 1, 2304, batch=17), 2304, batch=17)
+    with pytest.raises(ValueError, match="multiple of 2"):
+        waves_and_splits(configuration(3, 1, 2304, batch=9), 2304, batch=9)
+    assert all(waves_and_splits(c, 2304, batch=24, k=9216)[0] % 4 == 0 for c in candidate_configurations(2304, 9216, batch=24))
     assert min(waves_and_splits(c, 2304, batch=32, k=9216)[0] for c in candidate_configurations(2304, 9216, batch=32)) == 4
     assert max_waves_per_block(1) == 16 and max_waves_per_block(6) == 8
     for batch, f32, max_s in ((1, False, 36), (32, False, 16), (6, True, 36)):

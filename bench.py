@@ -21,9 +21,10 @@ step through hipBLASLt BF16 (torch.nn.functional.linear) and through the
 raw-BF16 twin kernel; per-shape microseconds; a roofline object for the dominant kernel - the fused GEMV at
 the 2304x9216 down_proj shape, timed live as 26 back-to-back launches over the
 26 layers' (cold) matrices; and the oracle's numpy decode + matmul timed on
-the host as the CPU baseline. Two more objects: the batch sweep B = 1..32 at
-the Gemma-2-9B gate_proj shape 14336x3584 against hipBLASLt BF16 (the
-crossover from the dot2 kernel to the MFMA kernel), batch-1 stress shapes
+the host as the CPU baseline. More objects: the batch sweep B = 1..32 at
+the Gemma-2-9B gate_proj shape 14336x3584 against hipBLASLt BF16 and the raw
+twin (the crossover from the dot2 kernel to the MFMA kernels), the
+decode-only kernel (SE12 -> BF16) at three shapes, batch-1 stress shapes
 with heavy-tailed weights (tied LM head 256000x2304, Gemma-2-27B down_proj
 4608x36864), and a random-init Gemma-2-2B greedy decode (prompt 512, 128
 tokens) whose decode tokens/s is the `decode_tok_s` field.
@@ -74,6 +75,7 @@ def parse_args(argv=None):
     p.add_argument("--no-per-shape", action="store_true")
     p.add_argument("--no-batch-sweep", action="store_true")
     p.add_argument("--no-stress", action="store_true")
+    p.add_argument("--no-decode", action="store_true", help="skip the decode-only kernel timings")
     p.add_argument("--no-e2e", action="store_true", help="skip the Gemma-2-2B greedy decode")
     p.add_argument("--no-micro", action="store_true", help="skip the microbenchmark / verdict files")
     p.add_argument("--no-model", action="store_true", help="skip the roofline model's calibration")
@@ -283,13 +285,15 @@ def cold_rotation(nbytes: int) -> int:
     return max(2, -(-int(1.1e9) // nbytes))
 
 
-def batch_sweep(device, batches=(1, 2, 4, 8, 16, 32)) -> dict:
+def batch_sweep(device, batches=(1, 2, 4, 5, 6, 7, 8, 16, 24, 32)) -> dict:
     """Gemma-2-9B gate_proj 14336x3584, BF16 N(0, 0.02): the fused product at
-    each batch (the dot2 kernel up to 4 rows, the MFMA kernel from 5; one pass
-    over the weights either way) against hipBLASLt BF16 at the same batch,
-    each timed per launch over a rotation of cold matrices."""
-    from se12_amd.hip import Se12MatVecKernel, encode_on_device
-    from se12_amd.launch import uses_mfma
+    each batch (the dot2 kernel up to 4 rows, an MFMA kernel from 5; one pass
+    over the weights either way) against hipBLASLt BF16 and the raw twin at
+    the same batch, each timed per launch over a rotation of cold matrices.
+    B = 5..7 show the MFMA kernel where the dot2 kernel, 4 batch rows per
+    pass, would need a second pass over the weights."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+    from se12_amd.launch import uses_mfma, uses_rx
 
     n, k = 14336, 3584
     gen = torch.Generator(device=device)
@@ -312,15 +316,62 @@ def batch_sweep(device, batches=(1, 2, 4, 8, 16, 32)) -> dict:
         us = time_graph(g, 10, 3) * 1e3 / len(kerns)
         gb = capture(lambda x=x: [torch.nn.functional.linear(x, w) for w in ws])
         us_b = time_graph(gb, 10, 3) * 1e3 / len(ws)
-        del g, gb
+        raws = [RawBf16MatVecKernel(w, max_batch=b) for w in ws]
+        yr = [torch.empty((b, n), dtype=torch.float32, device=device) for _ in raws]
+        gr = capture(lambda x=x: [r.multiply(x, out=y) for r, y in zip(raws, yr)])
+        us_r = time_graph(gr, 10, 3) * 1e3 / len(raws)
+        del g, gb, gr, raws, yr
         lc = kerns[0].default_launch(b)
-        pt = {"batch": b, "kernel": "mfma" if uses_mfma(b) else "dot2", "us": round(us, 3),
+        kernel = ("mfma_resident_x" if uses_rx(n, k, b) else "mfma_x_slab") if uses_mfma(b) else "dot2"
+        pt = {"batch": b, "kernel": kernel, "us": round(us, 3),
               "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
               "se12_gbps": round(kerns[0].tensor.byte_size() / (us * 1e-6) / 1e9, 1),
               "bf16_hipblaslt_us": round(us_b, 3), "speedup_of_se12": round(us_b / us, 4),
+              "raw_twin_us": round(us_r, 3), "speedup_vs_faster_baseline": round(min(us_b, us_r) / us, 4),
               "launch": [lc.threads_per_block.value, lc.blocks.value]}
         out["points"].append(pt)
         log(f"[bench] batch sweep {pt}")
+    return out
+
+
+def decode_only(device, shapes=((2304, 9216), (9216, 2304), (256000, 2304))) -> dict:
+    """The decode-only kernel (SE12 -> row-major BF16, the path of prefill and
+    mode="exact"; lws/adapters/cuda/kernels/se12_decode.cu:12-43 is the
+    reference's) on BF16 N(0, 0.02) matrices, timed per launch over a rotation
+    of cold copies in one graph, beside a device copy of the same BF16 matrix
+    (2 bytes read + 2 written per weight; the decode reads the streams, about
+    1.5 bytes, and writes 2). Algorithmic bytes per launch: the streams plus
+    the BF16 output."""
+    from se12_amd.hip import HipBenchmarkTimer, Se12MatVecKernel, encode_on_device
+    from se12_amd.micro import cold_copies
+
+    timer = HipBenchmarkTimer(device.index)
+    out = {}
+    for n, k in shapes:
+        gen = torch.Generator(device=device)
+        gen.manual_seed(n + k)
+        w = (torch.randn((n, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+        enc = encode_on_device(w)
+        copies = cold_copies(enc.byte_size() + 2 * n * k)
+        kerns = [Se12MatVecKernel(e, max_batch=1) for e in [enc] + [enc.clone() for _ in range(copies - 1)]]
+        dst = [torch.empty((n, k), dtype=torch.bfloat16, device=device) for _ in range(copies)]
+        st = timer.time_cold_rotation([lambda kk=kk, d=d: kk.decode_into(d) for kk, d in zip(kerns, dst)], 3, 10)
+        exact = bool(torch.equal(dst[0], w))
+        del kerns
+        srcs = [w] + [w.clone() for _ in range(copies - 1)]
+        st_c = timer.time_cold_rotation([lambda s_=s_, d=d: d.copy_(s_) for s_, d in zip(srcs, dst)], 3, 10)
+        del srcs, dst
+        alg = enc.byte_size() + 2 * n * k
+        us = st.median_us
+        out[f"{n}x{k}"] = {"us": round(us, 3), "p10_us": round(st.p10_us, 3), "p90_us": round(st.p90_us, 3),
+                           "algorithmic_bytes": alg, "gbps": round(alg / (us * 1e-6) / 1e9, 1),
+                           "frac_of_hbm_peak": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+                           "bf16_copy_us": round(st_c.median_us, 3),
+                           "bf16_copy_gbps": round(4 * n * k / (st_c.median_us * 1e-6) / 1e9, 1),
+                           "cold_copies": copies, "bit_exact": exact}
+        log(f"[bench] decode only {n}x{k}: {out[f'{n}x{k}']}")
+        del enc, w
+        torch.cuda.empty_cache()
     return out
 
 
@@ -759,6 +810,8 @@ def main(argv=None) -> int:
         torch.cuda.empty_cache()
         result["batch_sweep"] = batch_sweep(dev)
         torch.cuda.empty_cache()
+    if not args.no_decode:
+        result["decode_only"] = decode_only(dev)
     if not args.no_stress:
         result["stress"] = stress(dev)
     if not args.no_e2e:

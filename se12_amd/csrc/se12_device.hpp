@@ -333,6 +333,36 @@ __device__ __forceinline__ const int16_t* raw_tile_ptr(uint32_t info, const int1
     return (info_is_overflow(info) ? ovf_raw : fb_raw) + (int64_t)info_rank(info) * kTile;
 }
 
+// Waits for every vector memory load in flight (vmcnt(0)) through the
+// compiler's intrinsic, which its wait counting sees (inline asm it does not).
+// A branch whose loads fill registers that the other branch computes (a raw
+// tile beside a decoded one) ends with it: the join would otherwise inherit
+// the pending load and wait there, on the common path too, for every load in
+// flight, prefetched tiles included.
+// wait_vector_loads_to<N>() leaves the last N in flight (vmcnt(N)).
+template <int N>
+__device__ __forceinline__ void wait_vector_loads_to() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_vector_loads() { wait_vector_loads_to<0>(); }
+
+// LDS byte address of a pointer into LDS (the low half of its generic address)
+__device__ __forceinline__ uint32_t lds_address(const void* p) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(p));
+}
+
+// One 16-byte global load per lane straight into LDS: lane l's bytes land at
+// LDS byte address lds + 16 l (lds wave-uniform). Inline asm, which the
+// compiler's wait counting does not see: the caller waits for it itself
+// (s_waitcnt vmcnt) before reading the LDS it fills. The compiler's own
+// waits stay correct as long as loads it tracks are only waited for by
+// count (loads complete in order, so an unseen load only makes a count
+// wait for more).
+__device__ __forceinline__ void lds_load16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
 // Raw BF16 pairs of chunk j of a fallback tile (tile-local order, like sm).
 __device__ __forceinline__ void load_raw_chunk(const int16_t* tile_raw, int j, uint32_t lane, uint32_t w[8]) {
     const uint4* p = reinterpret_cast<const uint4*>(tile_raw + 1024 * j + 16 * lane);

@@ -292,12 +292,12 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
             const uint32_t info = side_info(t.side, 0);
             if (info_is_fallback(info)) {
                 const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
+                uint32_t wv[4][8];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    uint32_t wv[8];
-                    load_raw_part(raw, p, lane, wv);
-                    part(p, wv);
-                }
+                for (int p = 0; p < 4; ++p) load_raw_part(raw, p, lane, wv[p]);
+                wait_vector_loads();  // rare path: keeps the common path's waits exact
+#pragma unroll
+                for (int p = 0; p < 4; ++p) part(p, wv[p]);
             } else {
                 uint32_t pat[4][8];
                 lookup_tile(lut, t.t, pat);

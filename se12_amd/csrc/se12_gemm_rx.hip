@@ -114,23 +114,28 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
     const int kb = kg, ks = KG, ke = TC;
 
     // The wave's tiles in order: its slot's r-th row (j0 + r nw), its K
-    // tiles in ascending order. A cursor (r, kt) walks them and stops past
-    // the wave's last tile, where loads are no longer issued (a wave without
-    // rows loads nothing).
+    // tiles in ascending order. A cursor (r, kt) walks them; the load cursor
+    // stops at the wave's last tile (a one-tile wave's second ring slot
+    // re-loads that tile).
+    const int per_row = (ke - kb + ks - 1) / ks;               // K tiles per row of this group
+    const int n_tiles = rows * per_row;
     struct Cursor {
         int r, kt;
     };
     auto advance = [&](Cursor& c) {
-        if (c.r >= rows) return;
         c.kt += ks;
         if (c.kt >= ke) {
             c.kt = kb;
             ++c.r;
         }
     };
+    auto advance_clamped = [&](Cursor& c) {
+        Cursor n = c;
+        advance(n);
+        if (n.r < rows) c = n;
+    };
     auto row_of = [&](const Cursor& c) { return j0 + c.r * nw; };
     auto load = [&](RxTile<RAW>& t, const Cursor& c) {
-        if (c.r >= rows) return;
         const int tr = row_of(c), kt = c.kt;
         if constexpr (RAW) {
             rx_load_raw_blocks(t.r, a.wraw, a.K, tr, kt, lane);
@@ -139,23 +144,29 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
         }
     };
 
-    // the first kRxDepth tiles, then the pair table and all of x (direct to LDS)
-    RxTile<RAW> ring[kRxDepth]{};
+    // The first kRxDepth tiles, then all of x and the pair table straight to
+    // LDS (direct-to-LDS loads: no registers held); the block meets once
+    // everything has landed. (x first, with the barrier waiting for x only,
+    // measured no faster: the tiles' loads then start later.) The LDS loads
+    // are inline asm, which the compiler's wait counting does not see: with
+    // its own direct-to-LDS loads it waits for every load in flight (vmcnt(0))
+    // at each step of the ring below, the other slot's included.
+    RxTile<RAW> ring[kRxDepth];
     Cursor ld{0, kb};
+    constexpr int kLoadsPerTile = RAW ? 8 : 9;
+    if (n_tiles > 0) {
 #pragma unroll
-    for (int d = 0; d < kRxDepth; ++d) {
-        load(ring[d], ld);
-        advance(ld);
+        for (int d = 0; d < kRxDepth; ++d) {
+            load(ring[d], ld);
+            advance_clamped(ld);
+        }
     }
-    uint4 lutv;
-    if constexpr (!RAW) lutv = reinterpret_cast<const uint4*>(a.lut)[lane];
     {
-        // x in rounds of one piece per thread; block b starts at round
-        // b mod rounds, so that the blocks, which all read the same x from
-        // L2 at the same time, spread over its channels
         const int total = batch * ppr;                         // pieces of x
         const int rounds = (total + threads - 1) / threads;
         const uint16_t* x = static_cast<const uint16_t*>(a.x);
+        // block b starts at round b mod rounds, so that the blocks, which all
+        // read the same x from L2 at the same time, spread over its channels
         int r = (int)(blockIdx.x % (unsigned)rounds);
         for (int i = 0; i < rounds; ++i) {
             const int base = r * threads + w * 64;
@@ -163,14 +174,15 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
                 const int p = min(base + (int)lane, total - 1);  // a lane past the end re-loads the last piece
                 const int b = p / ppr, e = p - b * ppr;
                 const int q = e ^ (b & 7);                       // LDS piece p holds x piece q of row b
-                __builtin_amdgcn_global_load_lds(x + (int64_t)b * a.K + 8 * q, xs + 16 * base, 16, 0, 0);
+                lds_load16(x + (int64_t)b * a.K + 8 * q, lds_address(xs + 16 * base));
             }
             r = r + 1 == rounds ? 0 : r + 1;
         }
     }
-    if constexpr (!RAW) store_block_lut(lut, lutv, lane);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    // the 1 KB pair table: lane l's 16 bytes to LDS bytes 16 l .. + 15
+    if (!RAW && w == 0) lds_load16(reinterpret_cast<const uint4*>(a.lut) + lane, lds_address(lut));
+    wait_vector_loads();
+    lds_barrier();
 
     rx_floatx4_t acc[BG];
 #pragma unroll
@@ -243,12 +255,12 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
             const uint32_t info = side_info(t.side, 0);
             if (info_is_fallback(info)) {
                 const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
+                uint32_t wv[4][8];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) {
-                    uint32_t wv[8];
-                    rx_raw_part(raw, p, lane, wv);
-                    mfma_part(wv, kt, p);
-                }
+                for (int p = 0; p < 4; ++p) rx_raw_part(raw, p, lane, wv[p]);
+                wait_vector_loads();  // rare path: keeps the common path's waits exact
+#pragma unroll
+                for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p);
             } else {
                 chunks_to_blocks(t.t);  // in place: the slot is reloaded next
                 // each part's patterns merged with its sm bytes as soon as
@@ -274,34 +286,55 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
             for (int g = 0; g < BG; ++g) acc[g] = rx_floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
     };
-    // the ring: a step uses one slot, then reloads it with the tile
-    // kRxDepth ahead; the body holds kRxDepth steps so that every slot index
-    // is a constant, and leaves after the wave's last tile
+    // The ring (two slots): while tiles remain to load, a step uses one slot
+    // and reloads it with the tile two ahead; the last two tiles are used
+    // without reloads (a load past the wave's last tile would hold the wave,
+    // and the end of the kernel, for one more memory latency). Inside the
+    // loop every load is issued on every path, so the compiler's wait counts
+    // stay exact (a load skipped on one path would merge into a wait for all
+    // loads in flight, the other slot's included).
+    static_assert(kRxDepth == 2, "the ring below has two slots");
     Cursor cu{0, kb};
-    if (rows > 0 && kb < ke) {
-        bool more = true;
-        while (more) {
-#pragma unroll
-            for (int d = 0; d < kRxDepth; ++d) {
-                if (more) {
-                    use(ring[d], cu);
-                    // the slot's next loads after its use: hoisted above it,
-                    // they would hold a third tile's registers
-                    __builtin_amdgcn_sched_barrier(0);
-                    load(ring[d], ld);
-                    advance(ld);
-                    advance(cu);
-                    more = cu.r < rows;
-                }
-            }
+    auto step = [&](RxTile<RAW>& t) {
+        use(t, cu);
+        advance(cu);
+        __builtin_amdgcn_sched_barrier(0);  // no work of the next step above this one's
+    };
+    auto step_reload = [&](RxTile<RAW>& t) {
+        step(t);
+        // the slot's next loads after its use: hoisted above it, they would
+        // hold a third tile's registers
+        __builtin_amdgcn_sched_barrier(0);
+        load(t, ld);
+        advance_clamped(ld);
+    };
+    if (n_tiles > 0) {
+        // pair j uses tiles 2j, 2j + 1 and loads 2j + 2, 2j + 3
+        int j = 0;
+        for (; 2 * j + 3 < n_tiles; ++j) {
+            step_reload(ring[0]);
+            step_reload(ring[1]);
         }
+        // the last two or three tiles: a third is loaded into the first
+        // slot once it is used; the waits are explicit so that the second
+        // slot's use does not also wait for that load
+        const int left = n_tiles - 2 * j;  // 1 (a one-tile wave), 2 or 3
+        step(ring[0]);
+        if (left == 3) {
+            load(ring[0], ld);
+            wait_vector_loads_to<kLoadsPerTile>();
+        } else {
+            wait_vector_loads();
+        }
+        if (left >= 2) step(ring[1]);
+        if (left == 3) step(ring[0]);
     }
     if (KG == 1) return;
     // K groups: every wave is past its last MFMA (x is no longer read), the
     // groups 1.. of each slot leave their sums in LDS over x, and group 0
     // adds them in ascending group order and stores the row
     __syncthreads();
-    const bool has_row = rows > 0 && kb < ke;
+    const bool has_row = n_tiles > 0;
     rx_floatx4_t* part = reinterpret_cast<rx_floatx4_t*>(xs);  // [KG - 1][RW][64 lanes][BG]
     if (kg > 0) {
 #pragma unroll

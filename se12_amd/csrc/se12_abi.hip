@@ -996,7 +996,7 @@ int se12_decode(se12_handle* h, uint16_t* out, void* stream) {
     SE12_HIP(ds.enter(h->device));
     DecodeArgs a = decode_args(h, out);
     a.items = h->T;
-    hipError_t e = launch_decode(a, false, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_decode(a, false, static_cast<hipStream_t>(stream), h->cu_count);
     if (e != hipSuccess) return fail(SE12_E_HIP, "se12_decode launch: %s", hipGetErrorString(e));
     return SE12_OK;
 }
@@ -1013,7 +1013,7 @@ int se12_decode_rows(se12_handle* h, const int64_t* rows, int64_t nrows, uint16_
     a.rows = rows;
     a.nrows = nrows;
     a.items = nrows * h->TC;
-    hipError_t e = launch_decode(a, true, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_decode(a, true, static_cast<hipStream_t>(stream), h->cu_count);
     if (e != hipSuccess) return fail(SE12_E_HIP, "se12_decode_rows launch: %s", hipGetErrorString(e));
     return SE12_OK;
 }

@@ -1,7 +1,9 @@
 // Decode-only kernels: SE12 streams -> row-major BF16 bits, bit-exact with the
-// reference decoder (lws/domain/se12/codec.py:144-186). One wave decodes one
+// reference decoder (lws/domain/se12/codec.py:144-186). A wave decodes a
 // 16x256 tile with the same per-lane routine as the fused GEMV and writes its
-// rows straight to the cropped [rows, cols] output, replacing the reference's
+// rows straight to the cropped [rows, cols] output (the whole-matrix decode
+// streams several tiles per wave; the row decode takes one (row, K tile) per
+// wave), replacing the reference's
 // one-thread-per-tile kernel plus device untile/crop
 // (lws/adapters/cuda/kernels/se12_decode.cu:12-43,
 // lws/adapters/cuda/se12_decoder.py:147-185).
@@ -29,23 +31,19 @@ __device__ __forceinline__ void store16(uint16_t* out_row, int64_t col, int64_t 
     }
 }
 
-// Decodes tile `tile` for this lane; calls sink(j, w) for each chunk j.
+// Decodes a loaded tile for this lane; calls sink(j, w) for each chunk j.
 template <typename Sink>
-__device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t* lut, int64_t tile, uint32_t lane,
-                                            Sink&& sink) {
-    TileSide side;
-    TileLoads t;
-    load_side(side, a.side, tile, lane);
-    load_tile(t, a.sm, a.ec, tile, lane);
+__device__ __forceinline__ void decode_loaded(const DecodeArgs& a, const uint32_t* lut, const TileSide& side,
+                                              const TileLoads& t, uint32_t lane, Sink&& sink) {
     const uint32_t info = side_info(side, 0);
     if (info_is_fallback(info)) {
         const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
+        uint32_t w[4][8];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            uint32_t w[8];
-            load_raw_chunk(raw, j, lane, w);
-            sink(j, w);
-        }
+        for (int j = 0; j < 4; ++j) load_raw_chunk(raw, j, lane, w[j]);
+        wait_vector_loads();  // rare path: keeps the common path's waits exact
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sink(j, w[j]);
     } else {
         uint32_t pat[4][8];
         lookup_tile(lut, t, pat);
@@ -56,6 +54,76 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
             merge_chunk(pat[j], t.sm[j], w);
             sink(j, w);
         }
+    }
+}
+
+// Loads and decodes tile `tile` for this lane; calls sink(j, w) for each chunk j.
+template <typename Sink>
+__device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t* lut, int64_t tile, uint32_t lane,
+                                            Sink&& sink) {
+    TileSide side;
+    TileLoads t;
+    load_side(side, a.side, tile, lane);
+    load_tile(t, a.sm, a.ec, tile, lane);
+    decode_loaded(a, lut, side, t, lane, sink);
+}
+
+// Whole-matrix decode: nw waves stream the tiles, wave g taking tiles g,
+// g + nw, ... (the waves read a moving window of the tile-major streams),
+// each with the next tile's loads in flight while it decodes and stores the
+// current one. The last tile loads nothing after it (a wave cannot end
+// before its loads land), and every load inside the loop is issued on every
+// path, so the compiler's wait counts stay exact.
+__global__ __launch_bounds__(kDecodeWaves * kWave) void decode_stream_kernel(DecodeArgs a, int64_t nw) {
+    SE12_DECLARE_LUT(lut);
+    const int tid = threadIdx.x;
+    const uint32_t lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t g = (int64_t)blockIdx.x * kDecodeWaves + w;
+    const int64_t n = g < nw && g < a.T ? (a.T - 1 - g) / nw + 1 : 0;  // tiles of this wave
+    struct Slot {
+        TileSide side;
+        TileLoads t;
+    };
+    auto load = [&](Slot& sl, int64_t i) {
+        const int64_t tile = std::min<int64_t>(g + i * nw, a.T - 1);
+        load_side(sl.side, a.side, tile, lane);
+        load_tile(sl.t, a.sm, a.ec, tile, lane);
+    };
+    const bool vec_ok = a.out_vec_ok != 0;
+    auto emit = [&](const Slot& sl, int64_t i) {
+        const int64_t tile = g + i * nw;
+        const int tr = (int)(tile / a.TC);
+        const int kt = (int)(tile - (int64_t)tr * a.TC);
+        const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
+        decode_loaded(a, lut, sl.side, sl.t, lane, [&](int j, const uint32_t* wv) {
+            const int64_t row = (int64_t)tr * kTileRows + 4 * j + (lane >> 4);
+            if (row < a.N) store16(a.out + row * a.K, col, a.K, vec_ok, wv);
+        });
+    };
+    // the pair table, then the first tile (a wave past the grid's waves
+    // re-loads tile g's clamp, so that the table's wait count is exact)
+    const uint4 lutv = reinterpret_cast<const uint4*>(a.lut)[lane];
+    Slot s0, s1;
+    load(s0, 0);
+    store_block_lut(lut, lutv, lane);
+    lds_barrier();
+    if (n == 0) return;
+    int64_t i = 0;
+    while (true) {
+        if (i + 1 >= n) {
+            emit(s0, i);
+            break;
+        }
+        load(s1, i + 1);
+        emit(s0, i);
+        if (++i + 1 >= n) {
+            emit(s1, i);
+            break;
+        }
+        load(s0, i + 1);
+        emit(s1, i);
+        ++i;
     }
 }
 
@@ -99,13 +167,22 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeArgs
     }
 }
 
-hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream) {
+// waves of the whole-matrix decode per CU (MI355X, cold HBM: 2304x9216 19.0 us
+// with 4, 21.0 with 8, 20.0 with 16, 25.5 with 2, 21.3 with one wave per
+// tile; 14336x3584 38.8 / 39.9 / 40.6 / 57.3 / 41.7; the 256000x2304 LM head
+// 394 against 389 with one wave per tile)
+constexpr int kDecodeStreamWavesPerCu = 4;
+
+hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream, int cu_count) {
     if (a.items <= 0) return hipSuccess;
-    const int64_t blocks = (a.items + kDecodeWaves - 1) / kDecodeWaves;
-    if (rows)
+    if (rows) {
+        const int64_t blocks = (a.items + kDecodeWaves - 1) / kDecodeWaves;
         hipLaunchKernelGGL(decode_kernel<true>, dim3((uint32_t)blocks), dim3(kDecodeWaves * kWave), 0, stream, a);
-    else
-        hipLaunchKernelGGL(decode_kernel<false>, dim3((uint32_t)blocks), dim3(kDecodeWaves * kWave), 0, stream, a);
+    } else {
+        const int64_t nw = std::min<int64_t>(a.T, (int64_t)std::max(1, cu_count) * kDecodeStreamWavesPerCu);
+        const int64_t blocks = (nw + kDecodeWaves - 1) / kDecodeWaves;
+        hipLaunchKernelGGL(decode_stream_kernel, dim3((uint32_t)blocks), dim3(kDecodeWaves * kWave), 0, stream, a, nw);
+    }
     return hipGetLastError();
 }
 

@@ -259,7 +259,7 @@ constexpr size_t rx_lds_total(int64_t k, int batch, int waves, int kgroups) {
     return rx_lds_bytes(k, batch) > sums ? rx_lds_bytes(k, batch) : sums;
 }
 hipError_t launch_gemm_rx(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
-hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream);
+hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream, int cu_count);
 // Bind-time sidecar: one word per tile (fallback rank, or the chunks holding
 // escape codes) and the fallback tile count.
 // total[0] = fallback tiles, total[1] = tiles with more than the listed escapes

@@ -545,23 +545,27 @@ static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
     return tr;
 }
 
-// Default launch of the resident-x kernel: 12 waves per block (3 per SIMD,
-// the kernel's register limit) and one block per CU, fewer where a matrix
-// has fewer tile rows than its share of the CUs; on matrices of 16 or more
-// tile rows per CU, 8 waves and two blocks per CU (256000x2304: 172 us
-// against 191 at 8 rows, 184 against 186 at 16, 203 against 201 at 32).
-// Where rows are few, the K groups (rx_kgroups) put several waves on each
-// row.
+// Default launch of the resident-x kernel: one block per CU (fewer where a
+// matrix has fewer tile rows than its share of the CUs) of 12 waves (3 per
+// SIMD, the kernel's register limit) up to 2 tile rows per CU, 8 waves up to
+// 3 and, up to 16 batch rows, 6 waves up to 16, which with the K groups
+// (rx_kgroups) keeps about 4 waves per CU on rows, each on more tiles
+// (14336x3584, 3.5 rows per CU, B = 9 / 16: 20.0 / 21.5 us with 6 waves
+// against 21.6 / 22.5 with 12, B = 20 23.9 against 23.5; 9216x2304, 2.25 rows
+// per CU, B = 9 / 16 / 20: 13.3 / 13.9 / 14.7 with 8 against 14.1 / 14.5 /
+// 15.2; at 1 to 1.5 rows per CU 12 waves stay best); on
+// matrices of 16 or more tile rows per CU, 8 waves and two blocks per CU
+// (256000x2304: 172 us against 191 at 8 rows, 184 against 186 at 16, 203
+// against 201 at 32).
 static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
                               int32_t* blocks_out) {
-    (void)batch;
     const int64_t cus = std::max<int32_t>(1, hs[0]->cu_count);
     int64_t rows = 0;
     for (int32_t i = 0; i < count; ++i) rows += hs[i]->TR;
     const bool tall = rows >= 16 * cus;
     const int64_t per_matrix =
         std::max<int64_t>(1, std::min<int64_t>(rx_max_blocks(hs, count), ceil_div((tall ? 2 : 1) * cus, count)));
-    *waves_out = tall ? 8 : kRxMaxThreads / 64;
+    *waves_out = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
     *blocks_out = (int32_t)(per_matrix * count);
 }
 

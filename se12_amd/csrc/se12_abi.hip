@@ -519,23 +519,17 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // The launches of one product over `count` handles that share x (a single
 // matrix for se12_gemv, up to kMaxGroup for se12_gemv_grouped): one MFMA
 // launch for all rows, or one dot2 launch per 4 rows.
-// The resident-x batched kernel serves FAST launches of BF16 x with
-// kRxMinBatch or more rows, or kGemmMinBatch or more over at least
-// kRxMinTiles tiles, whose x fits a block's LDS beside the pair table, on
-// matrices of whole tile rows (both formats alike, so that a fused kernel and
-// its raw twin always run the same kernel and stay bit-identical). Below
-// those sizes the x-slab kernel measured as fast or faster (14336 x 3584 at 8
-// rows: 20.8 against 22.3 us; 4096 x 14336 at 5 rows: 29.5 against 26.6).
-constexpr int32_t kRxMinBatch = 9;
-constexpr int64_t kRxMinTiles = 14336;
-
+// The resident-x batched kernel serves every FAST MFMA launch (BF16 x with
+// kGemmMinBatch or more rows) whose x fits a block's LDS beside the pair
+// table, on matrices of whole tile rows (both formats alike, so that a fused
+// kernel and its raw twin always run the same kernel and stay bit-identical).
+// Since its waits and launch were refitted it beats the x-slab kernel at 5-8
+// rows too (default launches, cold: 9216x4096 B = 5 18.5 against 21.0 us,
+// 2304x2304 8.5 against 10.2, 3584x14336 22.6 against 24.3, 14336x3584 B = 8
+// 20.3 against 20.4).
 static bool rx_fits(se12_handle* const* hs, int32_t count, int32_t batch) {
-    int64_t tiles = 0;
-    for (int32_t i = 0; i < count; ++i) {
+    for (int32_t i = 0; i < count; ++i)
         if (hs[i]->N % SE12_TILE_ROWS != 0) return false;
-        tiles += (int64_t)hs[i]->TR * hs[i]->TC;
-    }
-    if (batch < kRxMinBatch && tiles < kRxMinTiles) return false;
     return (int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= hs[0]->lds_per_block;
 }
 

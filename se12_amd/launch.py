@@ -30,15 +30,12 @@ MFMA_MIN_BATCH = 5
 MFMA_MAX_K_SPLITS = 16
 MFMA_MAX_WAVES = 8
 MFMA_MAX_WAVES_GENERIC = 4   # the edge-handling MFMA variants (K % 256 != 0 or unaligned x)
-# The resident-x MFMA kernel: BF16 batches of RX_MIN_BATCH rows or more (or
-# MFMA_MIN_BATCH or more on matrices of RX_MIN_TILES tiles or more) on FAST
-# shapes whose x (batch x K BF16, in whole 1 KiB loads) fits a block's LDS
-# (gfx950: 160 KiB) beside the 1 KiB pair table. Its launch is (waves per
-# block 1..12, blocks per matrix 1..tile rows); the launch fixes the K groups
-# (rx_kgroups) and with them the order of every sum.
+# The resident-x MFMA kernel: every MFMA batch (MFMA_MIN_BATCH BF16 rows or
+# more) on FAST shapes whose x (batch x K BF16, in whole 1 KiB loads) fits a
+# block's LDS (gfx950: 160 KiB) beside the 1 KiB pair table. Its launch is
+# (waves per block 1..12, blocks per matrix 1..tile rows); the launch fixes
+# the K groups (rx_kgroups) and with them the order of every sum.
 RX_MAX_WAVES = 12
-RX_MIN_BATCH = 9
-RX_MIN_TILES = 14336
 LDS_PER_BLOCK = 160 * 1024
 LUT_BYTES = 1024
 RX_BLOCK_CANDIDATES = (32, 64, 128, 192, 256, 384, 512, 768, 1024)
@@ -94,7 +91,6 @@ def uses_rx(output_rows: int, k: int, batch: int, float32_activations: bool = Fa
     """Whether a launch runs the resident-x MFMA kernel (the library's rule)."""
     return (uses_mfma(batch, float32_activations) and aligned_x
             and not runs_generic(output_rows, k, float32_activations)
-            and (batch >= RX_MIN_BATCH or tile_rows(output_rows) * k_tiles(k) >= RX_MIN_TILES)
             and rx_lds_bytes(k, batch) + LUT_BYTES <= LDS_PER_BLOCK)
 
 

@@ -127,14 +127,14 @@ def test_launch_candidates_respect_each_kernels_limits():
         pairs = [waves_and_splits(c, 2304, batch=batch, k=9216, float32_activations=f32) for c in cfgs]
         assert max(s for _, s in pairs) == max_s
         assert max(w for w, _ in pairs) == max_waves_per_block(batch, f32)
-    # 9 or more BF16 rows of x that fit a block's LDS (9 x 2304: 41 KiB), or
-    # 5..8 rows over 14336 tiles or more: the resident-x kernel, (waves
-    # 1..12, blocks 1..tile rows); 9 rows at K = 9216 (162 KiB) do not fit
+    # 5 or more BF16 rows of x that fit a block's LDS (9 x 2304: 41 KiB): the
+    # resident-x kernel, (waves 1..12, blocks 1..tile rows); 9 rows at K =
+    # 9216 (162 KiB) do not fit, 6 (108 KiB) do
     from se12_amd.launch import rx_lds_bytes, uses_rx
 
     assert uses_rx(2304, 2304, 9) and not uses_rx(2304, 9216, 9) and not uses_rx(2304, 2304, 9, float32_activations=True)
-    assert not uses_rx(2304, 9216, 6) and uses_rx(4096, 14336, 5) and uses_rx(256000, 2304, 5)
-    assert not uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and not uses_rx(14336, 3584, 24)
+    assert uses_rx(2304, 9216, 6) and uses_rx(4096, 14336, 5) and not uses_rx(4096, 14336, 6) and uses_rx(256000, 2304, 5)
+    assert uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and not uses_rx(14336, 3584, 24)
     assert not uses_rx(2304, 2300, 9) and not uses_rx(2300, 2304, 9) and not uses_rx(256000, 2304, 4)
     assert rx_lds_bytes(9216, 6) == 6 * 1152 * 16 and rx_lds_bytes(2304, 5) == 1472 * 16
     pairs = [waves_and_splits(c, 2304, batch=9, k=2304) for c in candidate_configurations(2304, 2304, batch=9)]

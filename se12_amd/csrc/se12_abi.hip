@@ -337,8 +337,11 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     int64_t waves, splits = 1;
     if (tr < cus) {
         // one wave per K tile up to 9 (Gemma-2 2B), else 8 (2048x3584: 5.4 us
-        // against 14 waves' slower launch; 3584x4096: 6.3 against 7.4 with 16)
-        waves = tc <= 9 ? tc : 8;
+        // against 14 waves' slower launch; 3584x4096: 6.3 against 7.4 with
+        // 16), 4 at 4 rows per launch (2304x9216 11.4 against 11.8, 3584x4096
+        // 7.7-8.0 against 8.1, 3584x14336 18.5-19.0 against 19.1; at 3 rows
+        // 2304x9216 10.9 against 10.7)
+        waves = tc <= 9 ? tc : (bl >= 4 ? 4 : 8);
         if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
     } else if (tc > 32) {
         // long rows on many tile rows (4608x36864): one wave per block and
@@ -351,20 +354,21 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     } else if (tiles <= 10 * cus) {
         waves = std::min<int64_t>(16, tc);
     } else if (tiles <= 32 * cus) {
-        // 3 waves for 9 K tiles (9216x2304); longer rows 8 waves at 1..2 rows
-        // per launch when the tile rows fill the CUs once (4096x3584: 6.3 us
+        // 3 waves for 9 K tiles (9216x2304), 2 at 4 rows per launch (11.0 us
+        // against 11.3; at 3 rows 10.5 against 10.4); longer rows 8 waves at 1..2 rows per
+        // launch when the tile rows fill the CUs once (4096x3584: 6.3 us
         // against 7.2 with 3; 4096x4608: 7.3 against 8.3), 4 where some CUs
         // take two blocks (4608x4096: 8.6 against 9.0 with 8) and at 3..4
         // rows (7.95 / 9.0 against 8.2 / 9.2)
-        waves = tc <= 9 ? 3 : (bl >= 3 || tr > cus ? 4 : 8);
+        waves = tc <= 9 ? (bl >= 4 ? 2 : 3) : (bl >= 3 || tr > cus ? 4 : 8);
         waves = std::min<int64_t>(waves, tc);
     } else if (tiles <= 64 * cus) {
-        // 2 rows and more per launch: 2 waves (14336x3584, B = 2..4: 17.8 us
-        // against 19.5 with tc / 2 = 7 waves, 19.8 against 26.9 at B = 4);
-        // one row: about half the K tiles, rounded up to an even count
-        // (14336x3584: 8 waves 16.2 us, 7 waves 16.8)
+        // 2 rows per launch: 2 waves (14336x3584, B = 2: 17.8 us against 19.5
+        // with tc / 2 = 7 waves), 3..4 rows: 1 wave (B = 3 / 4: 17.4-17.7 /
+        // 18.3 against 18.6-18.9 / 19.1 with 2); one row: about half the K tiles, rounded up
+        // to an even count (14336x3584: 8 waves 16.2 us, 7 waves 16.8)
         const int64_t half = std::max<int64_t>(2, tc / 2);
-        waves = bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, half + (half & 1)));
+        waves = bl >= 3 ? 1 : bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, half + (half & 1)));
     } else {
         // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1
         // and 3 at B = 2..4 (B = 4: 154 us against 209 with 6); rows over

@@ -215,7 +215,10 @@ def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_a
         tr = tile_rows(output_rows)
         out = []
         for waves in (1, 2, 3, 4, 6, 8, 12):
-            for p in sorted({b for b in RX_BLOCK_CANDIDATES if b <= tr} | {-(-tr // waves)}):
+            # every candidate block count up to the tile rows, the tile rows
+            # themselves (one row slot per block holds them all: the default
+            # where they are fewer than the CUs) and one row per slot
+            for p in sorted({b for b in RX_BLOCK_CANDIDATES if b <= tr} | {tr, -(-tr // waves)}):
                 out.append(rx_configuration(waves, p))
         return tuple(out)
     mfma = uses_mfma(batch, float32_activations)

@@ -530,11 +530,30 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // Since its waits and launch were refitted it beats the x-slab kernel at 5-8
 // rows too (default launches, cold: 9216x4096 B = 5 18.5 against 21.0 us,
 // 2304x2304 8.5 against 10.2, 3584x14336 22.6 against 24.3, 14336x3584 B = 8
-// 20.3 against 20.4).
+// 20.3 against 20.4). With 17..32 rows whose x does not fit but 16 rows do
+// (K = 3584..4608), on matrices of at most one tile row per CU, LDS holds the
+// first 16 rows and batch group 1's operands come from global memory
+// (4096x3584 B = 24 / 32: 13.6 / 14.7 us against the x-slab kernel's 18.8 /
+// 19.5; 3584x4096 B = 20 / 32: 13.6 / 15.9 against 19.1 / 20.2; on taller
+// matrices it lost at 32 rows: 14336x3584 33.5 against 27.3, 36864x4608 85.2
+// against 80.5). Returns the rows of x the kernel keeps in LDS, 0 where the
+// x-slab kernel serves the launch.
+static int32_t rx_staged_rows(se12_handle* const* hs, int32_t count, int32_t batch) {
+    int64_t rows = 0;
+    for (int32_t i = 0; i < count; ++i) {
+        if (hs[i]->N % SE12_TILE_ROWS != 0) return 0;
+        rows += hs[i]->TR;
+    }
+    const int64_t lds = hs[0]->lds_per_block;
+    if ((int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= lds) return batch;
+    if (batch > 16 && (int64_t)(rx_lds_bytes(hs[0]->K, 16) + kLutBytes) <= lds &&
+        rows <= std::max<int32_t>(1, hs[0]->cu_count))
+        return 16;
+    return 0;
+}
+
 static bool rx_fits(se12_handle* const* hs, int32_t count, int32_t batch) {
-    for (int32_t i = 0; i < count; ++i)
-        if (hs[i]->N % SE12_TILE_ROWS != 0) return false;
-    return (int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= hs[0]->lds_per_block;
+    return rx_staged_rows(hs, count, batch) > 0;
 }
 
 static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
@@ -563,19 +582,22 @@ static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t bat
     const bool tall = rows >= 16 * cus;
     const int64_t per_matrix =
         std::max<int64_t>(1, std::min<int64_t>(rx_max_blocks(hs, count), ceil_div((tall ? 2 : 1) * cus, count)));
-    *waves_out = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
+    int32_t waves = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
+    if (rx_staged_rows(hs, count, batch) < batch) waves = std::min(waves, kRxMaxThreadsXG / 64);
+    *waves_out = waves;
     *blocks_out = (int32_t)(per_matrix * count);
 }
 
-static GemvPlan plan_rx(bool raw, int32_t batch, int32_t waves, int32_t blocks, int64_t k, size_t lds) {
+static GemvPlan plan_rx(bool raw, int32_t batch, int32_t staged, int32_t waves, int32_t blocks, int64_t k, size_t lds) {
     GemvPlan p{};
     p.batch = batch;
     p.raw = raw;
     p.waves = waves;
     p.blocks = blocks;
-    p.lds = std::max(lds, rx_lds_bytes(k, batch));
+    p.lds = std::max(lds, rx_lds_bytes(k, staged));
     p.g = 1;
     p.pf = 1;
+    p.xg = staged < batch ? 1 : 0;
     return p;
 }
 
@@ -618,7 +640,9 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     for (int32_t i = 0; i < count; ++i)
         generic = generic || (raw && (hs[i]->N % SE12_TILE_ROWS != 0 || !aligned16(hs[i]->wraw)));
     const bool mfma = uses_mfma(batch, xf32);
-    const bool rx = mfma && !generic && rx_fits(hs, count, batch);
+    const int32_t rx_rows = mfma && !generic ? rx_staged_rows(hs, count, batch) : 0;  // x rows in LDS
+    const bool rx = rx_rows > 0;
+    const int rx_max_threads = rx_rows < batch ? kRxMaxThreadsXG : kRxMaxThreads;
     const int32_t step = mfma ? batch : kGemvMaxBatchPerLaunch;
     const int32_t b_first = std::min<int32_t>(batch, step);
     int32_t waves, splits;
@@ -627,10 +651,10 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     if (rx) {
         splits = 1;
         if (launch) {
-            if (launch->threads_per_block < 64 || launch->threads_per_block > kRxMaxThreads ||
+            if (launch->threads_per_block < 64 || launch->threads_per_block > rx_max_threads ||
                 launch->threads_per_block % 64 != 0)
                 return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d",
-                            fn, launch->threads_per_block, kRxMaxThreads, batch);
+                            fn, launch->threads_per_block, rx_max_threads, batch);
             if (launch->blocks <= 0 || launch->blocks % count != 0 || launch->blocks / count > rx_max_blocks(hs, count))
                 return fail(SE12_E_INVALID, "%s: blocks %d must be %d x 1..%lld (blocks per matrix, at most its tile "
                             "rows)", fn, launch->blocks, count, (long long)rx_max_blocks(hs, count));
@@ -740,13 +764,13 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.TR = h->TR;
             a.TC = h->TC;
             a.S = rx ? rx_kgroups(h->TR, h->TC, waves, rx_blocks / count) : splits;
-            rx_lds = std::max(rx_lds, rx ? rx_lds_total(h->K, bl, waves, a.S) : 0);
+            rx_lds = std::max(rx_lds, rx ? rx_lds_total(h->K, rx_rows, bl, waves, a.S) : 0);
             g.tr_start[i] = start;
             start += mfma ? (int32_t)ceil_div(h->TR, gemm_min_waves(bl)) : h->TR;
         }
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);
-        GemvPlan p = rx     ? plan_rx(raw, bl, waves, rx_blocks, h0->K, rx_lds)
+        GemvPlan p = rx     ? plan_rx(raw, bl, rx_rows, waves, rx_blocks, h0->K, rx_lds)
                      : mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
                             : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
         if (fuse_pro) {

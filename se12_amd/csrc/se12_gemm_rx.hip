@@ -38,6 +38,11 @@
 // Batch rows past the batch in a 16-row group read row 0: MFMA output
 // column n depends on B column n only, and those columns are not stored.
 //
+// Where only 16 rows of x fit (17..32 rows at K = 3584..4608), LDS holds
+// rows 0..15 and each ring slot also loads batch group 1's B operands from
+// global memory (x stays in L2): 8 more 16-byte loads per lane per tile, 32
+// more VGPRs per slot, so at most 2 waves per SIMD (XG).
+//
 // FAST only: K % 256 == 0, 16-byte aligned x rows, and for the raw twin
 // N % 16 == 0 and an aligned W (the other cases run se12_gemm.hip).
 #include "se12_device.hpp"
@@ -52,11 +57,12 @@ namespace {
 
 // One tile's loads: sm / ec in the block layout once transposed (below), or
 // raw BF16 column blocks for the twin; the side record of the tile.
-template <bool RAW>
+template <bool RAW, bool XG>
 struct RxTile {
     TileSide side;
     TileLoads t;
     uint4 r[RAW ? 4 : 1][2];
+    uint4 xg[XG ? 8 : 1];  // batch group 1's B operands (x from global memory)
 };
 
 // Part p of a tile's sm (ec) is its contiguous kilobyte (512 bytes) of rows
@@ -88,9 +94,10 @@ __device__ __forceinline__ int rx_piece(int b, int q, int pieces_per_row) {
     return (b * pieces_per_row + (q ^ (b & 7))) * 16;
 }
 
-template <int BG, bool RAW>
-__global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3))) void gemm_rx_kernel(
-    GemvGroupArgs ga, int batch) {
+template <int BG, bool RAW, bool XG>
+__global__ __launch_bounds__(XG ? kRxMaxThreadsXG : kRxMaxThreads)
+__attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupArgs ga, int batch) {
+    static_assert(!XG || BG == 2, "x from global memory serves batch group 1");
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) char xs[];
     const GemvArgs a = ga.m[blockIdx.z];
@@ -135,12 +142,22 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
         if (n.r < rows) c = n;
     };
     auto row_of = [&](const Cursor& c) { return j0 + c.r * nw; };
-    auto load = [&](RxTile<RAW>& t, const Cursor& c) {
+    // batch group 1's x row of this lane when x comes from global memory
+    // (rows past the batch read the last row; their outputs are not stored)
+    const int xg_row = min(16 + (int)(lane & 15u), batch - 1);
+    auto load = [&](RxTile<RAW, XG>& t, const Cursor& c) {
         const int tr = row_of(c), kt = c.kt;
         if constexpr (RAW) {
             rx_load_raw_blocks(t.r, a.wraw, a.K, tr, kt, lane);
         } else {
             load_tile_block_order(t.t, t.side, a.sm, a.ec, a.side, (int64_t)tr * TC + kt, lane);
+        }
+        if constexpr (XG) {
+            // pieces 2 p + h (8 columns each) of this lane's 32-column slice
+            const uint4* xr = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + (int64_t)xg_row * a.K) +
+                              32 * kt + 8 * (int)(lane >> 4);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) t.xg[i] = xr[i];
         }
     };
 
@@ -151,9 +168,9 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
     // are inline asm, which the compiler's wait counting does not see: with
     // its own direct-to-LDS loads it waits for every load in flight (vmcnt(0))
     // at each step of the ring below, the other slot's included.
-    RxTile<RAW> ring[kRxDepth];
+    RxTile<RAW, XG> ring[kRxDepth];
     Cursor ld{0, kb};
-    constexpr int kLoadsPerTile = RAW ? 8 : 9;
+    constexpr int kLoadsPerTile = (RAW ? 8 : 9) + (XG ? 8 : 0);
     if (n_tiles > 0) {
 #pragma unroll
         for (int d = 0; d < kRxDepth; ++d) {
@@ -162,7 +179,7 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
         }
     }
     {
-        const int total = batch * ppr;                         // pieces of x
+        const int total = (XG ? 16 : batch) * ppr;             // pieces of x in LDS
         const int rounds = (total + threads - 1) / threads;
         const uint16_t* x = static_cast<const uint16_t*>(a.x);
         // block b starts at round b mod rounds, so that the blocks, which all
@@ -229,7 +246,7 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
     // 16) + p) .. + 15 of row l % 16, as 8 BF16 pairs; its first and second
     // 8 columns are the A operands of two MFMAs, whose B operands are the x
     // pieces (8 columns) 2 (4 (l / 16) + p) and the next
-    auto mfma_part = [&](const uint32_t wv[8], int kt, int p) {
+    auto mfma_part = [&](const uint32_t wv[8], int kt, int p, const uint4* xg) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const rx_bf16x8_t av =
@@ -237,19 +254,20 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
             const int q = 32 * kt + 8 * (int)(lane >> 4) + 2 * p + h;
 #pragma unroll
             for (int g = 0; g < BG; ++g) {
-                const uint4 bv = *reinterpret_cast<const uint4*>(xs + rx_piece(xrow[g], q, ppr));
+                const uint4 bv =
+                    (XG && g == 1) ? xg[2 * p + h] : *reinterpret_cast<const uint4*>(xs + rx_piece(xrow[g], q, ppr));
                 acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(rx_bf16x8_t, bv), acc[g], 0, 0, 0);
             }
         }
     };
-    auto use = [&](RxTile<RAW>& t, const Cursor& c) {
+    auto use = [&](RxTile<RAW, XG>& t, const Cursor& c) {
         const int kt = c.kt;
         if constexpr (RAW) {
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const uint32_t wv[8] = {t.r[p][0].x, t.r[p][0].y, t.r[p][0].z, t.r[p][0].w,
                                         t.r[p][1].x, t.r[p][1].y, t.r[p][1].z, t.r[p][1].w};
-                mfma_part(wv, kt, p);
+                mfma_part(wv, kt, p, t.xg);
             }
         } else {
             const uint32_t info = side_info(t.side, 0);
@@ -260,7 +278,7 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
                 for (int p = 0; p < 4; ++p) rx_raw_part(raw, p, lane, wv[p]);
                 wait_vector_loads();  // rare path: keeps the common path's waits exact
 #pragma unroll
-                for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p);
+                for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p, t.xg);
             } else {
                 chunks_to_blocks(t.t);  // in place: the slot is reloaded next
                 // each part's patterns merged with its sm bytes as soon as
@@ -275,7 +293,7 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
                 }
                 patch_tile_escapes<kBlockLayout>(wv, info, t.side, 0, lane);
 #pragma unroll
-                for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p);
+                for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p, t.xg);
             }
         }
         // the row's last K tile of this wave: with one K group the row is
@@ -295,12 +313,12 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
     // loads in flight, the other slot's included).
     static_assert(kRxDepth == 2, "the ring below has two slots");
     Cursor cu{0, kb};
-    auto step = [&](RxTile<RAW>& t) {
+    auto step = [&](RxTile<RAW, XG>& t) {
         use(t, cu);
         advance(cu);
         __builtin_amdgcn_sched_barrier(0);  // no work of the next step above this one's
     };
-    auto step_reload = [&](RxTile<RAW>& t) {
+    auto step_reload = [&](RxTile<RAW, XG>& t) {
         step(t);
         // the slot's next loads after its use: hoisted above it, they would
         // hold a third tile's registers
@@ -352,10 +370,10 @@ __global__ __launch_bounds__(kRxMaxThreads) __attribute__((amdgpu_waves_per_eu(3
 
 namespace {
 
-template <int BG, bool RAW>
+template <int BG, bool RAW, bool XG = false>
 hipError_t rx_go(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
     const dim3 grid(p.blocks / a.count, 1, a.count), block(p.waves * 64);
-    hipLaunchKernelGGL((gemm_rx_kernel<BG, RAW>), grid, block, p.lds, stream, a, batch);
+    hipLaunchKernelGGL((gemm_rx_kernel<BG, RAW, XG>), grid, block, p.lds, stream, a, batch);
     return hipGetLastError();
 }
 
@@ -366,6 +384,10 @@ hipError_t launch_gemm_rx(const GemvGroupArgs& a, int batch, const GemvPlan& p, 
         return hipErrorInvalidValue;
     for (int i = 0; i < a.count; ++i)
         if (a.m[i].S < 1 || p.waves % a.m[i].S != 0) return hipErrorInvalidValue;
+    if (p.xg) {
+        if (batch <= 16 || p.waves * 64 > kRxMaxThreadsXG) return hipErrorInvalidValue;
+        return p.raw ? rx_go<2, true, true>(a, batch, p, stream) : rx_go<2, false, true>(a, batch, p, stream);
+    }
     if (batch > 16) return p.raw ? rx_go<2, true>(a, batch, p, stream) : rx_go<2, false>(a, batch, p, stream);
     return p.raw ? rx_go<1, true>(a, batch, p, stream) : rx_go<1, false>(a, batch, p, stream);
 }

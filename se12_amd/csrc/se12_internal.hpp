@@ -129,6 +129,7 @@ struct GemvPlan {
     int waves;
     int blocks;
     size_t lds;
+    int xg;  // resident-x kernel: batch group 1's x from global memory (0 / 1)
 };
 
 struct DecodeArgs {
@@ -240,6 +241,8 @@ hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hip
 // (rx_kgroups). kRxDepth tiles in flight per wave, up to 3 waves per SIMD
 // (168 VGPRs: the decode, a tile in flight and the transposed tile in use).
 constexpr int kRxMaxThreads = 768;
+// with batch group 1's x from global memory: 2 waves per SIMD (210 VGPRs)
+constexpr int kRxMaxThreadsXG = 512;
 constexpr int kRxDepth = 2;
 // K groups of the resident-x kernel for one matrix: the largest power of two
 // that divides the waves per block, leaves each group at least two K tiles,
@@ -254,9 +257,10 @@ constexpr size_t rx_lds_bytes(int64_t k, int batch) {
 }
 // dynamic LDS: x, or (the same memory, after the main loop) the K groups'
 // sums, whichever is larger
-constexpr size_t rx_lds_total(int64_t k, int batch, int waves, int kgroups) {
+// (staged = the rows of x held in LDS: all of the batch, or 16)
+constexpr size_t rx_lds_total(int64_t k, int staged, int batch, int waves, int kgroups) {
     const size_t sums = kgroups > 1 ? (size_t)(waves - waves / kgroups) * (batch > 16 ? 2 : 1) * 1024 : 0;
-    return rx_lds_bytes(k, batch) > sums ? rx_lds_bytes(k, batch) : sums;
+    return rx_lds_bytes(k, staged) > sums ? rx_lds_bytes(k, staged) : sums;
 }
 hipError_t launch_gemm_rx(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream, int cu_count);

@@ -32,10 +32,15 @@ MFMA_MAX_WAVES = 8
 MFMA_MAX_WAVES_GENERIC = 4   # the edge-handling MFMA variants (K % 256 != 0 or unaligned x)
 # The resident-x MFMA kernel: every MFMA batch (MFMA_MIN_BATCH BF16 rows or
 # more) on FAST shapes whose x (batch x K BF16, in whole 1 KiB loads) fits a
-# block's LDS (gfx950: 160 KiB) beside the 1 KiB pair table. Its launch is
-# (waves per block 1..12, blocks per matrix 1..tile rows); the launch fixes
-# the K groups (rx_kgroups) and with them the order of every sum.
+# block's LDS (gfx950: 160 KiB) beside the 1 KiB pair table; and 17..32 rows
+# whose first 16 fit, on matrices of at most one tile row per CU (batch group
+# 1's x then comes from global memory, at most RX_MAX_WAVES_XG waves per
+# block). Its launch is (waves per block 1..12, blocks per matrix 1..tile
+# rows); the launch fixes the K groups (rx_kgroups) and with them the order of
+# every sum.
 RX_MAX_WAVES = 12
+RX_MAX_WAVES_XG = 8
+COMPUTE_UNITS = 256  # MI355X; the library uses the device's count
 LDS_PER_BLOCK = 160 * 1024
 LUT_BYTES = 1024
 RX_BLOCK_CANDIDATES = (32, 64, 128, 192, 256, 384, 512, 768, 1024)
@@ -87,11 +92,32 @@ def rx_lds_bytes(k: int, batch: int) -> int:
     return -(-(batch * (k // 8)) // 64) * 64 * 16
 
 
-def uses_rx(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True) -> bool:
+def rx_staged_rows(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
+                   compute_units: int = COMPUTE_UNITS) -> int:
+    """Rows of x the resident-x kernel keeps in LDS (the library's rule): the
+    whole batch where it fits, 16 for 17..32 rows whose first 16 fit on a
+    matrix of at most one tile row per CU, else 0 (the x-slab kernel)."""
+    if not (uses_mfma(batch, float32_activations) and aligned_x
+            and not runs_generic(output_rows, k, float32_activations)):
+        return 0
+    if rx_lds_bytes(k, batch) + LUT_BYTES <= LDS_PER_BLOCK:
+        return batch
+    if batch > 16 and rx_lds_bytes(k, 16) + LUT_BYTES <= LDS_PER_BLOCK and tile_rows(output_rows) <= compute_units:
+        return 16
+    return 0
+
+
+def uses_rx(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
+            compute_units: int = COMPUTE_UNITS) -> bool:
     """Whether a launch runs the resident-x MFMA kernel (the library's rule)."""
-    return (uses_mfma(batch, float32_activations) and aligned_x
-            and not runs_generic(output_rows, k, float32_activations)
-            and rx_lds_bytes(k, batch) + LUT_BYTES <= LDS_PER_BLOCK)
+    return rx_staged_rows(output_rows, k, batch, float32_activations, aligned_x, compute_units) > 0
+
+
+def rx_max_waves(output_rows: int, k: int, batch: int, compute_units: int = COMPUTE_UNITS) -> int:
+    """Waves per block of the resident-x kernel: 12, or 8 where batch group
+    1's x comes from global memory."""
+    staged = rx_staged_rows(output_rows, k, batch, compute_units=compute_units)
+    return RX_MAX_WAVES_XG if 0 < staged < batch else RX_MAX_WAVES
 
 
 def rx_kgroups(output_rows: int, k: int, waves: int, blocks_per_matrix: int) -> int:
@@ -156,8 +182,9 @@ def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int =
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
     if k is not None and uses_rx(output_rows, k, batch, float32_activations):
-        if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= WAVE_SIZE * RX_MAX_WAVES:
-            raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {WAVE_SIZE * RX_MAX_WAVES}]")
+        mw = rx_max_waves(output_rows, k, batch)
+        if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= WAVE_SIZE * mw:
+            raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {WAVE_SIZE * mw}]")
         if not 1 <= blocks <= tile_rows(output_rows):
             raise ValueError(f"blocks {blocks} must be in [1, {tile_rows(output_rows)}]")
         return tpb // WAVE_SIZE, blocks
@@ -192,7 +219,7 @@ def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 
     if blocks <= 0 or blocks * (tpb // 32) < output_rows * batch:
         raise ValueError(f"{blocks} blocks of {tpb // 32} warps do not cover {output_rows} rows x batch {batch}")
     if uses_rx(output_rows, k, batch, float32_activations, aligned_x):
-        waves = min(-(-tpb // WAVE_SIZE), RX_MAX_WAVES)
+        waves = min(-(-tpb // WAVE_SIZE), rx_max_waves(output_rows, k, batch))
         return rx_configuration(waves, -(-tile_rows(output_rows) // waves))
     mfma = uses_mfma(batch, float32_activations)
     generic = runs_generic(output_rows, k, float32_activations) or not aligned_x
@@ -214,7 +241,7 @@ def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_a
     if uses_rx(output_rows, k, batch, float32_activations):
         tr = tile_rows(output_rows)
         out = []
-        for waves in (1, 2, 3, 4, 6, 8, 12):
+        for waves in (w for w in (1, 2, 3, 4, 6, 8, 12) if w <= rx_max_waves(output_rows, k, batch)):
             # every candidate block count up to the tile rows, the tile rows
             # themselves (one row slot per block holds them all: the default
             # where they are fewer than the CUs) and one row per slot

@@ -85,9 +85,10 @@ def test_reference_launches_translate_to_valid_configurations(rows, k, batch):
             cfg = launch.from_reference_configuration(ref, rows, k, batch, float32_activations=f32)
             waves, splits = launch.waves_and_splits(cfg, rows, batch, k, float32_activations=f32)
             if launch.uses_rx(rows, k, batch, f32):
-                # the resident-x kernel: the block's threads (at most 12 waves),
-                # one tile row per wave slot; it never splits K
-                assert waves == min(-(-ref.threads_per_block.value // 64), launch.RX_MAX_WAVES)
+                # the resident-x kernel: the block's threads (at most 12 waves,
+                # 8 with batch group 1's x from global memory), one tile row
+                # per wave slot; it never splits K
+                assert waves == min(-(-ref.threads_per_block.value // 64), launch.rx_max_waves(rows, k, batch))
                 assert splits == -(-launch.tile_rows(rows) // waves)
                 continue
             assert splits == 1

@@ -95,6 +95,46 @@ def test_gate_9b_batch_sweep_default_launch(gpu, gate_9b, batch):
     assert torch.equal(y, yr)
 
 
+def test_q_9b_wide_batches_x_partly_from_global(gpu):
+    """Gemma-2-9B q_proj 4096x3584 at 20..32 batch rows: x no longer fits a
+    block's LDS from 23 rows, so the resident-x kernel keeps rows 0..15 there
+    and loads batch group 1's operands from global memory (at most 8 waves
+    per block). Against the oracle; the raw twin bit-identical under the
+    default and under other launch shapes; 12 waves are refused."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+    from se12_amd.launch import rx_configuration, rx_max_waves, rx_staged_rows
+
+    rows, cols = 4096, 3584
+    bits = o.normal_bf16(rows, cols, seed=7, std=0.02)
+    w = bf16_tensor(bits, gpu)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    fused, raw = Se12MatVecKernel(encode_on_device(w)), RawBf16MatVecKernel(w)
+    batches = (20, 23, 24, 31, 32)
+    xs = {b: o.normal_bf16(b, cols, seed=2000 + b, std=1.0) for b in batches}
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(np.concatenate([xs[b] for b in batches])))
+    r0 = 0
+    for b in batches:
+        assert rx_staged_rows(rows, cols, b) == (b if b <= 22 else 16)
+        x = bf16_tensor(xs[b], gpu)
+        y = fused.multiply(x)
+        yr = raw.multiply(x)
+        torch.cuda.synchronize()
+        assert max_rel_error(y, ref[r0:r0 + b]) <= REL_TOL, b
+        assert torch.equal(y, yr), b
+        for waves, blocks in ((8, 256), (4, 128), (6, 97)):
+            cfg = rx_configuration(waves, blocks)
+            yl, ylr = fused.multiply(x, launch=cfg), raw.multiply(x, launch=cfg)
+            torch.cuda.synchronize()
+            assert max_rel_error(yl, ref[r0:r0 + b]) <= REL_TOL, (b, waves, blocks)
+            assert torch.equal(yl, ylr), (b, waves, blocks)
+        if rx_max_waves(rows, cols, b) == 8:
+            from se12_amd._native import Se12Error
+
+            with pytest.raises(Se12Error, match="threads_per_block 768"):
+                fused.multiply(x, launch=rx_configuration(12, 256))
+        r0 += b
+
+
 def test_down_27b_heavy_tailed_full_size(gpu):
     from se12_amd.hip import HipSe12WeightDecoder, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
 

@@ -135,6 +135,15 @@ def test_launch_candidates_respect_each_kernels_limits():
     assert uses_rx(2304, 2304, 9) and not uses_rx(2304, 9216, 9) and not uses_rx(2304, 2304, 9, float32_activations=True)
     assert uses_rx(2304, 9216, 6) and uses_rx(4096, 14336, 5) and not uses_rx(4096, 14336, 6) and uses_rx(256000, 2304, 5)
     assert uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and not uses_rx(14336, 3584, 24)
+    # 17..32 rows whose first 16 fit, on at most one tile row per CU: 16 rows
+    # in LDS, batch group 1 from global memory, at most 8 waves
+    from se12_amd.launch import rx_max_waves, rx_staged_rows
+
+    assert rx_staged_rows(4096, 3584, 32) == 16 and rx_staged_rows(4096, 3584, 16) == 16
+    assert rx_staged_rows(4096, 3584, 24) == 16 and rx_staged_rows(4096, 2304, 32) == 32
+    assert rx_staged_rows(4112, 3584, 32) == 0 and rx_staged_rows(4096, 14336, 17) == 0
+    assert rx_staged_rows(4096, 3584, 32, compute_units=128) == 0
+    assert rx_max_waves(4096, 3584, 32) == 8 and rx_max_waves(4096, 3584, 16) == 12 and rx_max_waves(14336, 3584, 16) == 12
     assert not uses_rx(2304, 2300, 9) and not uses_rx(2300, 2304, 9) and not uses_rx(256000, 2304, 4)
     assert rx_lds_bytes(9216, 6) == 6 * 1152 * 16 and rx_lds_bytes(2304, 5) == 1472 * 16
     pairs = [waves_and_splits(c, 2304, batch=9, k=2304) for c in candidate_configurations(2304, 2304, batch=9)]

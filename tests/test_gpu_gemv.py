@@ -323,6 +323,43 @@ def test_grouped_launch_equals_separate_launches(gpu):
                 assert torch.equal(yr, y), (batch, waves, splits)
 
 
+def test_grouped_launch_with_x_partly_from_global(gpu):
+    """q/k/v-like matrices at K = 3584 and 23..32 batch rows: x fits a block's
+    LDS only up to 22 rows and the group has at most one tile row per CU, so
+    the grouped launch keeps rows 0..15 of x in LDS and loads batch group 1's
+    operands from global memory. Within the tolerance of the oracle; the raw
+    twin bit-identical; each matrix bit-identical to its own launch under the
+    same waves and K groups."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped
+    from se12_amd.launch import rx_configuration, rx_kgroups, rx_staged_rows
+
+    cols = 3584
+    shapes = [(1024, cols), (512, cols), (512, cols)]
+    bits = [heavy_tailed_bf16(r, c, seed=70 + i) for i, (r, c) in enumerate(shapes)]
+    encs = [o.encode(b.reshape(-1), r, c) for b, (r, c) in zip(bits, shapes)]
+    kerns = [Se12MatVecKernel(to_device(e, gpu), max_batch=32) for e in encs]
+    raws = [RawBf16MatVecKernel(bf16_tensor(b, gpu), max_batch=32) for b in bits]
+    total_rows = sum(r for r, _ in shapes)
+    for batch in (23, 24, 32):
+        assert rx_staged_rows(total_rows, cols, batch) == 16
+        xb = _x(batch, cols, seed=80 + batch)
+        x = bf16_tensor(xb, gpu)
+        refs = [o.gemv_reference(e, o.bf16_bits_to_f32(xb)) for e in encs]
+        ys, ysr = multiply_grouped(kerns, x), multiply_grouped(raws, x)
+        for y, yr, ref in zip(ys, ysr, refs):
+            assert max_rel_error(y, ref) <= REL_TOL, batch
+            assert torch.equal(y, yr), batch
+        for waves, per in ((8, 64), (4, 32), (6, 21)):
+            ys = multiply_grouped(kerns, x, launch=rx_configuration(waves, per, len(shapes)))
+            ysr = multiply_grouped(raws, x, launch=rx_configuration(waves, per, len(shapes)))
+            for k, y, yr, (rows, _), ref in zip(kerns, ys, ysr, shapes, refs):
+                tr = rows // 16
+                assert rx_kgroups(rows, cols, waves, per) == rx_kgroups(rows, cols, waves, min(per, tr))
+                assert torch.equal(y, k.multiply(x, launch=rx_configuration(waves, min(per, tr)))), (batch, waves, per)
+                assert torch.equal(yr, y), (batch, waves, per)
+                assert max_rel_error(y, ref) <= REL_TOL, (batch, waves, per)
+
+
 def test_grouped_launch_rejects_mixed_groups(gpu):
     from se12_amd import _native as nat
     from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped

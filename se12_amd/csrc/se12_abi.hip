@@ -536,20 +536,42 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // (4096x3584 B = 24 / 32: 13.6 / 14.7 us against the x-slab kernel's 18.8 /
 // 19.5; 3584x4096 B = 20 / 32: 13.6 / 15.9 against 19.1 / 20.2; on taller
 // matrices it lost at 32 rows: 14336x3584 33.5 against 27.3, 36864x4608 85.2
-// against 80.5). Returns the rows of x the kernel keeps in LDS, 0 where the
-// x-slab kernel serves the launch.
-static int32_t rx_staged_rows(se12_handle* const* hs, int32_t count, int32_t batch) {
+// against 80.5). Otherwise the launch is split along K: split s of S takes
+// K tiles [s TC / S, (s + 1) TC / S) of every row and holds only their
+// columns of x, with the fewest splits (at most kGemmMaxSplits) whose share
+// fits; the splits' partial sums meet per row through device memory.
+// `staged` = the rows of x the kernel keeps in LDS, `splits` = K splits;
+// staged 0 where the x-slab kernel serves the launch.
+struct RxLayout {
+    int32_t staged, splits;
+};
+
+static RxLayout rx_layout(se12_handle* const* hs, int32_t count, int32_t batch) {
     int64_t rows = 0;
     for (int32_t i = 0; i < count; ++i) {
-        if (hs[i]->N % SE12_TILE_ROWS != 0) return 0;
+        if (hs[i]->N % SE12_TILE_ROWS != 0) return {0, 0};
         rows += hs[i]->TR;
     }
     const int64_t lds = hs[0]->lds_per_block;
-    if ((int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= lds) return batch;
+    if ((int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= lds) return {batch, 1};
     if (batch > 16 && (int64_t)(rx_lds_bytes(hs[0]->K, 16) + kLutBytes) <= lds &&
         rows <= std::max<int32_t>(1, hs[0]->cu_count))
-        return 16;
-    return 0;
+        return {16, 1};
+    const int32_t tc = hs[0]->TC;
+    int32_t sp = 2;
+    while (sp <= std::min<int32_t>(kRxMaxSplits, tc) &&
+           (int64_t)(rx_lds_bytes(ceil_div(tc, sp) * SE12_TILE_COLS, batch) + kLutBytes) > lds)
+        ++sp;
+    if (sp > std::min<int32_t>(kRxMaxSplits, tc)) return {0, 0};
+    // what measured faster than the x-slab kernel: single matrices, and two
+    // splits only on long launches of two batch groups (the cross-block
+    // sums' round trips end every wave)
+    if (count > 1 || (sp == 2 && (batch <= 16 || rows * tc < 16384))) return {0, 0};
+    return {batch, sp};
+}
+
+static int32_t rx_staged_rows(se12_handle* const* hs, int32_t count, int32_t batch) {
+    return rx_layout(hs, count, batch).staged;
 }
 
 static bool rx_fits(se12_handle* const* hs, int32_t count, int32_t batch) {
@@ -577,25 +599,34 @@ static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
 static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
                               int32_t* blocks_out) {
     const int64_t cus = std::max<int32_t>(1, hs[0]->cu_count);
+    const RxLayout lay = rx_layout(hs, count, batch);
+    const int32_t sp = std::max<int32_t>(1, lay.splits);
+    // with K splits each split's blocks cover every row: rows per block as
+    // if the matrix had `splits` times its rows
     int64_t rows = 0;
-    for (int32_t i = 0; i < count; ++i) rows += hs[i]->TR;
+    for (int32_t i = 0; i < count; ++i) rows += hs[i]->TR * sp;
     const bool tall = rows >= 16 * cus;
-    const int64_t per_matrix =
-        std::max<int64_t>(1, std::min<int64_t>(rx_max_blocks(hs, count), ceil_div((tall ? 2 : 1) * cus, count)));
+    // a split launch takes at most one block per CU (each holds most of
+    // the LDS: a second block per CU would run after the first)
+    const int64_t per_matrix = std::max<int64_t>(
+        1, std::min<int64_t>(rx_max_blocks(hs, count),
+                             sp > 1 ? cus / ((int64_t)count * sp) : ceil_div((tall ? 2 : 1) * cus, count)));
     int32_t waves = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
     // at most one tile row per row slot where the rows allow it: a grouped
     // launch gives each matrix only its share of the blocks (9B gate/up, 2 x
     // 14336x3584, 128 blocks each, B = 8 / 16: 33.0 / 34.3 us with 8 waves
     // against 40.9 / 41.1 with 6)
-    if (!tall)
+    if (!tall && sp == 1)
         while (waves < 8 && per_matrix * waves < rx_max_blocks(hs, count)) waves = waves < 6 ? 6 : 8;
-    if (rx_staged_rows(hs, count, batch) < batch) waves = std::min(waves, kRxMaxThreadsXG / 64);
+    if (lay.staged < batch) waves = std::min(waves, kRxMaxThreadsXG / 64);
     *waves_out = waves;
-    *blocks_out = (int32_t)(per_matrix * count);
+    *blocks_out = (int32_t)(per_matrix * sp * count);
 }
 
-static GemvPlan plan_rx(bool raw, int32_t batch, int32_t staged, int32_t waves, int32_t blocks, int64_t k, size_t lds) {
+static GemvPlan plan_rx(bool raw, int32_t batch, int32_t staged, int32_t splits, int32_t waves, int32_t blocks,
+                        int64_t k, size_t lds) {
     GemvPlan p{};
+    p.ksplits = splits;
     p.batch = batch;
     p.raw = raw;
     p.waves = waves;
@@ -646,7 +677,10 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     for (int32_t i = 0; i < count; ++i)
         generic = generic || (raw && (hs[i]->N % SE12_TILE_ROWS != 0 || !aligned16(hs[i]->wraw)));
     const bool mfma = uses_mfma(batch, xf32);
-    const int32_t rx_rows = mfma && !generic ? rx_staged_rows(hs, count, batch) : 0;  // x rows in LDS
+    const RxLayout rx_lay = mfma && !generic ? rx_layout(hs, count, batch) : RxLayout{0, 0};
+    const int32_t rx_rows = rx_lay.staged;  // x rows in LDS
+    const int32_t rx_splits = std::max<int32_t>(1, rx_lay.splits);
+    const int64_t rx_k = ceil_div(h0->TC, rx_splits) * SE12_TILE_COLS;  // x columns a block holds
     const bool rx = rx_rows > 0;
     const int rx_max_threads = rx_rows < batch ? kRxMaxThreadsXG : kRxMaxThreads;
     const int32_t step = mfma ? batch : kGemvMaxBatchPerLaunch;
@@ -655,21 +689,23 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
     int32_t rx_blocks = 0;
     int64_t grid_rows = tr_total;  // grid rows per split: tile rows, or row blocks (MFMA)
     if (rx) {
-        splits = 1;
         if (launch) {
             if (launch->threads_per_block < 64 || launch->threads_per_block > rx_max_threads ||
                 launch->threads_per_block % 64 != 0)
                 return fail(SE12_E_INVALID, "%s: threads_per_block %d must be a multiple of 64 in [64, %d] at batch %d",
                             fn, launch->threads_per_block, rx_max_threads, batch);
-            if (launch->blocks <= 0 || launch->blocks % count != 0 || launch->blocks / count > rx_max_blocks(hs, count))
-                return fail(SE12_E_INVALID, "%s: blocks %d must be %d x 1..%lld (blocks per matrix, at most its tile "
-                            "rows)", fn, launch->blocks, count, (long long)rx_max_blocks(hs, count));
+            if (launch->blocks <= 0 || launch->blocks % (count * rx_splits) != 0 ||
+                launch->blocks / (count * rx_splits) > rx_max_blocks(hs, count))
+                return fail(SE12_E_INVALID, "%s: blocks %d must be %d x 1..%lld (matrices x K splits x blocks per "
+                            "matrix and split, at most its tile rows)", fn, launch->blocks, count * rx_splits,
+                            (long long)rx_max_blocks(hs, count));
             waves = launch->threads_per_block / 64;
             rx_blocks = launch->blocks;
         } else {
             rx_default_launch(hs, count, batch, &waves, &rx_blocks);
         }
-        grid_rows = rx_blocks;
+        splits = rx_splits;
+        grid_rows = rx_blocks / rx_splits;
     } else if (launch) {
         const int max_threads = mfma ? (generic ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
                                      : max_threads_for(b_first, xf32, generic);
@@ -769,14 +805,14 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.Np = h->Np;
             a.TR = h->TR;
             a.TC = h->TC;
-            a.S = rx ? rx_kgroups(h->TR, h->TC, waves, rx_blocks / count) : splits;
-            rx_lds = std::max(rx_lds, rx ? rx_lds_total(h->K, rx_rows, bl, waves, a.S) : 0);
+            a.S = rx ? rx_kgroups(h->TR, h->TC / rx_splits, waves, rx_blocks / (count * rx_splits)) : splits;
+            rx_lds = std::max(rx_lds, rx ? rx_lds_total(rx_k, rx_rows, bl, waves, a.S) : 0);
             g.tr_start[i] = start;
             start += mfma ? (int32_t)ceil_div(h->TR, gemm_min_waves(bl)) : h->TR;
         }
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);
-        GemvPlan p = rx     ? plan_rx(raw, bl, rx_rows, waves, rx_blocks, h0->K, rx_lds)
+        GemvPlan p = rx     ? plan_rx(raw, bl, rx_rows, rx_splits, waves, rx_blocks, rx_k, rx_lds)
                      : mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
                             : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
         if (fuse_pro) {

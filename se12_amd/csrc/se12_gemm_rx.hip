@@ -43,6 +43,14 @@
 // global memory (x stays in L2): 8 more 16-byte loads per lane per tile, 32
 // more VGPRs per slot, so at most 2 waves per SIMD (XG).
 //
+// Where x fits neither way, the launch splits K (grid y = S splits): split s
+// takes K tiles [s TC / S, (s + 1) TC / S) of every row and its blocks hold
+// only those columns of x. A row's sum over a split goes to the partial sums
+// [S][batch][Np] with device-scope stores as the row ends; at its end the
+// wave waits for those stores and arrives on each of its rows' counters (one
+// lane per row); the last of a row's S arrivals adds the partial sums in
+// ascending split order, stores the row and resets the counter.
+//
 // FAST only: K % 256 == 0, 16-byte aligned x rows, and for the raw twin
 // N % 16 == 0 and an aligned W (the other cases run se12_gemm.hip).
 #include "se12_device.hpp"
@@ -111,14 +119,18 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
     // K groups: the host sets KG (in S) so that it divides W, every wave has
     // K tiles, and with KG > 1 every row slot holds at most one row
     const int KG = a.S;
+    // K splits (grid y): split s takes K tiles [kb0, ke0) of every row and
+    // holds only their columns of x
+    const int S = (int)gridDim.y, s = (int)blockIdx.y;
+    const int kb0 = (int)((int64_t)s * TC / S), ke0 = (int)((int64_t)(s + 1) * TC / S);
     const int RW = W / KG;                                     // row slots per block
     const int kg = w / RW, rw = w - kg * RW;
     const int nw = (int)gridDim.x * RW;                        // row slots of this matrix
     const int j0 = rw * (int)gridDim.x + (int)blockIdx.x;      // this slot's first row
     const int rows = a.TR > j0 ? (a.TR - 1 - j0) / nw + 1 : 0; // rows j0, j0 + nw, ...
-    const int ppr = (int)(a.K >> 3);                           // 16-byte pieces per x row
+    const int ppr = (ke0 - kb0) * (kTileCols / 8);             // 16-byte pieces per x row in LDS
     // this group's K tiles: kb, kb + ks, ... below ke
-    const int kb = kg, ks = KG, ke = TC;
+    const int kb = kb0 + kg, ks = KG, ke = ke0;
 
     // The wave's tiles in order: its slot's r-th row (j0 + r nw), its K
     // tiles in ascending order. A cursor (r, kt) walks them; the load cursor
@@ -191,7 +203,7 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
                 const int p = min(base + (int)lane, total - 1);  // a lane past the end re-loads the last piece
                 const int b = p / ppr, e = p - b * ppr;
                 const int q = e ^ (b & 7);                       // LDS piece p holds x piece q of row b
-                lds_load16(x + (int64_t)b * a.K + 8 * q, lds_address(xs + 16 * base));
+                lds_load16(x + (int64_t)b * a.K + 8 * (q + 32 * kb0), lds_address(xs + 16 * base));
             }
             r = r + 1 == rounds ? 0 : r + 1;
         }
@@ -242,6 +254,67 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
         }
     };
 
+    // With K splits, a row's sum over this split's K tiles goes to the
+    // partial sums [S][batch][Np] (device-scope stores, no wait), in
+    // store_row's lane layout; the wave arrives on its rows' counters at its
+    // end (finish_splits).
+    auto store_partial = [&](int tr) {
+        const int src = (int)((((lane & 3u) << 4) | (lane >> 2)) << 2);
+#pragma unroll
+        for (int g = 0; g < BG; ++g) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[e] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(acc[g][e])));
+            const int b = 16 * g + (int)(lane >> 2);
+            if (b < batch) {
+                float* pp = a.partial + ((int64_t)s * batch + b) * a.Np + (int64_t)tr * kTileRows + 4 * (int)(lane & 3u);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) __hip_atomic_store(pp + e, v[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    };
+    // Once the wave's partial stores have completed, one lane per row arrives
+    // on the row's counter (device scope); the last of the S arrivals adds
+    // the S partial sums in ascending split order, stores the row and resets
+    // the counter for the next launch.
+    auto finish_splits = [&](int n_rows) {
+        wait_vector_loads();
+        for (int r0 = 0; r0 < n_rows; r0 += 64) {
+            const int r = r0 + (int)lane;
+            int old = -1;
+            if (r < n_rows) old = __hip_atomic_fetch_add(&a.counters[j0 + r * nw], 1, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            uint64_t last = __ballot(old == S - 1);
+            while (last) {
+                const int tr = j0 + (r0 + __builtin_ctzll(last)) * nw;
+                last &= last - 1;
+#pragma unroll
+                for (int g = 0; g < BG; ++g) {
+                    const int b = 16 * g + (int)(lane >> 2);
+                    if (b < batch) {
+                        const int64_t n = (int64_t)tr * kTileRows + 4 * (int)(lane & 3u);
+                        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                        for (int ss = 0; ss < S; ++ss) {
+                            const float* pp = a.partial + ((int64_t)ss * batch + b) * a.Np + n;
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                v[e] += __hip_atomic_load(pp + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        }
+                        float* yp = a.y + (int64_t)b * a.N + n;
+                        if (y_vec) {
+                            *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) yp[e] = v[e];
+                        }
+                    }
+                }
+                if (lane == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    };
+
     // part p of a tile in the block layout: lane l holds columns 16 (4 (l /
     // 16) + p) .. + 15 of row l % 16, as 8 BF16 pairs; its first and second
     // 8 columns are the A operands of two MFMAs, whose B operands are the x
@@ -251,7 +324,7 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
         for (int h = 0; h < 2; ++h) {
             const rx_bf16x8_t av =
                 __builtin_bit_cast(rx_bf16x8_t, make_uint4(wv[4 * h], wv[4 * h + 1], wv[4 * h + 2], wv[4 * h + 3]));
-            const int q = 32 * kt + 8 * (int)(lane >> 4) + 2 * p + h;
+            const int q = 32 * (kt - kb0) + 8 * (int)(lane >> 4) + 2 * p + h;
 #pragma unroll
             for (int g = 0; g < BG; ++g) {
                 const uint4 bv =
@@ -299,7 +372,10 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
         // the row's last K tile of this wave: with one K group the row is
         // done; with more, its single row waits for the combine below
         if (KG == 1 && kt + ks >= ke) {
-            store_row(row_of(c));
+            if (S == 1)
+                store_row(row_of(c));
+            else
+                store_partial(row_of(c));
 #pragma unroll
             for (int g = 0; g < BG; ++g) acc[g] = rx_floatx4_t{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -347,7 +423,10 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
         if (left >= 2) step(ring[1]);
         if (left == 3) step(ring[0]);
     }
-    if (KG == 1) return;
+    if (KG == 1) {
+        if (S > 1 && rows > 0) finish_splits(rows);
+        return;
+    }
     // K groups: every wave is past its last MFMA (x is no longer read), the
     // groups 1.. of each slot leave their sums in LDS over x, and group 0
     // adds them in ascending group order and stores the row
@@ -365,14 +444,19 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
     for (int k = 1; k < KG; ++k)
 #pragma unroll
         for (int g = 0; g < BG; ++g) acc[g] += part[(((k - 1) * RW + rw) * 64 + (int)lane) * BG + g];
-    store_row(j0);
+    if (S == 1) {
+        store_row(j0);
+        return;
+    }
+    store_partial(j0);
+    finish_splits(1);
 }
 
 namespace {
 
 template <int BG, bool RAW, bool XG = false>
 hipError_t rx_go(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
-    const dim3 grid(p.blocks / a.count, 1, a.count), block(p.waves * 64);
+    const dim3 grid(p.blocks / (a.count * p.ksplits), p.ksplits, a.count), block(p.waves * 64);
     hipLaunchKernelGGL((gemm_rx_kernel<BG, RAW, XG>), grid, block, p.lds, stream, a, batch);
     return hipGetLastError();
 }
@@ -380,7 +464,8 @@ hipError_t rx_go(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream
 }  // namespace
 
 hipError_t launch_gemm_rx(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
-    if (batch < 1 || batch > 32 || p.waves < 1 || p.waves * 64 > kRxMaxThreads || p.blocks % a.count != 0)
+    if (batch < 1 || batch > 32 || p.waves < 1 || p.waves * 64 > kRxMaxThreads || p.ksplits < 1 ||
+        p.blocks % (a.count * p.ksplits) != 0 || (p.xg && p.ksplits != 1))
         return hipErrorInvalidValue;
     for (int i = 0; i < a.count; ++i)
         if (a.m[i].S < 1 || p.waves % a.m[i].S != 0) return hipErrorInvalidValue;

@@ -129,7 +129,8 @@ struct GemvPlan {
     int waves;
     int blocks;
     size_t lds;
-    int xg;  // resident-x kernel: batch group 1's x from global memory (0 / 1)
+    int xg;       // resident-x kernel: batch group 1's x from global memory (0 / 1)
+    int ksplits;  // resident-x kernel: K splits (grid y), each holding its columns of x
 };
 
 struct DecodeArgs {
@@ -244,6 +245,9 @@ constexpr int kRxMaxThreads = 768;
 // with batch group 1's x from global memory: 2 waves per SIMD (210 VGPRs)
 constexpr int kRxMaxThreadsXG = 512;
 constexpr int kRxDepth = 2;
+// K splits of a resident-x launch whose x does not fit (each split holds its
+// share of x's columns): more splits measured slower than the x-slab kernel
+constexpr int kRxMaxSplits = 8;
 // K groups of the resident-x kernel for one matrix: the largest power of two
 // that divides the waves per block, leaves each group at least two K tiles,
 // and keeps every row slot (blocks x waves / KG of them) to at most one row.

@@ -35,11 +35,17 @@ MFMA_MAX_WAVES_GENERIC = 4   # the edge-handling MFMA variants (K % 256 != 0 or 
 # block's LDS (gfx950: 160 KiB) beside the 1 KiB pair table; and 17..32 rows
 # whose first 16 fit, on matrices of at most one tile row per CU (batch group
 # 1's x then comes from global memory, at most RX_MAX_WAVES_XG waves per
-# block). Its launch is (waves per block 1..12, blocks per matrix 1..tile
-# rows); the launch fixes the K groups (rx_kgroups) and with them the order of
-# every sum.
+# block). A single matrix whose x fits neither way can split K: split s of S
+# takes K tiles [s TC / S, (s + 1) TC / S) of every row and holds only their
+# columns of x (the fewest splits that fit, 3..RX_MAX_SPLITS, or 2 on
+# launches of 16384+ tiles with 17+ batch rows; the library adds the splits'
+# partial sums in split order). Its launch is (waves per block 1..12, blocks
+# per matrix and split 1..tile rows) with blocks = that count x splits x
+# matrices; the launch fixes the K groups (rx_kgroups) and with them the order
+# of every sum.
 RX_MAX_WAVES = 12
 RX_MAX_WAVES_XG = 8
+RX_MAX_SPLITS = 8
 COMPUTE_UNITS = 256  # MI355X; the library uses the device's count
 LDS_PER_BLOCK = 160 * 1024
 LUT_BYTES = 1024
@@ -92,19 +98,41 @@ def rx_lds_bytes(k: int, batch: int) -> int:
     return -(-(batch * (k // 8)) // 64) * 64 * 16
 
 
-def rx_staged_rows(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
-                   compute_units: int = COMPUTE_UNITS) -> int:
-    """Rows of x the resident-x kernel keeps in LDS (the library's rule): the
-    whole batch where it fits, 16 for 17..32 rows whose first 16 fit on a
-    matrix of at most one tile row per CU, else 0 (the x-slab kernel)."""
+def rx_layout(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
+              compute_units: int = COMPUTE_UNITS) -> tuple[int, int]:
+    """(rows of x the resident-x kernel keeps in LDS, K splits) of a launch
+    over one matrix (the library's rule): (batch, 1) where x fits; (16, 1) for
+    17..32 rows whose first 16 fit on a matrix of at most one tile row per
+    CU; (batch, S) with the fewest K splits S whose share of x's columns fits,
+    where splits pay; else (0, 0), the x-slab kernel."""
     if not (uses_mfma(batch, float32_activations) and aligned_x
             and not runs_generic(output_rows, k, float32_activations)):
-        return 0
+        return 0, 0
     if rx_lds_bytes(k, batch) + LUT_BYTES <= LDS_PER_BLOCK:
-        return batch
+        return batch, 1
     if batch > 16 and rx_lds_bytes(k, 16) + LUT_BYTES <= LDS_PER_BLOCK and tile_rows(output_rows) <= compute_units:
-        return 16
-    return 0
+        return 16, 1
+    tc = k_tiles(k)
+    for s in range(2, min(RX_MAX_SPLITS, tc) + 1):
+        if rx_lds_bytes(-(-tc // s) * 256, batch) + LUT_BYTES <= LDS_PER_BLOCK:
+            if s == 2 and (batch <= 16 or tile_rows(output_rows) * tc < 16384):
+                return 0, 0
+            return batch, s
+    return 0, 0
+
+
+def rx_staged_rows(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
+                   compute_units: int = COMPUTE_UNITS) -> int:
+    """Rows of x the resident-x kernel keeps in LDS (rx_layout); 0 where the
+    x-slab kernel serves the launch."""
+    return rx_layout(output_rows, k, batch, float32_activations, aligned_x, compute_units)[0]
+
+
+def rx_splits(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
+              compute_units: int = COMPUTE_UNITS) -> int:
+    """K splits of a resident-x launch over one matrix (rx_layout); 0 where
+    the x-slab kernel serves the launch."""
+    return rx_layout(output_rows, k, batch, float32_activations, aligned_x, compute_units)[1]
 
 
 def uses_rx(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
@@ -120,19 +148,21 @@ def rx_max_waves(output_rows: int, k: int, batch: int, compute_units: int = COMP
     return RX_MAX_WAVES_XG if 0 < staged < batch else RX_MAX_WAVES
 
 
-def rx_kgroups(output_rows: int, k: int, waves: int, blocks_per_matrix: int) -> int:
+def rx_kgroups(output_rows: int, k: int, waves: int, blocks_per_matrix: int, splits: int = 1) -> int:
     """K groups of a resident-x launch (the library's rule): the largest power
     of two that divides the waves per block, leaves every group at least two
-    K tiles and keeps each row slot (blocks x waves / groups) to one row."""
-    tr, tc, kg = tile_rows(output_rows), k_tiles(k), 1
+    of its split's K tiles and keeps each row slot (blocks per matrix and
+    split x waves / groups) to one row."""
+    tr, tc, kg = tile_rows(output_rows), k_tiles(k) // splits, 1
     while waves % (2 * kg) == 0 and tc >= 4 * kg and blocks_per_matrix * (waves // (2 * kg)) >= tr:
         kg *= 2
     return kg
 
 
-def rx_configuration(waves: int, blocks_per_matrix: int, matrices: int = 1) -> LaunchConfiguration:
+def rx_configuration(waves: int, blocks_per_matrix: int, matrices: int = 1, splits: int = 1) -> LaunchConfiguration:
+    """A resident-x launch: `blocks_per_matrix` blocks per matrix and K split."""
     return LaunchConfiguration(threads_per_block=ThreadsPerBlock(waves * WAVE_SIZE),
-                               blocks=BlockCount(blocks_per_matrix * matrices))
+                               blocks=BlockCount(blocks_per_matrix * splits * matrices))
 
 
 def grid_rows(output_rows: int, waves: int, batch: int = 1, float32_activations: bool = False) -> int:
@@ -178,15 +208,16 @@ def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int =
                      float32_activations: bool = False) -> tuple[int, int]:
     """(waves per block, K splits) of a configuration for a matrix with
     `output_rows` rows; for the resident-x kernel (K given), (waves per
-    block, blocks), which never split K."""
+    block, blocks), whose K splits the shape fixes (rx_splits)."""
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
     if k is not None and uses_rx(output_rows, k, batch, float32_activations):
         mw = rx_max_waves(output_rows, k, batch)
         if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= WAVE_SIZE * mw:
             raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {WAVE_SIZE * mw}]")
-        if not 1 <= blocks <= tile_rows(output_rows):
-            raise ValueError(f"blocks {blocks} must be in [1, {tile_rows(output_rows)}]")
+        sp = rx_splits(output_rows, k, batch, float32_activations)
+        if blocks % sp or not 1 <= blocks // sp <= tile_rows(output_rows):
+            raise ValueError(f"blocks {blocks} must be {sp} K splits x 1..{tile_rows(output_rows)}")
         return tpb // WAVE_SIZE, blocks
     generic = runs_generic(output_rows, k, float32_activations) if k is not None else float32_activations
     hi = WAVE_SIZE * max_waves_per_block(batch, float32_activations, generic)
@@ -220,7 +251,8 @@ def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 
         raise ValueError(f"{blocks} blocks of {tpb // 32} warps do not cover {output_rows} rows x batch {batch}")
     if uses_rx(output_rows, k, batch, float32_activations, aligned_x):
         waves = min(-(-tpb // WAVE_SIZE), rx_max_waves(output_rows, k, batch))
-        return rx_configuration(waves, -(-tile_rows(output_rows) // waves))
+        return rx_configuration(waves, -(-tile_rows(output_rows) // waves),
+                                splits=rx_splits(output_rows, k, batch, float32_activations, aligned_x))
     mfma = uses_mfma(batch, float32_activations)
     generic = runs_generic(output_rows, k, float32_activations) or not aligned_x
     hi = max_waves_per_block(batch, float32_activations, generic)
@@ -240,13 +272,19 @@ def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_a
     tc = k_tiles(k)
     if uses_rx(output_rows, k, batch, float32_activations):
         tr = tile_rows(output_rows)
+        sp = rx_splits(output_rows, k, batch, float32_activations)
         out = []
         for waves in (w for w in (1, 2, 3, 4, 6, 8, 12) if w <= rx_max_waves(output_rows, k, batch)):
             # every candidate block count up to the tile rows, the tile rows
             # themselves (one row slot per block holds them all: the default
-            # where they are fewer than the CUs) and one row per slot
-            for p in sorted({b for b in RX_BLOCK_CANDIDATES if b <= tr} | {tr, -(-tr // waves)}):
-                out.append(rx_configuration(waves, p))
+            # where they are fewer than the CUs) and one row per slot; with K
+            # splits (one block per CU: each holds most of the LDS) up to the
+            # CUs' share of a split
+            ps = {b for b in RX_BLOCK_CANDIDATES if b <= tr} | {tr, -(-tr // waves)}
+            if sp > 1:
+                ps = {p for p in ps if p * sp <= COMPUTE_UNITS} | {min(tr, COMPUTE_UNITS // sp)}
+            for p in sorted(ps):
+                out.append(rx_configuration(waves, p, splits=sp))
         return tuple(out)
     mfma = uses_mfma(batch, float32_activations)
     mw = max_waves_per_block(batch, float32_activations, runs_generic(output_rows, k, float32_activations))

@@ -87,9 +87,11 @@ def test_reference_launches_translate_to_valid_configurations(rows, k, batch):
             if launch.uses_rx(rows, k, batch, f32):
                 # the resident-x kernel: the block's threads (at most 12 waves,
                 # 8 with batch group 1's x from global memory), one tile row
-                # per wave slot; it never splits K
+                # per wave slot in each of the K splits the shape fixes
+                # (`splits` here counts blocks)
                 assert waves == min(-(-ref.threads_per_block.value // 64), launch.rx_max_waves(rows, k, batch))
-                assert splits == -(-launch.tile_rows(rows) // waves)
+                sp = launch.rx_splits(rows, k, batch, f32)
+                assert splits == -(-launch.tile_rows(rows) // waves) * sp
                 continue
             assert splits == 1
             # the block's threads in whole wave64s, a whole number of the MFMA
@@ -110,8 +112,12 @@ def test_translation_keeps_the_block_and_refuses_uncovered_launches():
     assert launch.waves_and_splits(cfg, 2304, 1, 9216) == (1, 1)
     # B = 24 on the x-slab MFMA kernel: 4 tile rows per block, 448 threads
     # (7 waves) -> 8 waves
+    cfg = launch.from_reference_configuration(RefLaunch(RefThreads(448), RefBlocks(25000)), 14336, 3584, 24)
+    assert launch.waves_and_splits(cfg, 14336, 24, 3584) == (8, 1)
+    # B = 24 at K = 9216 on the resident-x kernel with 3 K splits: 7 waves,
+    # one tile row per slot, in each split
     cfg = launch.from_reference_configuration(RefLaunch(RefThreads(448), RefBlocks(4000)), 2304, 9216, 24)
-    assert launch.waves_and_splits(cfg, 2304, 24, 9216) == (8, 1)
+    assert launch.waves_and_splits(cfg, 2304, 24, 9216) == (7, 21 * 3)
     with pytest.raises(ValueError, match="do not cover"):
         launch.from_reference_configuration(RefLaunch(RefThreads(256), RefBlocks(287)), 2304, 9216, 1)
     for t in (0, 16, 48 + 1, 2048):

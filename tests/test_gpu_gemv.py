@@ -360,6 +360,43 @@ def test_grouped_launch_with_x_partly_from_global(gpu):
                 assert max_rel_error(y, ref) <= REL_TOL, (batch, waves, per)
 
 
+@pytest.mark.parametrize("batch", [12, 16, 24, 32])
+def test_resident_x_k_splits(gpu, batch):
+    """x of 12..32 rows at K = 14336 fits a block's LDS only as a share of its
+    columns: the resident-x kernel splits K (3 to 7 splits, each block holding
+    its split's columns of x) and the last block of a row to arrive adds the
+    splits' partial sums in split order. Heavy-tailed weights (listed
+    escapes); against the oracle under the default and other launches (K
+    groups; several rows per row slot; one slot holding all 65 rows), the raw
+    twin bit-identical and a repeated launch bit-identical under each; a block
+    count that is not a multiple of the splits refused."""
+    from se12_amd import _native as nat
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+    from se12_amd.launch import rx_configuration, rx_layout
+
+    rows, cols = 1040, 14336
+    staged, splits = rx_layout(rows, cols, batch)
+    assert staged == batch and splits == {12: 3, 16: 3, 24: 5, 32: 7}[batch]
+    bits = heavy_tailed_bf16(rows, cols, seed=90)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    fused = Se12MatVecKernel(to_device(enc, gpu))
+    raw = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
+    xb = _x(batch, cols, seed=91 + batch)
+    x = bf16_tensor(xb, gpu)
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+    for launch in (None, rx_configuration(12, 32, splits=splits), rx_configuration(4, 8, splits=splits),
+                   rx_configuration(1, 1, splits=splits), rx_configuration(6, 65, splits=splits)):
+        y = fused.multiply(x, launch=launch).clone()
+        y2 = fused.multiply(x, launch=launch)
+        yr = raw.multiply(x, launch=launch)
+        torch.cuda.synchronize()
+        assert max_rel_error(y, ref) <= REL_TOL, launch
+        assert torch.equal(y, y2), launch
+        assert torch.equal(y, yr), launch
+    with pytest.raises(nat.Se12Error, match="K splits"):
+        fused.multiply(x, launch=rx_configuration(8, 32 * splits + 1))
+
+
 def test_grouped_launch_rejects_mixed_groups(gpu):
     from se12_amd import _native as nat
     from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, multiply_grouped

@@ -119,12 +119,13 @@ def test_launch_candidates_respect_each_kernels_limits():
         waves_and_splits(configuration(6, 1, 2304, batch=17), 2304, batch=17)
     with pytest.raises(ValueError, match="multiple of 2"):
         waves_and_splits(configuration(3, 1, 2304, batch=9), 2304, batch=9)
-    assert all(waves_and_splits(c, 2304, batch=24, k=9216)[0] % 4 == 0 for c in candidate_configurations(2304, 9216, batch=24))
-    assert min(waves_and_splits(c, 2304, batch=32, k=9216)[0] for c in candidate_configurations(2304, 9216, batch=32)) == 4
+    # (the x-slab kernel serves 14336x3584 at 24 and 32 rows)
+    assert all(waves_and_splits(c, 14336, batch=24, k=3584)[0] % 4 == 0 for c in candidate_configurations(14336, 3584, batch=24))
+    assert min(waves_and_splits(c, 14336, batch=32, k=3584)[0] for c in candidate_configurations(14336, 3584, batch=32)) == 4
     assert max_waves_per_block(1) == 16 and max_waves_per_block(6) == 8
-    for batch, f32, max_s in ((1, False, 36), (32, False, 16), (6, True, 36)):
-        cfgs = candidate_configurations(2304, 9216, batch=batch, float32_activations=f32)
-        pairs = [waves_and_splits(c, 2304, batch=batch, k=9216, float32_activations=f32) for c in cfgs]
+    for rows, k, batch, f32, max_s in ((2304, 9216, 1, False, 36), (14336, 3584, 32, False, 12), (2304, 9216, 6, True, 36)):
+        cfgs = candidate_configurations(rows, k, batch=batch, float32_activations=f32)
+        pairs = [waves_and_splits(c, rows, batch=batch, k=k, float32_activations=f32) for c in cfgs]
         assert max(s for _, s in pairs) == max_s
         assert max(w for w, _ in pairs) == max_waves_per_block(batch, f32)
     # 5 or more BF16 rows of x that fit a block's LDS (9 x 2304: 41 KiB): the
@@ -141,13 +142,41 @@ def test_launch_candidates_respect_each_kernels_limits():
 
     assert rx_staged_rows(4096, 3584, 32) == 16 and rx_staged_rows(4096, 3584, 16) == 16
     assert rx_staged_rows(4096, 3584, 24) == 16 and rx_staged_rows(4096, 2304, 32) == 32
-    assert rx_staged_rows(4112, 3584, 32) == 0 and rx_staged_rows(4096, 14336, 17) == 0
+    assert rx_staged_rows(4112, 3584, 32) == 0 and rx_staged_rows(4096, 14336, 17) == 17
     assert rx_staged_rows(4096, 3584, 32, compute_units=128) == 0
     assert rx_max_waves(4096, 3584, 32) == 8 and rx_max_waves(4096, 3584, 16) == 12 and rx_max_waves(14336, 3584, 16) == 12
     assert not uses_rx(2304, 2300, 9) and not uses_rx(2300, 2304, 9) and not uses_rx(256000, 2304, 4)
     assert rx_lds_bytes(9216, 6) == 6 * 1152 * 16 and rx_lds_bytes(2304, 5) == 1472 * 16
     pairs = [waves_and_splits(c, 2304, batch=9, k=2304) for c in candidate_configurations(2304, 2304, batch=9)]
     assert max(w for w, _ in pairs) == 12 and max(b for _, b in pairs) == 144 and min(b for _, b in pairs) >= 1
+
+
+def test_resident_x_k_split_rule():
+    """A single matrix whose x fits a block's LDS neither whole nor as its
+    first 16 rows splits K into the fewest ranges whose columns of x fit
+    (3..8; 2 only on launches of 16384+ tiles with 17+ rows); the x-slab
+    kernel serves the rest. Blocks then count K splits too."""
+    from se12_amd.launch import (candidate_configurations, rx_configuration, rx_kgroups, rx_layout, rx_splits,
+                                 waves_and_splits)
+
+    assert rx_layout(3584, 14336, 16) == (16, 3)      # 19 K tiles of 56: 152 KiB of x per block
+    assert rx_layout(3584, 14336, 24) == (24, 5) and rx_layout(3584, 14336, 32) == (32, 7)
+    assert rx_layout(2304, 9216, 24) == (24, 3) and rx_layout(2304, 9216, 32) == (32, 4)
+    assert rx_layout(4608, 36864, 9) == (9, 5) and rx_layout(4608, 36864, 16) == (16, 8)
+    assert rx_layout(36864, 4608, 24) == (24, 2)      # 2304 tile rows x 18 K tiles
+    assert rx_layout(3584, 14336, 9) == (0, 0)        # two splits at one batch group
+    assert rx_layout(2304, 9216, 16) == (0, 0) and rx_layout(14336, 3584, 32) == (0, 0)
+    assert rx_layout(4608, 36864, 24) == (0, 0)       # 12 splits: over the limit
+    assert rx_layout(4096, 3584, 32) == (16, 1) and rx_layout(2304, 2304, 32) == (32, 1)
+    assert rx_splits(2304, 9216, 4) == 0 and rx_splits(2304, 9216, 24, float32_activations=True) == 0
+    assert rx_configuration(8, 85, splits=3).blocks.value == 255
+    assert rx_kgroups(3584, 14336, 8, 85, splits=3) == 2   # 18 K tiles per split, 224 rows over 85 x 4 slots
+    assert rx_kgroups(3584, 14336, 8, 32, splits=3) == 1
+    for c in candidate_configurations(3584, 14336, batch=16):
+        waves, blocks = waves_and_splits(c, 3584, batch=16, k=14336)
+        assert blocks % 3 == 0 and 1 <= blocks // 3 <= 224 and blocks <= 3 * 256
+    with pytest.raises(ValueError, match="3 K splits"):
+        waves_and_splits(rx_configuration(8, 85), 3584, batch=16, k=14336)
 
 
 def test_resident_x_kgroups_rule():

@@ -285,23 +285,23 @@ def cold_rotation(nbytes: int) -> int:
     return max(2, -(-int(1.1e9) // nbytes))
 
 
-def batch_sweep(device, batches=(1, 2, 4, 5, 6, 7, 8, 16, 24, 32)) -> dict:
-    """Gemma-2-9B gate_proj 14336x3584, BF16 N(0, 0.02): the fused product at
-    each batch (the dot2 kernel up to 4 rows, an MFMA kernel from 5; one pass
-    over the weights either way) against hipBLASLt BF16 and the raw twin at
-    the same batch, each timed per launch over a rotation of cold matrices.
-    B = 5..7 show the MFMA kernel where the dot2 kernel, 4 batch rows per
-    pass, would need a second pass over the weights."""
+def batch_sweep(device, batches=(1, 2, 4, 5, 6, 7, 8, 16, 24, 32), n=14336, k=3584, seed=9_000) -> dict:
+    """Gemma-2-9B gate_proj 14336x3584 (or another n x k), BF16 N(0, 0.02):
+    the fused product at each batch (the dot2 kernel up to 4 rows, an MFMA
+    kernel from 5; one pass over the weights either way) against hipBLASLt
+    BF16 and the raw twin at the same batch, each timed per launch over a
+    rotation of cold matrices. B = 5..7 show the MFMA kernel where the dot2
+    kernel, 4 batch rows per pass, would need a second pass over the
+    weights."""
     from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
-    from se12_amd.launch import uses_mfma, uses_rx
+    from se12_amd.launch import rx_splits, uses_mfma, uses_rx
 
-    n, k = 14336, 3584
     gen = torch.Generator(device=device)
     ws, kerns = [], []
     r_se12 = cold_rotation(int(n * k * 1.504))
     r_bf16 = cold_rotation(2 * n * k)
     for r in range(max(r_se12, r_bf16)):
-        gen.manual_seed(9_000 + r)
+        gen.manual_seed(seed + r)
         w = (torch.randn((n, k), generator=gen, device=device, dtype=torch.float32) * 0.02).to(torch.bfloat16)
         if r < r_se12:
             kerns.append(Se12MatVecKernel(encode_on_device(w), max_batch=max(batches)))
@@ -309,7 +309,7 @@ def batch_sweep(device, batches=(1, 2, 4, 5, 6, 7, 8, 16, 24, 32)) -> dict:
             ws.append(w)
     out = {"shape": [n, k], "rotation": {"se12": r_se12, "bf16": r_bf16}, "points": []}
     for b in batches:
-        gen.manual_seed(9_999 + b)
+        gen.manual_seed(seed + 999 + b)
         x = torch.randn((b, k), generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
         y = torch.empty((b, n), dtype=torch.float32, device=device)
         g = capture(lambda x=x, y=y: [kk.multiply(x, out=y) for kk in kerns])
@@ -323,6 +323,8 @@ def batch_sweep(device, batches=(1, 2, 4, 5, 6, 7, 8, 16, 24, 32)) -> dict:
         del g, gb, gr, raws, yr
         lc = kerns[0].default_launch(b)
         kernel = ("mfma_resident_x" if uses_rx(n, k, b) else "mfma_x_slab") if uses_mfma(b) else "dot2"
+        if uses_rx(n, k, b) and rx_splits(n, k, b) > 1:
+            kernel += f"_{rx_splits(n, k, b)}_k_splits"
         pt = {"batch": b, "kernel": kernel, "us": round(us, 3),
               "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
               "se12_gbps": round(kerns[0].tensor.byte_size() / (us * 1e-6) / 1e9, 1),
@@ -809,6 +811,10 @@ def main(argv=None) -> int:
         del stack, flat
         torch.cuda.empty_cache()
         result["batch_sweep"] = batch_sweep(dev)
+        torch.cuda.empty_cache()
+        # the step's own dominant shape, Gemma-2-2B down_proj 2304x9216, from
+        # the batches whose x no longer fits a block's LDS whole (9+)
+        result["batch_sweep_down_proj"] = batch_sweep(dev, batches=(8, 9, 16, 24, 32), n=2304, k=9216, seed=19_000)
         torch.cuda.empty_cache()
     if not args.no_decode:
         result["decode_only"] = decode_only(dev)

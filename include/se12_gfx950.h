@@ -70,10 +70,20 @@ typedef struct se12_streams_out {
     int64_t fallback_raw_tiles;
 } se12_streams_out;
 
-/* Launch shape of the GEMV: `threads_per_block` = 64 * waves per workgroup
- * (64..1024), `blocks` = tile_rows * k_splits, k_splits dividing the K tiles
- * into equal contiguous ranges. Mirrors the reference LaunchConfiguration
- * (lws/domain/launch/heuristic.py:40-43) re-derived for wave64. */
+/* Launch shape of the GEMV: `threads_per_block` = 64 * waves per workgroup.
+ * Its `blocks` depend on the kernel the batch runs:
+ *  - dot2 kernel (batch 1..4 per launch, FP32 x): 1..16 waves, `blocks` =
+ *    tile_rows * k_splits, k_splits cutting the K tiles into contiguous
+ *    ranges;
+ *  - x-slab MFMA kernel (BF16 x, 5..32 rows): a multiple of ceil(batch / 8)
+ *    waves (4 for 3) up to 8, `blocks` = ceil(tile_rows / (those rows)) *
+ *    k_splits (k_splits <= 16);
+ *  - resident-x MFMA kernel (BF16 x, 5..32 rows, x or a K split's share of
+ *    it held in LDS): 1..12 waves (8 where batch group 1's x comes from
+ *    global memory), `blocks` = matrices * k_splits * blocks per matrix and
+ *    split (1..tile_rows), the k_splits fixed by the shape.
+ * Mirrors the reference LaunchConfiguration (lws/domain/launch/heuristic.py:
+ * 40-43) re-derived for wave64. */
 typedef struct se12_launch {
     int32_t threads_per_block;
     int32_t blocks;

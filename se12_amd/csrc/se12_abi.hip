@@ -595,7 +595,10 @@ static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
 // 15.2; at 1 to 1.5 rows per CU 12 waves stay best); on
 // matrices of 16 or more tile rows per CU, 8 waves and two blocks per CU
 // (256000x2304: 172 us against 191 at 8 rows, 184 against 186 at 16, 203
-// against 201 at 32).
+// against 201 at 32). A launch with K splits counts each row once per split
+// and takes at most one block per CU (each block holds most of the LDS: 258
+// blocks on 256 CUs ran a second generation, 39 us against 26 at 3584x14336
+// B = 16), with the waves by rows per block as above.
 static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t batch, int32_t* waves_out,
                               int32_t* blocks_out) {
     const int64_t cus = std::max<int32_t>(1, hs[0]->cu_count);

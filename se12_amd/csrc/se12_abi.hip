@@ -356,19 +356,23 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     } else if (tiles <= 32 * cus) {
         // 3 waves for 9 K tiles (9216x2304), 2 at 4 rows per launch (11.0 us
         // against 11.3; at 3 rows 10.5 against 10.4); longer rows 8 waves at 1..2 rows per
-        // launch when the tile rows fill the CUs once (4096x3584: 6.3 us
-        // against 7.2 with 3; 4096x4608: 7.3 against 8.3), 4 where some CUs
-        // take two blocks (4608x4096: 8.6 against 9.0 with 8) and at 3..4
-        // rows (7.95 / 9.0 against 8.2 / 9.2)
-        waves = tc <= 9 ? (bl >= 4 ? 2 : 3) : (bl >= 3 || tr > cus ? 4 : 8);
+        // launch when the tile rows fill the CUs evenly (4096x3584: 6.3 us
+        // against 7.2 with 3; 4096x4608: 7.3 against 8.3; 9B q/k/v grouped,
+        // 512 tile rows: 10.0 against 10.9 with 4), 4 where some CUs take
+        // two blocks and others one (4608x4096: 8.6 against 9.0 with 8) and
+        // at 3..4 rows (7.95 / 9.0 against 8.2 / 9.2)
+        waves = tc <= 9 ? (bl >= 4 ? 2 : 3) : (bl >= 3 || (tr > cus && tr % cus != 0) ? 4 : 8);
         waves = std::min<int64_t>(waves, tc);
     } else if (tiles <= 64 * cus) {
         // 2 rows per launch: 2 waves (14336x3584, B = 2: 17.8 us against 19.5
         // with tc / 2 = 7 waves), 3..4 rows: 1 wave (B = 3 / 4: 17.4-17.7 /
         // 18.3 against 18.6-18.9 / 19.1 with 2); one row: about half the K tiles, rounded up
-        // to an even count (14336x3584: 8 waves 16.2 us, 7 waves 16.8)
+        // to an even count (14336x3584: 8 waves 16.2 us, 7 waves 16.8), and
+        // for an odd count two tiles per wave (2B gate/up grouped, 9 K tiles:
+        // 5 waves 13.6 us against 14.2 with 4 and 15.2 with 6)
         const int64_t half = std::max<int64_t>(2, tc / 2);
-        waves = bl >= 3 ? 1 : bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, half + (half & 1)));
+        const int64_t one_row = tc % 2 == 1 ? (tc + 1) / 2 : half + (half & 1);
+        waves = bl >= 3 ? 1 : bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, one_row));
     } else {
         // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1
         // and 3 at B = 2..4 (B = 4: 154 us against 209 with 6); rows over
@@ -735,12 +739,14 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             grid_rows = gemm_row_blocks(hs, count, gemm_min_waves(batch));
         } else {
             default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, &waves, &splits);
-            // a launch with the norm in its head: one wave fewer where that
-            // splits the K tiles evenly (Gemma-2-2B gate/up, 9 K tiles: 3
-            // waves instead of 4 measured 15 us less per decoded token; the
-            // plain product measured the same either way)
-            if (pro && !generic && splits == 1 && waves > 2 && h0->TC % waves != 0 && h0->TC % (waves - 1) == 0)
-                --waves;
+            // a launch with the norm in its head: one or two waves fewer where
+            // that splits the K tiles evenly (Gemma-2-2B gate/up, 9 K tiles: 3
+            // waves instead of 4 measured 15 us less per decoded token)
+            if (pro && !generic && splits == 1 && waves > 2 && h0->TC % waves != 0) {
+                int32_t even = waves - 1;
+                while (even > 2 && h0->TC % even != 0) --even;
+                if (h0->TC % even == 0 && even >= waves - 2) waves = even;
+            }
         }
     }
     if (grid_rows * splits > INT32_MAX) return fail(SE12_E_INVALID, "%s: grid too large", fn);

@@ -351,6 +351,9 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         waves = 1;
         splits = std::max<int64_t>(1, (tc + 18) / 36);
         if (bl >= 3) splits = splits * 3 / 2;
+        // 2 rows: ~48 tiles per split (4608x36864: 3 splits 47.6 us against
+        // 49.7 with 4)
+        if (bl == 2) splits = std::max<int64_t>(1, (tc + 24) / 48);
     } else if (tiles <= 10 * cus) {
         waves = std::min<int64_t>(16, tc);
     } else if (tiles <= 32 * cus) {
@@ -364,15 +367,23 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         waves = tc <= 9 ? (bl >= 4 ? 2 : 3) : (bl >= 3 || (tr > cus && tr % cus != 0) ? 4 : 8);
         waves = std::min<int64_t>(waves, tc);
     } else if (tiles <= 64 * cus) {
-        // 2 rows per launch: 2 waves (14336x3584, B = 2: 17.8 us against 19.5
-        // with tc / 2 = 7 waves), 3..4 rows: 1 wave (B = 3 / 4: 17.4-17.7 /
-        // 18.3 against 18.6-18.9 / 19.1 with 2); one row: about half the K tiles, rounded up
-        // to an even count (14336x3584: 8 waves 16.2 us, 7 waves 16.8), and
-        // for an odd count two tiles per wave (2B gate/up grouped, 9 K tiles:
-        // 5 waves 13.6 us against 14.2 with 4 and 15.2 with 6)
-        const int64_t half = std::max<int64_t>(2, tc / 2);
-        const int64_t one_row = tc % 2 == 1 ? (tc + 1) / 2 : half + (half & 1);
-        waves = bl >= 3 ? 1 : bl >= 2 ? std::min<int64_t>(2, tc) : std::max<int64_t>(1, std::min<int64_t>(tc, one_row));
+        // 3..4 rows per launch: 1 wave (14336x3584, B = 3 / 4: 17.4-17.7 /
+        // 18.3 us against 18.6-18.9 / 19.1 with 2); 2 rows: 1 wave where the
+        // tile rows give each CU 3+ blocks (14336x3584 16.1 against 16.6-17.4
+        // with 2; 2B gate/up grouped 14.4 against 15.2), else 2 (27B q/k/v
+        // grouped, 512 tile rows: 13.6 against 16.5 with 1); one row: two
+        // tiles per wave for an odd count (2B gate/up grouped, 9 K tiles: 5
+        // waves 13.6 us against 14.2 with 4 and 15.2 with 6), for an even
+        // count 2 waves on 3+ blocks per CU (14336x3584: 15.9 against 16.3
+        // with 8) and 8 on fewer (27B q/k/v grouped: 12.1 against 12.5 with 2
+        // and 13.4 with 10)
+        if (bl >= 3)
+            waves = 1;
+        else if (bl == 2)
+            waves = tr >= 3 * cus ? 1 : 2;
+        else
+            waves = tc % 2 == 1 ? (tc + 1) / 2 : (tr >= 3 * cus ? 2 : 8);
+        waves = std::max<int64_t>(1, std::min<int64_t>(tc, waves));
     } else {
         // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1
         // and 3 at B = 2..4 (B = 4: 154 us against 209 with 6); rows over

@@ -387,12 +387,14 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
     } else {
         // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1
         // and 3 at B = 2..4 (B = 4: 154 us against 209 with 6); rows over
-        // 12 K tiles (36864x4608) 4 waves at B = 1..2 (45.0 / 45.4 us against
-        // 46.2 / 47.1) and 8 at B = 3..4 (49.7 against 52.9)
+        // 12 K tiles 8 waves (36864x4608 B = 1 / 2: 45.0 / 45.3 us against
+        // 45.4 / 45.8 with 4; 256000x3584: 216.8 / 217.0 against 225.6 /
+        // 223.2), at B = 3..4 on 256+ tiles per CU 2 (256000x3584 B = 4: 231
+        // against 258 with 8)
         if (tc <= 12)
             waves = bl >= 2 ? 3 : 6;
         else
-            waves = bl >= 3 ? 8 : 4;
+            waves = bl >= 3 && tiles >= 256 * cus ? 2 : 8;
         waves = std::min<int64_t>(waves, tc);
     }
     waves = std::max<int64_t>(1, std::min(waves, mw));

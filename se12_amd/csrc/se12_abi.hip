@@ -632,11 +632,12 @@ static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t bat
         1, std::min<int64_t>(rx_max_blocks(hs, count),
                              sp > 1 ? cus / ((int64_t)count * sp) : ceil_div((tall ? 2 : 1) * cus, count)));
     int32_t waves = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
-    // at most one tile row per row slot where the rows allow it: a grouped
-    // launch gives each matrix only its share of the blocks (9B gate/up, 2 x
-    // 14336x3584, 128 blocks each, B = 8 / 16: 33.0 / 34.3 us with 8 waves
-    // against 40.9 / 41.1 with 6)
-    if (!tall && sp == 1)
+    // a grouped launch gives each matrix only its share of the blocks: at
+    // most one tile row per row slot where the rows allow it (9B gate/up, 2
+    // x 14336x3584, 128 blocks each, B = 8 / 16: 33.0 / 34.3 us with 8 waves
+    // against 40.9 / 41.1 with 6; a single matrix stays at 6: 36864x4608 B =
+    // 8 / 16 53.0 / 56.1 against 57.1 / 59.2 with 8)
+    if (!tall && sp == 1 && count > 1)
         while (waves < 8 && per_matrix * waves < rx_max_blocks(hs, count)) waves = waves < 6 ? 6 : 8;
     if (lay.staged < batch) waves = std::min(waves, kRxMaxThreadsXG / 64);
     *waves_out = waves;

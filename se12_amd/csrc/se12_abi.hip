@@ -587,12 +587,8 @@ static RxLayout rx_layout(se12_handle* const* hs, int32_t count, int32_t batch) 
     return {batch, sp};
 }
 
-static int32_t rx_staged_rows(se12_handle* const* hs, int32_t count, int32_t batch) {
-    return rx_layout(hs, count, batch).staged;
-}
-
 static bool rx_fits(se12_handle* const* hs, int32_t count, int32_t batch) {
-    return rx_staged_rows(hs, count, batch) > 0;
+    return rx_layout(hs, count, batch).staged > 0;
 }
 
 static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {

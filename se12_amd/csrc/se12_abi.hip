@@ -636,8 +636,18 @@ static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t bat
     if (!tall && sp == 1 && count > 1)
         while (waves < 8 && per_matrix * waves < rx_max_blocks(hs, count)) waves = waves < 6 ? 6 : 8;
     if (lay.staged < batch) waves = std::min(waves, kRxMaxThreadsXG / 64);
+    int64_t blocks = per_matrix;
+    // a grouped launch of 2-3 tile rows per CU whose x leaves room for two
+    // blocks per CU: 4 waves and two blocks per CU (9B q/k/v, 512 tile rows,
+    // B = 5 / 8: 16.3 / 17.0 us against 17.2 / 17.7 with 12 waves x one
+    // block; 27B q/k/v 19.4 / 20.0 against 20.3 / 21.0)
+    if (count > 1 && sp == 1 && lay.staged == batch && rows >= 2 * cus && rows <= 3 * cus &&
+        2 * (int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= hs[0]->lds_per_block) {
+        waves = 4;
+        blocks = std::min<int64_t>(rx_max_blocks(hs, count), ceil_div(2 * cus, count));
+    }
     *waves_out = waves;
-    *blocks_out = (int32_t)(per_matrix * sp * count);
+    *blocks_out = (int32_t)(blocks * sp * count);
 }
 
 static GemvPlan plan_rx(bool raw, int32_t batch, int32_t staged, int32_t splits, int32_t waves, int32_t blocks,

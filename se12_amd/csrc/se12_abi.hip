@@ -606,9 +606,9 @@ static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
 // against 21.6 / 22.5 with 12, B = 20 23.9 against 23.5; 9216x2304, 2.25 rows
 // per CU, B = 9 / 16 / 20: 13.3 / 13.9 / 14.7 with 8 against 14.1 / 14.5 /
 // 15.2; at 1 to 1.5 rows per CU 12 waves stay best); on
-// matrices of 16 or more tile rows per CU, 8 waves and two blocks per CU
-// (256000x2304: 172 us against 191 at 8 rows, 184 against 186 at 16, 203
-// against 201 at 32). A launch with K splits counts each row once per split
+// matrices of 16 or more tile rows per CU, 8 waves, with two blocks per CU
+// from 32 tile rows per CU where two fit (256000x2304: 172 us against 191 at
+// 8 rows, 184 against 186 at 16, 203 against 201 at 32). A launch with K splits counts each row once per split
 // and takes at most one block per CU (each block holds most of the LDS: 258
 // blocks on 256 CUs ran a second generation, 39 us against 26 at 3584x14336
 // B = 16), with the waves by rows per block as above.
@@ -622,11 +622,17 @@ static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t bat
     int64_t rows = 0;
     for (int32_t i = 0; i < count; ++i) rows += hs[i]->TR * sp;
     const bool tall = rows >= 16 * cus;
+    // two blocks per CU only on very tall launches whose x leaves room for
+    // them (256000x2304 B = 8: 172 against 191 us; 27B gate/up grouped, 18
+    // tile rows per CU, B = 8 / 16: 96.6 / 99.3 us with one block per CU
+    // against 103.2 / 113.0 with two)
+    const bool two_per_cu = rows >= 32 * cus && lay.staged == batch &&
+                            2 * (int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= hs[0]->lds_per_block;
     // a split launch takes at most one block per CU (each holds most of
     // the LDS: a second block per CU would run after the first)
     const int64_t per_matrix = std::max<int64_t>(
         1, std::min<int64_t>(rx_max_blocks(hs, count),
-                             sp > 1 ? cus / ((int64_t)count * sp) : ceil_div((tall ? 2 : 1) * cus, count)));
+                             sp > 1 ? cus / ((int64_t)count * sp) : ceil_div((two_per_cu ? 2 : 1) * cus, count)));
     int32_t waves = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
     // a grouped launch gives each matrix only its share of the blocks: at
     // most one tile row per row slot where the rows allow it (9B gate/up, 2

@@ -88,6 +88,8 @@ def parse_args(argv=None):
     p.add_argument("--profile-batch", type=int, default=None, metavar="B",
                    help="only the batch sweep's 14336x3584 product at batch B (cold rotation of matrices), for "
                         "hardware-counter runs of one kernel")
+    p.add_argument("--profile-shape", default="14336x3584", metavar="NxK",
+                   help="the matrix shape of --profile-batch (default 14336x3584)")
     p.add_argument("--profile-e2e", choices=("se12", "raw", "bf16"), default=None,
                    help="only the Gemma-2-2B decode of one backend: prefill 512, capture, a 0.5 s pause, 32 graph-"
                         "replayed steps (kernel traces of the decode step)")
@@ -158,11 +160,11 @@ def profile_down(args, device) -> int:
 
 def profile_batch(args, device, batch: int) -> int:
     """The batch sweep's product alone at one batch: 14336x3584 (a Gemma-2-9B
-    MLP shape), a rotation of distinct matrices over more than 1 GB so that
-    every launch streams from HBM, default launch."""
+    MLP shape) or --profile-shape, a rotation of distinct matrices over more
+    than 1 GB so that every launch streams from HBM, default launch."""
     from se12_amd.hip import Se12MatVecKernel, encode_on_device
 
-    n, k = 14336, 3584
+    n, k = (int(v) for v in args.profile_shape.split("x"))
     gen = torch.Generator(device=device)
     kerns = []
     for r in range(cold_rotation(int(n * k * 1.504))):
@@ -176,7 +178,7 @@ def profile_batch(args, device, batch: int) -> int:
     g = capture(lambda: [kk.multiply(x, out=y) for kk in kerns])
     ms = time_graph(g, args.steps, args.warmup)
     launch = kerns[0].default_launch(batch)
-    print(json.dumps({"profile": f"fused SE12 product 14336x3584 at batch {batch}",
+    print(json.dumps({"profile": f"fused SE12 product {n}x{k} at batch {batch}",
                       "us_per_launch": round(ms * 1e3 / len(kerns), 3),
                       "launch": [launch.threads_per_block.value, launch.blocks.value]}), flush=True)
     return 0

@@ -600,8 +600,10 @@ static int64_t rx_max_blocks(se12_handle* const* hs, int32_t count) {
 // Default launch of the resident-x kernel: one block per CU (fewer where a
 // matrix has fewer tile rows than its share of the CUs) of 12 waves (3 per
 // SIMD, the kernel's register limit) up to 2 tile rows per CU, 8 waves up to
-// 3 and, up to 16 batch rows, 6 waves up to 16, which with the K groups
-// (rx_kgroups) keeps about 4 waves per CU on rows, each on more tiles
+// 3 and, up to 16 batch rows, 12 up to 4 (one K group: the idle waves speed
+// the copy of x; 14336x3584 B = 16 20.7 us against 21.4 with 6) and 6 waves
+// up to 16, which with the K groups (rx_kgroups) keeps about 4 waves per CU
+// on rows, each on more tiles
 // (14336x3584, 3.5 rows per CU, B = 9 / 16: 20.0 / 21.5 us with 6 waves
 // against 21.6 / 22.5 with 12, B = 20 23.9 against 23.5; 9216x2304, 2.25 rows
 // per CU, B = 9 / 16 / 20: 13.3 / 13.9 / 14.7 with 8 against 14.1 / 14.5 /
@@ -633,7 +635,11 @@ static void rx_default_launch(se12_handle* const* hs, int32_t count, int32_t bat
     const int64_t per_matrix = std::max<int64_t>(
         1, std::min<int64_t>(rx_max_blocks(hs, count),
                              sp > 1 ? cus / ((int64_t)count * sp) : ceil_div((two_per_cu ? 2 : 1) * cus, count)));
-    int32_t waves = tall ? 8 : rows > 3 * cus && batch <= 16 ? 6 : rows > 2 * cus ? 8 : kRxMaxThreads / 64;
+    int32_t waves = tall                              ? 8
+                    : rows > 4 * cus && batch <= 16   ? 6
+                    : rows > 3 * cus && batch <= 16   ? kRxMaxThreads / 64
+                    : rows > 2 * cus                  ? 8
+                                                      : kRxMaxThreads / 64;
     // a grouped launch gives each matrix only its share of the blocks: at
     // most one tile row per row slot where the rows allow it (9B gate/up, 2
     // x 14336x3584, 128 blocks each, B = 8 / 16: 33.0 / 34.3 us with 8 waves

@@ -152,8 +152,11 @@ def rx_kgroups(output_rows: int, k: int, waves: int, blocks_per_matrix: int, spl
     """K groups of a resident-x launch (the library's rule): the largest power
     of two that divides the waves per block, leaves every group at least two
     of its split's K tiles and keeps each row slot (blocks per matrix and
-    split x waves / groups) to one row."""
+    split x waves / groups) to one row; one group from 3 tile rows per
+    block."""
     tr, tc, kg = tile_rows(output_rows), k_tiles(k) // splits, 1
+    if tr >= 3 * blocks_per_matrix:
+        return kg
     while waves % (2 * kg) == 0 and tc >= 4 * kg and blocks_per_matrix * (waves // (2 * kg)) >= tr:
         kg *= 2
     return kg

@@ -186,7 +186,8 @@ def test_resident_x_kgroups_rule():
 
     assert rx_kgroups(2304, 9216, 8, 144) == 8         # 144 tile rows, 36 K tiles: one row per block
     assert rx_kgroups(2304, 9216, 8, 72) == 4
-    assert rx_kgroups(14336, 3584, 8, 256) == 2        # 896 rows over 256 blocks x 4 slots; 14 K tiles
+    assert rx_kgroups(14336, 3584, 8, 256) == 1        # 896 rows: 3+ per block keep the waves busy
+    assert rx_kgroups(14336, 3584, 8, 320) == 2        # 2.8 rows per block over 4 slots each; 14 K tiles
     assert rx_kgroups(14336, 3584, 8, 512) == 4
     assert rx_kgroups(9216, 2304, 8, 256) == 2
     assert rx_kgroups(9216, 2304, 8, 576) == 4         # 9 K tiles: groups of 2..3 tiles

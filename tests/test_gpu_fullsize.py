@@ -135,6 +135,31 @@ def test_q_9b_wide_batches_x_partly_from_global(gpu):
         r0 += b
 
 
+@pytest.mark.parametrize("batch", [1, 2, 5, 8, 16])
+def test_9b_qkv_grouped_default_launch(gpu, batch):
+    """Gemma-2-9B q/k/v (4096, 2048 and 2048 rows at K = 3584) in one grouped
+    launch under the default launch at batch 1..16 (dot2 with 8 waves per
+    block at 1, 2 at 2; from 5 rows the resident-x kernel, at 5 and 8 with 4
+    waves and two blocks per CU, k/v's share of the blocks past their rows):
+    within REL_TOL of the oracle, the raw twin bit-identical."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device, multiply_grouped
+
+    cols = 3584
+    shapes = [(4096, cols), (2048, cols), (2048, cols)]
+    bits = [o.normal_bf16(r, c, seed=300 + i, std=0.02) for i, (r, c) in enumerate(shapes)]
+    ws = [bf16_tensor(b, gpu) for b in bits]
+    encs = [o.encode(b.reshape(-1), r, c) for b, (r, c) in zip(bits, shapes)]
+    fused = [Se12MatVecKernel(encode_on_device(w)) for w in ws]
+    raws = [RawBf16MatVecKernel(w) for w in ws]
+    xb = o.normal_bf16(batch, cols, seed=310 + batch, std=1.0)
+    x = bf16_tensor(xb, gpu)
+    ys, yrs = multiply_grouped(fused, x), multiply_grouped(raws, x)
+    torch.cuda.synchronize()
+    for y, yr, e in zip(ys, yrs, encs):
+        assert torch.equal(y, yr)
+        assert max_rel_error(y, o.gemv_reference(e, o.bf16_bits_to_f32(xb))) <= REL_TOL
+
+
 def test_down_27b_heavy_tailed_full_size(gpu):
     from se12_amd.hip import HipSe12WeightDecoder, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
 

@@ -507,7 +507,7 @@ def roofline_model(device, props, per_shape: dict) -> dict:
     from se12_amd.hip import HipBenchmarkTimer, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
 
     timer = HipBenchmarkTimer(device.index)
-    facts = rl.DeviceFacts(hbm_peak_gbps=props.hbm_peak_gbps, copy_gbps=timer.measure_peak_copy_bandwidth(),
+    facts = rl.DeviceFacts(hbm_peak_gbps=props.hbm_peak_gbps, copy_gbps=timer.measure_copy_traffic_gbps(),
                            stream_read_gbps=timer.measure_stream_read_bandwidth(),
                            launch_us=timer.measure_graph_launch_us())
     gen = torch.Generator(device=device)
@@ -628,7 +628,7 @@ def main(argv=None) -> int:
         return profile_batch(args, dev, args.profile_batch)
     if args.profile_e2e:
         return profile_e2e(args.profile_e2e, dev)
-    props = HipGpuProbe(0).properties()
+    props = HipGpuProbe(0).facts()
     log(f"[bench] device {props.name} {props.arch} CUs={props.compute_units}")
     t0 = time.perf_counter()
     stack = build_stack(args.layers, dev)
@@ -834,6 +834,7 @@ def main(argv=None) -> int:
         result["micro"] = {
             "verdict": v["verdict"], "per_batch": {b: e["verdict"] for b, e in v["per_batch"].items()},
             "peak_copy_bandwidth_gbps": round(v["peak_copy_bandwidth_gbps"], 1),
+            "copy_traffic_gbps": round(v["copy_traffic_gbps"], 1),
             "rows": [{"shape": row["shape"], "batch": row["batch_size"],
                       **{n: r.get("median_microseconds") and round(r["median_microseconds"], 3)
                          for n, r in row["results"].items()},

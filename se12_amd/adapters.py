@@ -23,7 +23,20 @@ configuration (waves per block, tile rows x K splits); any other object with
 `threads_per_block.value` and `blocks.value` - the reference's own
 `LaunchConfiguration`, as its tuner and heuristic build them - carries the
 reference's meaning and is translated by
-`se12_amd.launch.from_reference_configuration`.
+`se12_amd.launch.from_reference_configuration`, with this adapter's
+`sm_count` as the compute-unit count the library's kernel choice uses.
+
+The reference's other GPU ports are built the same way:
+
+    CudaGpuProbe(device_index=None)             -> HipGpuProbe
+    CudaBenchmarkTimer(device_index, l2_size)   -> HipBenchmarkTimer
+    FilesystemTuningCache(directory, gpu_slug)  -> FilesystemTuningCache
+
+(lws/adapters/cuda/gpu_probe.py:59-80, lws/adapters/cuda/benchmark_timer.py:
+20-66, lws/adapters/filesystem/tuning_cache.py:31-59). They return the port's
+value objects (se12_amd.ports), and `tune_launch(gpu_slug, requests,
+evaluators, cache)` takes the reference's arguments
+(lws/application/gpu/tune_launch.py:43-48).
 """
 
 from __future__ import annotations
@@ -36,6 +49,10 @@ from . import _native as nat
 from . import hip
 from .compiler import KernelSource
 from .launch import LaunchConfiguration, from_reference_configuration
+from .tune import FilesystemTuningCache, tune_launch  # noqa: F401  (re-exported ports)
+
+HipGpuProbe = hip.HipGpuProbe
+HipBenchmarkTimer = hip.HipBenchmarkTimer
 
 
 def _count(sm_count: Any) -> int:
@@ -51,7 +68,8 @@ def _native_launch(kernel: hip._GemvBase, activations: torch.Tensor, launch: Any
     x = activations.unsqueeze(0) if activations.dim() == 1 else activations
     return from_reference_configuration(launch, kernel.rows, kernel.cols, x.shape[0],
                                         float32_activations=x.dtype == torch.float32,
-                                        aligned_x=x.is_contiguous() and x.data_ptr() % 16 == 0)
+                                        aligned_x=x.is_contiguous() and x.data_ptr() % 16 == 0,
+                                        compute_units=kernel.sm_count)
 
 
 class _ReferenceSignature:

@@ -27,6 +27,16 @@ from typing import Any
 
 # gfx targets the library holds code objects for (se12_amd/csrc/build.py)
 LIBRARY_ARCHES = ("gfx950",)
+
+
+def arch_number(arch: str) -> int:
+    """A gfx architecture as HIP's major * 10 + minor: gfx950 -> 95."""
+    d = arch.split(":", 1)[0].strip().removeprefix("gfx")
+    return int(d[:-2]) * 10 + int(d[-2], 16)
+
+
+# the reference's integer compile-target arch -> the library's gfx target
+ARCH_BY_NUMBER = {arch_number(a): a for a in LIBRARY_ARCHES}
 CACHE_DIR_ENV_VAR = "LWS_CACHE_DIR"
 
 # reference kernel name -> the C entry point that replaces it
@@ -93,7 +103,7 @@ def device_compile_target(device: int | None = None) -> CompileTarget:
     """choose_compile_target for a HIP device (default: the current one)."""
     from .hip import HipGpuProbe
 
-    return choose_compile_target(HipGpuProbe(device).properties().arch)
+    return choose_compile_target(HipGpuProbe(device).facts().arch)
 
 
 class AotCompiledKernelHandle:
@@ -125,10 +135,20 @@ class AotKernelCompiler:
         raw = os.environ.get(CACHE_DIR_ENV_VAR)
         self.cache_directory = pathlib.Path(raw) if raw else pathlib.Path.home() / ".cache" / "lws"
 
-    def compile(self, source: Any, target: CompileTarget) -> AotCompiledKernelHandle:
+    def compile(self, source: Any, target: Any) -> AotCompiledKernelHandle:
+        """`target` is this module's CompileTarget, or the reference's SASS
+        target (kind value "sass", integer arch) that its
+        `choose_compile_target(capability, nvrtc_targets, ForcePtx(False))`
+        (decisions.py:70-84) picks from HipGpuProbe.properties(): the
+        capability and targets there encode gfx950 as 95. A PTX target, or an
+        architecture the library holds no code object for, is refused."""
         kind = getattr(target, "kind", None)
         arch = getattr(getattr(target, "arch", None), "value", None)
-        if kind is not CompileTargetKind.CODE_OBJECT or not isinstance(arch, str):
+        if getattr(kind, "value", None) == "sass" and isinstance(arch, int):
+            arch = ARCH_BY_NUMBER.get(arch)
+            if arch is None:
+                raise UnsupportedDeviceError(f"the SE12 library holds no code object for sm_{target.arch.value}")
+        elif kind is not CompileTargetKind.CODE_OBJECT or not isinstance(arch, str):
             raise UnsupportedDeviceError(
                 f"target {target!r} is not a gfx code-object target (use se12_amd.compiler.choose_compile_target)")
         if base_arch(arch) not in LIBRARY_ARCHES:

@@ -279,13 +279,19 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
     // the S partial sums in ascending split order, stores the row and resets
     // the counter for the next launch.
     auto finish_splits = [&](int n_rows) {
-        wait_vector_loads();
+        // the wait for this wave's partial stores is also a compiler barrier
+        // (memory clobber): no store sinks below it and no counter update
+        // rises above it (the builtin wait is not modelled as touching
+        // memory, so it would order nothing)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         for (int r0 = 0; r0 < n_rows; r0 += 64) {
             const int r = r0 + (int)lane;
             int old = -1;
             if (r < n_rows) old = __hip_atomic_fetch_add(&a.counters[j0 + r * nw], 1, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
             uint64_t last = __ballot(old == S - 1);
+            // the other splits' partial sums are read only after the arrival
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
             while (last) {
                 const int tr = j0 + (r0 + __builtin_ctzll(last)) * nw;
                 last &= last - 1;

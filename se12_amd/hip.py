@@ -21,6 +21,7 @@ from __future__ import annotations
 
 import ctypes
 import dataclasses
+import os
 import statistics as _st
 from typing import Any, Callable
 
@@ -38,6 +39,7 @@ from .format import (
     tile_grid,
     validate_device_streams,
 )
+from . import ports as P
 from .launch import BlockCount, LaunchConfiguration, ThreadsPerBlock
 
 
@@ -161,8 +163,9 @@ class _GemvBase:
                          launch: LaunchConfiguration | None = None) -> torch.Tensor:
         """`multiply` through se12_gemv_noalloc: the library allocates nothing
         (its split-K scratch is a static per-GPU array shared by every such
-        call on the GPU, so overlapping calls race); `out` is required."""
-        x, xd = _activations(activations, self.cols, self.device)
+        call on the GPU, so overlapping calls race); `out` is required, and
+        x must be contiguous (it is not copied)."""
+        x, xd = _activations(activations, self.cols, self.device, copy=False)
         out = _require(out, "out", torch.float32, (x.shape[0], self.rows), self.device)
         nat.check(nat.lib().se12_gemv_noalloc(self.handle.raw, nat.ptr(x), xd, x.shape[0], nat.ptr(out),
                                               _launch_struct(launch), nat.stream_ptr()))
@@ -244,17 +247,26 @@ class RawBf16MatVecKernel(_GemvBase):
         self.handle = bind_raw_bf16(self.weights, max_batch)
 
 
-def _activations(activations: torch.Tensor, cols: int, device) -> tuple[torch.Tensor, int]:
+def _activations(activations: torch.Tensor, cols: int, device, copy: bool = True) -> tuple[torch.Tensor, int]:
+    """x as a contiguous [B, cols] tensor and its library dtype code. With
+    `copy=False` a non-contiguous x is refused instead of copied (the copy is
+    a device allocation)."""
     x = activations.unsqueeze(0) if activations.dim() == 1 else activations
     if x.dim() != 2 or x.shape[1] != cols:
         raise ValueError(f"activations must be [B, {cols}], got {tuple(activations.shape)}")
     if x.device != device:
         raise ValueError(f"activations on {x.device}, weights on {device}")
     if x.dtype == torch.bfloat16:
-        return x.contiguous(), nat.X_BF16
-    if x.dtype == torch.float32:
-        return x.contiguous(), nat.X_F32
-    raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
+        code = nat.X_BF16
+    elif x.dtype == torch.float32:
+        code = nat.X_F32
+    else:
+        raise ValueError(f"activations must be bfloat16 or float32, got {x.dtype}")
+    if not x.is_contiguous():
+        if not copy:
+            raise ValueError("activations must be contiguous here: copying them would allocate device memory")
+        x = x.contiguous()
+    return x, code
 
 
 def _fp32_out(out: torch.Tensor | None, b: int, rows: int, device, name: str = "out") -> torch.Tensor:
@@ -471,11 +483,13 @@ def codebook_from_histogram(counts) -> tuple[int, ...]:
 
 
 HBM_TRANSFERS_PER_CLOCK = 4
+DEVICE_INDEX_ENV_VAR = "LWS_DEVICE"
 
 
 @dataclasses.dataclass(frozen=True)
-class DeviceProperties:
-    """hipDeviceProp_t facts the roofline and the launch heuristic use."""
+class DeviceFacts:
+    """hipDeviceProp_t facts the roofline, the launch heuristic and the
+    reports use (flat; the port's nested DeviceProperties is built from it)."""
 
     name: str
     arch: str
@@ -517,17 +531,39 @@ class DeviceProperties:
             base = base.replace("--", "-")
         return f"{base}-{self.arch.split(':')[0]}"
 
+    @property
+    def capability(self) -> tuple[int, int]:
+        """(major, minor) of the gfx architecture as HIP reports them
+        (hipDeviceProp major / minor): gfx950 -> (9, 5), gfx942 -> (9, 4)."""
+        digits = self.arch.split(":")[0].removeprefix("gfx")
+        return int(digits[:-2] or 0), int(digits[-2], 16) if len(digits) >= 2 else 0
+
+
+def _library_targets() -> tuple[int, ...]:
+    """The architectures the library holds code objects for, in the
+    capability encoding (major * 10 + minor: gfx950 -> 95)."""
+    from .compiler import LIBRARY_ARCHES, arch_number
+
+    return tuple(arch_number(a) for a in LIBRARY_ARCHES)
+
 
 class HipGpuProbe:
-    """GpuProbe over hipGetDeviceProperties (gpu_probe.py:59-80)."""
+    """GpuProbe over hipGetDeviceProperties (lws/application/ports/gpu/
+    gpu_probe.py:17-27, the reference adapter lws/adapters/cuda/gpu_probe.py:
+    59-80): `properties()`, `software_versions()` and `smoke_test()` return
+    the port's value objects (se12_amd.ports); `facts()` the flat
+    hipDeviceProp_t record this package's own code reads."""
 
     def __init__(self, device: int | None = None) -> None:
-        self.device = torch.cuda.current_device() if device is None else device
+        if device is None:
+            env = os.environ.get(DEVICE_INDEX_ENV_VAR)  # the reference's default (gpu_probe.py:83-89)
+            device = int(env) if env is not None else torch.cuda.current_device()
+        self.device = device
 
-    def properties(self) -> DeviceProperties:
+    def facts(self) -> DeviceFacts:
         info = nat.DeviceInfo()
         nat.check(nat.lib().se12_device_info_get(self.device, ctypes.byref(info)))
-        return DeviceProperties(
+        return DeviceFacts(
             name=info.name.decode(), arch=info.arch.decode(), compute_units=info.compute_units,
             wavefront_size=info.wavefront_size, l2_bytes=info.l2_bytes, lds_bytes_per_cu=info.lds_bytes_per_cu,
             lds_bytes_per_block=info.lds_bytes_per_block, total_memory_bytes=info.total_memory_bytes,
@@ -538,21 +574,62 @@ class HipGpuProbe:
             driver_version=info.driver_version,
         )
 
-    def software_versions(self) -> dict:
-        return {"torch": torch.__version__, "hip": getattr(torch.version, "hip", None), "se12": nat.version()}
+    def properties(self) -> P.DeviceProperties:
+        """The nested DeviceProperties the reference's entry points read
+        (lws/domain/device/properties.py:98-107): identity and slug, compute
+        units as `sm_count`, VRAM total / free, L2 size, peak bandwidth from
+        the memory clock, and the library's code-object targets."""
+        f = self.facts()
+        free, total = torch.cuda.mem_get_info(self.device)
+        major, minor = f.capability
+        identity = P.DeviceIdentity(name=P.DeviceName(f.name), slug=P.GpuSlug(f.slug))
+        compute = P.ComputeHardware(capability=P.ComputeCapability(major=major, minor=minor),
+                                    sm_count=P.SmCount(f.compute_units))
+        memory = P.MemoryProfile(
+            vram=P.VramSizes(total=P.Bytes(int(total)), free=P.Bytes(int(free))),
+            characteristics=P.MemoryCharacteristics(l2_size=P.Bytes(f.l2_bytes),
+                                                    bandwidth=P.GigabytesPerSecond(f.hbm_peak_gbps)))
+        return P.DeviceProperties(
+            identity_and_compute=P.IdentityAndCompute(identity=identity, compute=compute),
+            memory_and_nvrtc=P.MemoryAndNvrtc(memory=memory, nvrtc_targets=P.NvrtcTargets(_library_targets())))
 
-    def smoke_test(self) -> bool:
-        """Does a kernel run on this device at all (gpu_probe.py:152-166)."""
+    def software_versions(self) -> P.SoftwareVersions:
+        """Report-only versions (properties.py:147-165): HIP driver and
+        runtime, torch and its architecture list, the library's build string
+        in CuPy's and NVRTC's places."""
+        f = self.facts()
+        lib_version = nat.version()
+        arch_list = tuple(torch.cuda.get_arch_list()) if hasattr(torch.cuda, "get_arch_list") else ()
+        core = P.VersionsCore(
+            toolchain=P.ToolchainVersions(driver=str(f.driver_version), cuda_runtime=str(f.runtime_version)),
+            torch_and_cupy=P.TorchAndCupy(torch=P.TorchInfo(version=torch.__version__,
+                                                            arch_list=P.TorchArchList(arch_list)),
+                                          cupy_version=lib_version))
+        return P.SoftwareVersions(core=core, nvrtc=P.NvrtcInfo(version=lib_version,
+                                                              targets=P.NvrtcTargets(_library_targets())))
+
+    def smoke_test(self) -> P.SupportVerdict:
+        """Does torch run a kernel on this device, and does the library's
+        kernel (one 16 x 256 fused product) give the right sum (the reference's
+        check, gpu_probe.py:152-166, runs a torch kernel only)."""
         try:
-            a = torch.ones(16, device=f"cuda:{self.device}")
-            return bool((a + a).sum().item() == 32.0)
+            dev = torch.device("cuda", self.device)
+            a = torch.full((8,), 1.0, device=dev) * 2
+            if a.sum().item() != 16.0:
+                return P.SupportVerdict(False)
+            w = torch.full((16, 256), 1.0, dtype=torch.bfloat16, device=dev)
+            x = torch.full((1, 256), 0.5, dtype=torch.bfloat16, device=dev)
+            y = Se12MatVecKernel(encode_on_device(w), max_batch=1).multiply(x)
+            return P.SupportVerdict(bool(torch.all(y == 128.0).item()))
         except Exception:
-            return False
+            return P.SupportVerdict(False)
 
 
 # MI355X's last-level Infinity Cache (MALL) is not reported by hipDeviceProp;
 # the flush covers it explicitly.
 INFINITY_CACHE_BYTES = 256 * 1024 * 1024
+GIBIBYTE = 1024 ** 3
+PEAK_COPY_FRACTION_OF_FREE = 0.25
 
 
 @dataclasses.dataclass(frozen=True)
@@ -569,14 +646,24 @@ def latency_stats(samples_us) -> LatencyStats:
 
 
 class HipBenchmarkTimer:
-    """Event timing after a cache flush of at least 2 x (L2 + Infinity Cache)
-    (benchmark_timer.py:20-66; the reference flushes 2 x L2 only)."""
+    """BenchmarkTimer (lws/application/ports/gpu/benchmark_timer.py:13-21):
+    HIP event timing after a cache eviction of at least 2 x (L2 + Infinity
+    Cache) (the reference adapter, lws/adapters/cuda/benchmark_timer.py:
+    20-66, flushes 2 x L2 only). Constructed as the reference's
+    `CudaBenchmarkTimer(device_index, l2_size)`; `l2_size` is a `Bytes`-like
+    object or an int, queried from the device when omitted.
 
-    def __init__(self, device: int | None = None, l2_bytes: int | None = None) -> None:
-        self.device = torch.cuda.current_device() if device is None else device
-        if l2_bytes is None:
-            l2_bytes = HipGpuProbe(self.device).properties().l2_bytes
-        flush = 2 * (int(l2_bytes) + INFINITY_CACHE_BYTES)
+    Port methods: `time_operation(operation, counts) -> LatencySamples` and
+    `measure_peak_copy_bandwidth() -> GigabytesPerSecond`. The package's own
+    measurements use `time_stats`, `time_cold_rotation` and
+    `measure_copy_traffic_gbps`."""
+
+    def __init__(self, device_index: int | None = None, l2_size: Any = None) -> None:
+        self.device = torch.cuda.current_device() if device_index is None else int(device_index)
+        if l2_size is None:
+            l2_size = HipGpuProbe(self.device).facts().l2_bytes
+        self.l2_size = int(P.value_of(l2_size))
+        flush = 2 * (self.l2_size + INFINITY_CACHE_BYTES)
         self.flush_buffer = torch.zeros(flush // 4, dtype=torch.float32, device=f"cuda:{self.device}")
 
     def flush(self) -> None:
@@ -584,8 +671,32 @@ class HipBenchmarkTimer:
         dirty lines whose write-back competes with the timed operation."""
         torch.sum(self.flush_buffer)
 
-    def time_operation(self, operation: Callable[[], Any], warmup: int = 25, timed: int = 100, flush: bool = True,
-                       graph: bool = False) -> LatencyStats:
+    # -- the port --------------------------------------------------------
+
+    def time_operation(self, operation: Callable[[], Any], counts: Any) -> P.LatencySamples:
+        """`counts.warmup` untimed runs, then `counts.timed` samples, each
+        after a cache eviction, in microseconds (benchmark_timer.py:31-50)."""
+        st = self.time_stats(operation, warmup=int(counts.warmup), timed=int(counts.timed))
+        return P.LatencySamples(values=st.samples)
+
+    def measure_peak_copy_bandwidth(self) -> P.GigabytesPerSecond:
+        """GB/s of a device-to-device FP32 copy of min(1 GiB, 25% of free
+        memory), the copied bytes counted once, median of 20 samples after 10
+        warmups: the reference's peak (benchmark_timer.py:55-66), which its
+        verdict's 70% bar divides by."""
+        free, _ = torch.cuda.mem_get_info(self.device)
+        target = min(GIBIBYTE, int(free * PEAK_COPY_FRACTION_OF_FREE))
+        n = -(-target // 4)
+        src = torch.empty(n, dtype=torch.float32, device=f"cuda:{self.device}")
+        dst = torch.empty_like(src)
+        st = self.time_stats(lambda: dst.copy_(src), warmup=10, timed=20)
+        del src, dst
+        return P.GigabytesPerSecond(n * 4 / (st.median_us * 1e-6) / 1e9)
+
+    # -- this package's measurements ---------------------------------------
+
+    def time_stats(self, operation: Callable[[], Any], warmup: int = 25, timed: int = 100, flush: bool = True,
+                   graph: bool = False) -> LatencyStats:
         """Microseconds per call, one event pair per sample on the current
         stream. `graph=True` captures the operation once in a HIP graph and
         times its replays, as a decode runtime issues it: without the ~2 us a
@@ -687,16 +798,17 @@ class HipBenchmarkTimer:
             for _ in range(launches):
                 t.add_(1.0)
 
-        st = self.time_operation(chain, warmup=5, timed=20, flush=False, graph=True)
+        st = self.time_stats(chain, warmup=5, timed=20, flush=False, graph=True)
         return st.median_us / launches
 
-    def measure_peak_copy_bandwidth(self, nbytes: int = 1 << 30) -> float:
-        """GB/s of a device-to-device copy of `nbytes` (read + write counted),
-        the measured peak the 80%-of-HBM target is checked against."""
+    def measure_copy_traffic_gbps(self, nbytes: int = 1 << 30) -> float:
+        """GB/s of HBM traffic of a device-to-device copy of `nbytes`, read
+        and write both counted: the copy's physical rate, for the roofline
+        (the port's measure_peak_copy_bandwidth counts the bytes once)."""
         n = nbytes // 4
         src = torch.empty(n, dtype=torch.float32, device=f"cuda:{self.device}")
         dst = torch.empty_like(src)
-        st = self.time_operation(lambda: dst.copy_(src), warmup=5, timed=20, flush=False)
+        st = self.time_stats(lambda: dst.copy_(src), warmup=5, timed=20, flush=False)
         return 2 * n * 4 / (st.median_us * 1e-6) / 1e9
 
 

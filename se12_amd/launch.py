@@ -208,17 +208,17 @@ def max_waves_per_block(batch: int, float32_activations: bool = False, generic: 
 
 
 def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int = 1, k: int | None = None,
-                     float32_activations: bool = False) -> tuple[int, int]:
+                     float32_activations: bool = False, compute_units: int = COMPUTE_UNITS) -> tuple[int, int]:
     """(waves per block, K splits) of a configuration for a matrix with
     `output_rows` rows; for the resident-x kernel (K given), (waves per
     block, blocks), whose K splits the shape fixes (rx_splits)."""
     tpb = launch.threads_per_block.value
     blocks = launch.blocks.value
-    if k is not None and uses_rx(output_rows, k, batch, float32_activations):
-        mw = rx_max_waves(output_rows, k, batch)
+    if k is not None and uses_rx(output_rows, k, batch, float32_activations, compute_units=compute_units):
+        mw = rx_max_waves(output_rows, k, batch, compute_units)
         if tpb % WAVE_SIZE or not WAVE_SIZE <= tpb <= WAVE_SIZE * mw:
             raise ValueError(f"threads_per_block {tpb} must be a multiple of 64 in [64, {WAVE_SIZE * mw}]")
-        sp = rx_splits(output_rows, k, batch, float32_activations)
+        sp = rx_splits(output_rows, k, batch, float32_activations, compute_units=compute_units)
         if blocks % sp or not 1 <= blocks // sp <= tile_rows(output_rows):
             raise ValueError(f"blocks {blocks} must be {sp} K splits x 1..{tile_rows(output_rows)}")
         return tpb // WAVE_SIZE, blocks
@@ -236,7 +236,7 @@ def waves_and_splits(launch: LaunchConfiguration, output_rows: int, batch: int =
 
 
 def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 1, float32_activations: bool = False,
-                                 aligned_x: bool = True) -> LaunchConfiguration:
+                                 aligned_x: bool = True, compute_units: int = COMPUTE_UNITS) -> LaunchConfiguration:
     """This kernel's configuration for a launch built with the reference's
     meaning: one 32-lane warp per output element, `threads_per_block` in
     32..1024, and `blocks` x warps per block covering rows x batch
@@ -245,17 +245,19 @@ def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 
     (rounded up to whole wave64s, and for the MFMA kernel to a multiple of the
     batch's tile rows per block, within the variant's limit) and splits no K
     tiles, as the reference kernel never does. A launch that leaves outputs
-    uncovered, which the reference kernel would leave unwritten, is refused."""
+    uncovered, which the reference kernel would leave unwritten, is refused.
+    `compute_units` is the count the library's kernel choice uses (the
+    adapter's sm_count)."""
     tpb = int(launch.threads_per_block.value)
     blocks = int(launch.blocks.value)
     if tpb % 32 or not 32 <= tpb <= 1024:
         raise ValueError(f"threads_per_block {tpb} must be a multiple of 32 in [32, 1024]")
     if blocks <= 0 or blocks * (tpb // 32) < output_rows * batch:
         raise ValueError(f"{blocks} blocks of {tpb // 32} warps do not cover {output_rows} rows x batch {batch}")
-    if uses_rx(output_rows, k, batch, float32_activations, aligned_x):
-        waves = min(-(-tpb // WAVE_SIZE), rx_max_waves(output_rows, k, batch))
+    if uses_rx(output_rows, k, batch, float32_activations, aligned_x, compute_units):
+        waves = min(-(-tpb // WAVE_SIZE), rx_max_waves(output_rows, k, batch, compute_units))
         return rx_configuration(waves, -(-tile_rows(output_rows) // waves),
-                                splits=rx_splits(output_rows, k, batch, float32_activations, aligned_x))
+                                splits=rx_splits(output_rows, k, batch, float32_activations, aligned_x, compute_units))
     mfma = uses_mfma(batch, float32_activations)
     generic = runs_generic(output_rows, k, float32_activations) or not aligned_x
     hi = max_waves_per_block(batch, float32_activations, generic)
@@ -267,17 +269,18 @@ def from_reference_configuration(launch, output_rows: int, k: int, batch: int = 
     return configuration(min(waves, hi), 1, output_rows, batch, float32_activations)
 
 
-def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_activations: bool = False) -> tuple[LaunchConfiguration, ...]:
+def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_activations: bool = False,
+                             compute_units: int = COMPUTE_UNITS) -> tuple[LaunchConfiguration, ...]:
     """Every (waves, splits) worth timing: waves per block up to the batch's
     limit (valid for the fused kernel and its raw twin alike), K splits up to
     the K tiles; for the dot2 kernel never more waves than tiles per split
     (search_space.py:17-19 enumerates threads per block the same way)."""
     tc = k_tiles(k)
-    if uses_rx(output_rows, k, batch, float32_activations):
+    if uses_rx(output_rows, k, batch, float32_activations, compute_units=compute_units):
         tr = tile_rows(output_rows)
-        sp = rx_splits(output_rows, k, batch, float32_activations)
+        sp = rx_splits(output_rows, k, batch, float32_activations, compute_units=compute_units)
         out = []
-        for waves in (w for w in (1, 2, 3, 4, 6, 8, 12) if w <= rx_max_waves(output_rows, k, batch)):
+        for waves in (w for w in (1, 2, 3, 4, 6, 8, 12) if w <= rx_max_waves(output_rows, k, batch, compute_units)):
             # every candidate block count up to the tile rows, the tile rows
             # themselves (one row slot per block holds them all: the default
             # where they are fewer than the CUs) and one row per slot; with K
@@ -285,7 +288,7 @@ def candidate_configurations(output_rows: int, k: int, batch: int = 1, float32_a
             # CUs' share of a split
             ps = {b for b in RX_BLOCK_CANDIDATES if b <= tr} | {tr, -(-tr // waves)}
             if sp > 1:
-                ps = {p for p in ps if p * sp <= COMPUTE_UNITS} | {min(tr, COMPUTE_UNITS // sp)}
+                ps = {p for p in ps if p * sp <= compute_units} | {min(tr, compute_units // sp)}
             for p in sorted(ps):
                 out.append(rx_configuration(waves, p, splits=sp))
         return tuple(out)

@@ -119,7 +119,13 @@ def faster_baseline(results: dict[str, VariantResult]) -> VariantResult | None:
 
 def decide_shape_verdict(results: dict[str, VariantResult], peak_gbps: float) -> dict | None:
     """None unless the fused kernel and a baseline were both timed
-    (run_microbenchmark.py:102-117)."""
+    (run_microbenchmark.py:102-117). `peak_gbps` is the copy peak as the
+    reference measures it, the copied bytes counted once
+    (HipBenchmarkTimer.measure_peak_copy_bandwidth;
+    lws/adapters/cuda/benchmark_timer.py:55-66), and the baseline's rate is
+    its BF16-equivalent bandwidth (bytes_moved / median), so
+    `baseline_fraction_of_peak` is the reference's ratio
+    (verdict.py:40-47)."""
     fused = results.get(FUSED)
     base = faster_baseline(results)
     if fused is None or not fused.accuracy_passed or base is None:
@@ -244,7 +250,7 @@ def _rocm_version() -> str | None:
 def device_metadata(device, peak_gbps: float, warmup: int, timed: int) -> dict:
     """The reference's report metadata (lws/domain/benchmark/summary.py:
     14-41), AMD facts under its names, plus AMD-only fields."""
-    props = HipGpuProbe(device.index).properties()
+    props = HipGpuProbe(device.index).facts()
     fs = sysfs_facts(props.pci_address)
     part = fs["compute_partition"]
     return {
@@ -302,7 +308,10 @@ def run(shapes=DEFAULT_SHAPES, batches=DEFAULT_BATCHES, device=None, warmup: int
     """Measures every (shape, batch) and returns (micro report, verdict file)."""
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
     timer = HipBenchmarkTimer(dev.index)
-    peak = timer.measure_peak_copy_bandwidth()
+    # the verdict's peak: the reference's copy figure (bytes counted once);
+    # the copy's physical traffic (read + write) is reported beside it
+    peak = float(timer.measure_peak_copy_bandwidth().value)
+    traffic = timer.measure_copy_traffic_gbps()
     rows = []
     for r, c in shapes:
         got = benchmark_shape(r, c, batches, timer, peak, dev, warmup=warmup, timed=timed)
@@ -323,6 +332,7 @@ def run(shapes=DEFAULT_SHAPES, batches=DEFAULT_BATCHES, device=None, warmup: int
             ratios.setdefault(row["batch_size"], []).append((tuple(row["shape"]), v["ratio"], v["baseline_fraction_of_peak"]))
     verdict = verdict_payload(meta["gpu_slug"], meta["compute_capability"], ratios)
     verdict["peak_copy_bandwidth_gbps"] = peak
+    verdict["copy_traffic_gbps"] = traffic
     verdict["peak_bandwidth_fraction"] = PEAK_BANDWIDTH_FRACTION
     # the headline row (first shape, batch 1) carries the reference's
     # per-row metadata fields at the top level
@@ -330,6 +340,7 @@ def run(shapes=DEFAULT_SHAPES, batches=DEFAULT_BATCHES, device=None, warmup: int
     fr = head["results"].get(FUSED, {})
     raw_rows = [row for row in rows if row["results"].get(RAW, {}).get("bandwidth_gbps")]
     micro = dict(meta)
+    micro["copy_traffic_gbps"] = traffic
     micro.update({
         "shape": head["shape"], "batch_size": head["batch_size"],
         "median_microseconds": fr.get("median_microseconds"), "p10_microseconds": fr.get("p10_microseconds"),

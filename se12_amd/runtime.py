@@ -156,7 +156,7 @@ def current_gpu_slug(device=None) -> str:
     from .hip import HipGpuProbe
 
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    return HipGpuProbe(dev.index if dev.index is not None else torch.cuda.current_device()).properties().slug
+    return HipGpuProbe(dev.index if dev.index is not None else torch.cuda.current_device()).facts().slug
 
 
 # ---------------------------------------------------------------------------
@@ -523,10 +523,10 @@ def load_packed(packed: Any, mode: str = "auto", order: str | None = None, devic
 
 def tuned_lookup(device, kind: str, tuning_dir=None) -> LaunchLookup | None:
     """The launch lookup of this GPU's tuning file, or None without one."""
-    from .tune import load_tuning
+    from .tune import FilesystemTuningCache, tuning_directory, tuning_lookup
 
-    tf = load_tuning(current_gpu_slug(device), tuning_dir)
-    return tf.lookup(kind) if tf is not None else None
+    tf = FilesystemTuningCache(tuning_directory(tuning_dir), current_gpu_slug(device)).load()
+    return tuning_lookup(tf, kind) if tf is not None else None
 
 
 def load_reference(model_dir, device=None, order: str | None = "matched",

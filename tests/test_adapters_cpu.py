@@ -8,6 +8,7 @@ import dataclasses
 import inspect
 
 import pytest
+import torch
 
 from se12_amd import adapters, compiler, launch
 
@@ -148,3 +149,91 @@ def test_adapter_arguments_are_checked_before_any_gpu_call():
             adapters.Se12MatVecKernel(c, t, None, bad)
     with pytest.raises(compiler.UnsupportedDeviceError):
         adapters.RawBf16MatVecKernel(c, object(), None, 256)
+
+
+@pytest.mark.parametrize("batch", [24, 32])
+def test_translation_follows_the_adapters_compute_units(batch):
+    """A matrix of 256 tile rows at K = 3584: x of 24 or 32 rows does not fit
+    a block's LDS but its first 16 rows do, and on a GPU of 256+ CUs (one
+    tile row per CU) such batches run the resident-x kernel with batch group
+    1's x from global memory; with 132 compute units the library picks the
+    x-slab kernel instead. The translation must follow the count the library
+    was given."""
+    rows, k = 4096, 3584
+    ref = RefLaunch(RefThreads(256), RefBlocks(-(-rows * batch // 8)))
+    cfg256 = launch.from_reference_configuration(ref, rows, k, batch, compute_units=256)
+    assert launch.uses_rx(rows, k, batch, compute_units=256)
+    assert launch.waves_and_splits(cfg256, rows, batch, k, compute_units=256) == (4, 64)
+    assert launch.rx_staged_rows(rows, k, batch, compute_units=256) == 16
+    assert not launch.uses_rx(rows, k, batch, compute_units=132)
+    # the rows whose x fits whole run the resident-x kernel on either GPU
+    assert launch.uses_rx(rows, k, 20, compute_units=132) and launch.uses_rx(rows, k, 20, compute_units=256)
+    cfg132 = launch.from_reference_configuration(ref, rows, k, batch, compute_units=132)
+    # the x-slab kernel: a multiple of ceil(batch / 8) (4 for 3) tile rows per block, no K split
+    lo = launch.mfma_min_waves(batch)
+    assert launch.waves_and_splits(cfg132, rows, batch, k, compute_units=132) == (4 if lo <= 4 else lo, 1)
+    assert cfg132.blocks.value == -(-launch.tile_rows(rows) // lo)
+    # and the candidates the tuner would time follow the same rule
+    c132 = launch.candidate_configurations(rows, k, batch, compute_units=132)
+    for c in c132:
+        launch.waves_and_splits(c, rows, batch, k, compute_units=132)
+
+
+def test_adapter_translation_passes_its_sm_count(monkeypatch):
+    seen = {}
+
+    def fake(launch_cfg, rows, k, batch, **kw):
+        seen.update(kw)
+        return "translated"
+
+    monkeypatch.setattr(adapters, "from_reference_configuration", fake)
+
+    class K:
+        rows, cols, sm_count = 4096, 3584, 132
+
+    x = torch.zeros((24, 3584), dtype=torch.bfloat16)
+    assert adapters._native_launch(K(), x, RefLaunch(RefThreads(256), RefBlocks(12288))) == "translated"
+    assert seen["compute_units"] == 132
+
+
+def test_aot_compiler_takes_the_reference_sass_target():
+    """The reference's choose_compile_target gives CompileTarget(SASS,
+    ComputeArch(95)) from the probe's capability (9, 5) and targets (95,)
+    (lws/domain/device/decisions.py:70-103); the compiler accepts that for
+    gfx950 and refuses PTX or another architecture."""
+
+    @dataclasses.dataclass(frozen=True)
+    class Kind:
+        value: str
+
+    @dataclasses.dataclass(frozen=True)
+    class Arch:
+        value: int
+
+    @dataclasses.dataclass(frozen=True)
+    class RefTarget:
+        kind: Kind
+        arch: Arch
+
+    c = compiler.AotKernelCompiler()
+    h = c.compile(compiler.KernelSource(""), RefTarget(Kind("sass"), Arch(95)))
+    assert h.function("lws_gemv_se12") is h.library.se12_gemv
+    for bad in (RefTarget(Kind("sass"), Arch(94)), RefTarget(Kind("ptx"), Arch(95))):
+        with pytest.raises(compiler.UnsupportedDeviceError):
+            c.compile(compiler.KernelSource(""), bad)
+    assert compiler.arch_number("gfx950:sramecc+:xnack-") == 95
+
+
+def test_port_adapters_take_the_reference_constructor_arguments():
+    # lws/adapters/cuda/gpu_probe.py:62, benchmark_timer.py:24,
+    # lws/adapters/filesystem/tuning_cache.py:44
+    def names(cls):
+        return list(inspect.signature(cls.__init__).parameters)[1:]
+
+    assert len(names(adapters.HipGpuProbe)) == 1
+    assert names(adapters.HipBenchmarkTimer) == ["device_index", "l2_size"]
+    assert names(adapters.FilesystemTuningCache) == ["directory", "gpu_slug"]
+    assert list(inspect.signature(adapters.HipBenchmarkTimer.time_operation).parameters)[1:] == ["operation", "counts"]
+    assert list(inspect.signature(adapters.tune_launch).parameters) == ["gpu_slug", "requests", "evaluators", "cache"]
+    for m in ("properties", "software_versions", "smoke_test"):
+        assert list(inspect.signature(getattr(adapters.HipGpuProbe, m)).parameters) == ["self"]

@@ -32,7 +32,7 @@ def _setup(gpu):
 
     compiler = AotKernelCompiler()
     target = device_compile_target(gpu.index)
-    sm_count = HipGpuProbe(gpu.index).properties().compute_units
+    sm_count = HipGpuProbe(gpu.index).facts().compute_units
     return compiler, target, sm_count
 
 

@@ -109,17 +109,18 @@ def test_tuned_configurations_are_consumed_and_stay_order_matched(gpu, tmp_path)
     runtime.pack_pretrained(model, tmp_path / "packed")
     model.save_pretrained(tmp_path / "orig")
     shapes = {(256, 256), (128, 256), (512, 256), (256, 512)}
-    reqs = [tune.TuneRequest(r, c, b) for r, c in sorted(shapes) for b in (1, 2)]
+    reqs = [tune.tune_request(r, c, b) for r, c in sorted(shapes) for b in (1, 2)]
     slug = runtime.current_gpu_slug(gpu)
-    tf = tune.tune_launch(slug, reqs, tune.gpu_evaluators(gpu, samples=3), directory=tmp_path / "t")
-    assert len(tf.entries) == len(reqs)
+    tf = tune.tune_launch(slug, reqs, tune.gpu_evaluators(gpu, samples=3),
+                          tune.FilesystemTuningCache(tmp_path / "t", slug))
+    assert len(tf.entries.items) == len(reqs)
     attn = runtime.register_attention()
     fused = runtime.load_packed(tmp_path / "packed", mode="fused", order="matched", device=gpu, log=None,
                                 attn_implementation=attn, tuning_dir=tmp_path / "t")
     ref = runtime.load_reference(tmp_path / "orig", device=gpu, order="matched", attn_implementation=attn,
                                  tuning_dir=tmp_path / "t")
     q = fused.model.layers[0].self_attn.q_proj
-    assert q.launch_lookup(256, 256, 1) == tf.lookup("order_matched")(256, 256, 1)
+    assert q.launch_lookup(256, 256, 1) == tune.tuning_lookup(tf, "order_matched")(256, 256, 1)
     ids = torch.randint(0, cfg.vocab_size, (2, 10), device=gpu, generator=torch.Generator(device=gpu).manual_seed(4))
     with torch.no_grad():
         sf, lf = _generate(fused, ids, 6)

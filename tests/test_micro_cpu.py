@@ -83,3 +83,57 @@ def test_sysfs_readers_tolerate_missing_files(tmp_path):
     assert micro._current_level(str(table)) == 1400.0
     table.write_text("0: 500Mhz\n")
     assert micro._current_level(str(table)) is None
+
+
+# Medians (us) of one full MI355X microbenchmark run: (rows, cols, batch,
+# fused, raw twin, hipBLASLt). Its copy of 1 GiB moved 4,628.4 GB/s of HBM
+# traffic, i.e. 2,314.2 GB/s with the copied bytes counted once.
+MEASURED_ROWS = [
+    (2304, 9216, 1, 9.259, 10.246, 14.789),
+    (2304, 9216, 4, 11.482, 13.502, 14.854),
+    (2304, 9216, 16, 17.063, 17.936, 15.260),
+    (9216, 2304, 1, 8.619, 11.190, 15.050),
+    (9216, 2304, 4, 10.762, 11.859, 15.337),
+    (9216, 2304, 16, 13.920, 15.453, 15.480),
+    (256000, 2304, 1, 141.660, 184.914, 193.561),
+    (256000, 2304, 4, 159.098, 193.506, 196.643),
+    (256000, 2304, 16, 183.955, 291.371, 201.955),
+]
+COPY_TRAFFIC_GBPS = 4628.4
+
+
+def _replay(peak_gbps: float) -> dict:
+    ratios: dict = {}
+    for rows, cols, b, fused, raw, blas in MEASURED_ROWS:
+        moved = micro.bytes_moved(rows, cols, b)
+        res = {n: timed(n, us, moved / (us * 1e-6) / 1e9)
+               for n, us in ((micro.FUSED, fused), (micro.RAW, raw), (micro.BLAS, blas))}
+        v = micro.decide_shape_verdict(res, peak_gbps)
+        ratios.setdefault(b, []).append(((rows, cols), v["ratio"], v["baseline_fraction_of_peak"]))
+    p = runtime.verdict_payload("gpu-gfx950", "gfx950", ratios)
+    return {b: e["verdict"] for b, e in p["per_batch"].items()}
+
+
+def test_measured_rows_give_the_reference_verdicts_with_the_copy_counted_once():
+    """The reference's 70% bar divides the baseline's BF16-equivalent rate by
+    a copy whose bytes are counted once (lws/adapters/cuda/benchmark_timer.py:
+    55-66, verdict.py:40-47). On these rows every baseline clears it, so batch
+    1 and 4 are GO (every ratio <= 0.95) and batch 16 is NO-GO (2304x9216 at
+    1.118 against hipBLASLt)."""
+    assert _replay(COPY_TRAFFIC_GBPS / 2) == {"1": "GO", "4": "GO", "16": "NO-GO"}
+    # a copy counted twice (read + write) halves every fraction and turns the
+    # same timings INCONCLUSIVE at batch 4 and 16
+    assert _replay(COPY_TRAFFIC_GBPS) == {"1": "GO", "4": "INCONCLUSIVE", "16": "INCONCLUSIVE"}
+
+
+def test_auto_policy_follows_the_replayed_verdict(tmp_path):
+    ratios: dict = {}
+    for rows, cols, b, fused, raw, blas in MEASURED_ROWS:
+        moved = micro.bytes_moved(rows, cols, b)
+        res = {n: timed(n, us, moved / (us * 1e-6) / 1e9)
+               for n, us in ((micro.FUSED, fused), (micro.RAW, raw), (micro.BLAS, blas))}
+        v = micro.decide_shape_verdict(res, COPY_TRAFFIC_GBPS / 2)
+        ratios.setdefault(b, []).append(((rows, cols), v["ratio"], v["baseline_fraction_of_peak"]))
+    runtime.write_verdict(runtime.verdict_payload("gpu-gfx950", "gfx950", ratios), tmp_path)
+    pol = runtime.load_policy("gpu-gfx950", tmp_path)
+    assert [pol.fused_for(b) for b in (1, 2, 4, 5, 16, 17)] == [True, True, True, False, False, False]

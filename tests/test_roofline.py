@@ -5,6 +5,8 @@ crossing of ratio 1 as the decode cost grows."""
 
 from __future__ import annotations
 
+import dataclasses
+
 import pytest
 
 from se12_amd import roofline as r
@@ -83,11 +85,16 @@ def test_calibration_and_eta_fit_from_the_raw_kernel():
 
 
 def test_peak_from_hip_device_properties():
-    from se12_amd.hip import DeviceProperties
+    from se12_amd.hip import DeviceFacts
 
-    p = DeviceProperties(name="x", arch="gfx950", compute_units=256, wavefront_size=64, l2_bytes=4 << 20,
-                         lds_bytes_per_cu=160 << 10, lds_bytes_per_block=160 << 10, total_memory_bytes=288 << 30,
-                         clock_khz=2_400_000, memory_clock_khz=2_000_000, memory_bus_width_bits=8192)
+    p = DeviceFacts(name="x", arch="gfx950:sramecc+:xnack-", compute_units=256, wavefront_size=64, l2_bytes=4 << 20,
+                    lds_bytes_per_cu=160 << 10, lds_bytes_per_block=160 << 10, total_memory_bytes=288 << 30,
+                    clock_khz=2_400_000, memory_clock_khz=2_000_000, memory_bus_width_bits=8192)
     # MI355X: 2.0 GHz x 4 transfers x 8192 bits / 8 = 8,192 GB/s (published: 8.0 TB/s)
     assert p.hbm_peak_gbps == pytest.approx(8192.0)
     assert abs(p.hbm_peak_gbps / r.HBM_PEAK_PUBLISHED_GBPS - 1) < 0.03
+    # HIP's major / minor of the gfx architecture (gfx950 -> 9.5, gfx942 -> 9.4, gfx90a -> 9.0)
+    assert p.capability == (9, 5)
+    assert dataclasses.replace(p, arch="gfx942").capability == (9, 4)
+    assert dataclasses.replace(p, arch="gfx90a").capability == (9, 0)
+    assert dataclasses.replace(p, arch="gfx1100").capability == (11, 0)

@@ -23,7 +23,8 @@ reference loads that file back. Here:
   `launch_lookup` the runtime's layers call, and `load_packed` /
   `load_reference` read it for the current GPU.
 
-The candidates are this kernel's (se12_amd.launch.candidate_configurations);
+The candidates are this kernel's (se12_amd.launch.candidate_configurations,
+for BF16 and for FP32 activations: `tuning_candidates`);
 the best and order-matched rules are the reference's, restated in
 se12_amd.launch. The GPU evaluator times one launch per sample after a
 read-only cache eviction (median over samples, HIP events) and passes a
@@ -171,8 +172,30 @@ class FilesystemTuningCache:
 
 
 def _measure(evaluator: Any, cfg: LaunchConfiguration) -> TimingAndAccuracy:
-    m = evaluator.evaluate(cfg) if hasattr(evaluator, "evaluate") else evaluator(cfg)
+    """One evaluation; a configuration the kernel refuses for the
+    evaluator's activations (the library's validation raises) counts as
+    failing, since evaluators need not catch it (the reference's does not,
+    lws/adapters/cuda/candidate_evaluator.py:40-53)."""
+    from ._native import Se12Error
+
+    try:
+        m = evaluator.evaluate(cfg) if hasattr(evaluator, "evaluate") else evaluator(cfg)
+    except (ValueError, Se12Error):
+        return TimingAndAccuracy(float("inf"), False)
     return TimingAndAccuracy(float(m.median_latency_microseconds), bool(m.passes_accuracy_check))
+
+
+def tuning_candidates(rows: int, cols: int, batch: int) -> tuple[LaunchConfiguration, ...]:
+    """The configurations timed per request: those of BF16 activations, then
+    those only FP32 activations take (at 5+ rows BF16 runs an MFMA kernel and
+    FP32 the dot2 kernel, whose configurations differ). A request does not
+    say which the evaluators feed (the reference's tuner feeds FP32,
+    lws/tune.py:80-83; this package's BF16), so both sets are offered and a
+    kernel refuses the other's."""
+    bf16 = candidate_configurations(rows, cols, batch=batch)
+    seen = set(bf16)
+    f32 = tuple(c for c in candidate_configurations(rows, cols, batch=batch, float32_activations=True) if c not in seen)
+    return bf16 + f32
 
 
 def tune_launch(gpu_slug: Any, requests: Sequence[Any], evaluators: Callable[[Any], Any], cache: Any) -> P.TuningFile:
@@ -185,7 +208,7 @@ def tune_launch(gpu_slug: Any, requests: Sequence[Any], evaluators: Callable[[An
         pair = evaluators(req)
         rows, cols = int(req.weight_shape.output_rows), int(req.weight_shape.k)
         batch = int(P.value_of(req.batch))
-        cands = candidate_configurations(rows, cols, batch=batch)
+        cands = tuning_candidates(rows, cols, batch)
         raw_timed = tuple(TimedCandidate(c, _measure(pair.raw, c)) for c in cands)
         fused_timed = tuple(TimedCandidate(c, _measure(pair.fused, c)) for c in cands)
         best_raw, best_fused = best_configuration(raw_timed), best_configuration(fused_timed)

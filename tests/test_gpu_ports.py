@@ -158,6 +158,84 @@ def test_timer_times_operations_and_counts_the_copy_once(gpu):
     assert verdict in ("GO", "NO-GO", "INCONCLUSIVE") and fraction > 0
 
 
+class DefaultMatchEvaluator:
+    """A CandidateEvaluator in the manner of the reference's tuner
+    (lws/adapters/cuda/candidate_evaluator.py:31-60): a kernel bound to its
+    weights, timed over repeated launches with a configuration, passing when
+    its output is within 1e-4 x max(|ref|, 1) of the kernel's own
+    default-launch output."""
+
+    def __init__(self, kernel, activations: torch.Tensor) -> None:
+        self.kernel, self.activations = kernel, activations
+        self.reference = kernel.multiply(activations)
+
+    def evaluate(self, configuration):
+        import time
+
+        for _ in range(2):
+            self.kernel.multiply(self.activations, configuration)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            out = self.kernel.multiply(self.activations, configuration)
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) / 5 * 1e6
+        rel = ((out - self.reference).abs() / self.reference.abs().clamp_min(1.0)).max().item()
+
+        @dataclasses.dataclass(frozen=True)
+        class TimingAndAccuracy:
+            median_latency_microseconds: float
+            passes_accuracy_check: bool
+
+        return TimingAndAccuracy(us, rel <= 1e-4)
+
+
+@dataclasses.dataclass(frozen=True)
+class EvaluatorPair:
+    raw: object
+    fused: object
+
+
+def test_tuner_with_reference_style_evaluators_over_the_adapters(gpu, tmp_path):
+    """The tuner's composition as lws.tune builds it (lws/tune.py:38-99):
+    adapters built with the reference's constructor arguments, one evaluator
+    per kernel, the cache port; every tuned configuration then runs through
+    the adapter within REL_TOL of the oracle, raw and fused bit-identical
+    under the order-matched one."""
+    from se12_amd.adapters import (FilesystemTuningCache, HipGpuProbe, RawBf16MatVecKernel, Se12MatVecKernel,
+                                   tune_launch)
+    from se12_amd.compiler import AotKernelCompiler
+
+    props = HipGpuProbe(gpu.index).properties()
+    compute = props.identity_and_compute.compute
+    target = reference_compile_target(compute.capability, props.memory_and_nvrtc.nvrtc_targets)
+    compiler = AotKernelCompiler()
+    rows, cols = 768, 2304
+    bits, enc = normal_case(rows, cols, seed=71)
+    fused = Se12MatVecKernel(compiler, target, to_device(enc, gpu), compute.sm_count)
+    raw = RawBf16MatVecKernel(compiler, target, torch.from_numpy(bits.astype(np.int16)).to(gpu).view(torch.bfloat16),
+                              compute.sm_count)
+    xs = {b: torch.from_numpy(o.bf16_bits_to_f32(o.normal_bf16(b, cols, seed=72 + b, std=1.0))).to(gpu)
+          for b in (1, 4, 8)}   # FP32, as lws.tune feeds them: at 8 rows the dot2 kernel, MFMA configurations refused
+
+    def evaluators(req):
+        x = xs[req.batch.value]
+        return EvaluatorPair(raw=DefaultMatchEvaluator(raw, x), fused=DefaultMatchEvaluator(fused, x))
+
+    slug = props.identity_and_compute.identity.slug
+    cache = FilesystemTuningCache(tmp_path, slug)
+    reqs = [TuneRequest(WeightShape(rows, cols), BatchSize(b)) for b in (1, 4, 8)]
+    tf = tune_launch(slug, reqs, evaluators, cache)
+    assert cache.load() == tf and len(tf.entries.items) == 3
+    for e in tf.entries.items:
+        x = xs[e.key.batch.value]
+        ref = o.gemv_reference(enc, x.cpu().numpy())
+        c = e.configurations
+        for cfg in (c.independent.fused, c.order_matched):
+            assert max_rel_error(fused.multiply(x, cfg), ref) <= REL_TOL
+        assert torch.equal(fused.multiply(x, c.order_matched), raw.multiply(x, c.order_matched))
+
+
 def test_tuner_writes_through_the_cache_port(gpu, tmp_path):
     from se12_amd.adapters import FilesystemTuningCache, HipGpuProbe, tune_launch
     from se12_amd.tune import gpu_evaluators, tuning_lookup

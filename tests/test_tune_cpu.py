@@ -94,7 +94,7 @@ def pair_of(raw_fn, fused_fn):
 
 def test_each_kernel_keeps_its_fastest_passing_configuration():
     req = request(2304, 9216, 1)
-    cands = candidate_configurations(2304, 9216, batch=1)
+    cands = tune.tuning_candidates(2304, 9216, 1)
     # raw fastest at the smallest block, fused at the largest
     raw = lambda r, c: RefMeasurement(float(c.threads_per_block.value), True)
     fused = lambda r, c: RefMeasurement(float(-c.threads_per_block.value), True)
@@ -120,13 +120,13 @@ def test_every_candidate_is_evaluated_for_both_kernels():
         return p
 
     tune.tune_launch("g", [req], evaluators, MemoryCache())
-    cands = list(candidate_configurations(1024, 2304, batch=4))
+    cands = list(tune.tuning_candidates(1024, 2304, 4))
     assert made[0].raw.seen == cands and made[0].fused.seen == cands
 
 
 def test_order_matched_is_the_best_combined_passing_configuration():
     req = request(1024, 2304, 4)
-    cands = candidate_configurations(1024, 2304, batch=4)
+    cands = tune.tuning_candidates(1024, 2304, 4)
     target = cands[len(cands) // 2]
     raw = lambda r, c: RefMeasurement(1.0 if c == target else 5.0, True)
     fused = lambda r, c: RefMeasurement(2.0 if c == target else 1.5, c == target or c == cands[0])
@@ -195,3 +195,33 @@ def test_other_gpus_files_are_ignored_with_a_warning(tmp_path):
 
 def test_no_directory_means_no_file(tmp_path):
     assert tune.FilesystemTuningCache(tmp_path / "missing", "g").load() is None
+
+
+def test_candidates_cover_bf16_and_fp32_activations():
+    """At 16 rows BF16 activations run an MFMA kernel and FP32 ones the dot2
+    kernel: the tuner offers both sets, BF16's first, without repeats."""
+    bf16 = candidate_configurations(2304, 9216, batch=16)
+    f32 = candidate_configurations(2304, 9216, batch=16, float32_activations=True)
+    both = tune.tuning_candidates(2304, 9216, 16)
+    assert both[:len(bf16)] == bf16 and set(both) == set(bf16) | set(f32) and len(set(both)) == len(both)
+
+
+def test_refused_configurations_count_as_failing():
+    """An evaluator whose kernel refuses a configuration (the library raises
+    for a launch its activations cannot take; the reference's evaluator does
+    not catch that) leaves the candidate failing, not the tuner crashing."""
+    from se12_amd._native import Se12Error
+
+    f32 = set(candidate_configurations(2304, 9216, batch=16, float32_activations=True))
+
+    def fn(r, c):
+        if c not in f32:
+            raise ValueError("threads_per_block 448 must be a multiple of 64 in [128, 512]")
+        if c.blocks.value % 7 == 0:
+            raise Se12Error(-2, "launch refused")
+        return RefMeasurement(float(c.threads_per_block.value + c.blocks.value), True)
+
+    tf = tune.tune_launch("g", [request(2304, 9216, 16)], pair_of(fn, fn), MemoryCache())
+    (e,) = tf.entries.items
+    for cfg in (e.configurations.independent.raw, e.configurations.independent.fused, e.configurations.order_matched):
+        assert cfg in f32 and cfg.blocks.value % 7 != 0

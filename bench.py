@@ -423,11 +423,21 @@ def stress(device) -> dict:
         st_r = timer.time_cold_rotation([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(raws, ys)], 3, 10)
         del raws
         us, us_b, us_r = st.median_us, st_b.median_us, st_r.median_us
-        lc = Se12MatVecKernel(enc, max_batch=1).default_launch(1)
+        k0 = Se12MatVecKernel(enc, max_batch=1)
+        lc = k0.default_launch(1)
+        bs = k0.bind_stats()
+        # the kernel's reads besides the format's bytes: tiles bind decoded to
+        # raw BF16 (more escapes than a side record lists) add 8,192 bytes each
+        streamed = enc.byte_size() + bs["raw_tiles"] * 8192
         out[name] = {"shape": [n, k], "us": round(us, 3), "p10_us": round(st.p10_us, 3), "p90_us": round(st.p90_us, 3),
                      "cold_copies": copies, "se12_bytes": enc.byte_size(),
                      "bytes_per_weight": round(enc.byte_size() / (n * k), 4),
                      "se12_gbps": round(enc.byte_size() / (us * 1e-6) / 1e9, 1),
+                     "bind_decoded_raw_tiles": bs["raw_tiles"],
+                     "bind_decoded_raw_bytes": bs["raw_tiles"] * 8192,
+                     "streamed_bytes": streamed,
+                     "streamed_gbps": round(streamed / (us * 1e-6) / 1e9, 1),
+                     "sidecar_bytes": bs["sidecar_bytes"],
                      "bf16_equiv_gbps": round(2 * n * k / (us * 1e-6) / 1e9, 1),
                      "bf16_hipblaslt_us": round(us_b, 3), "raw_twin_us": round(us_r, 3),
                      "speedup_of_se12": round(us_b / us, 4), "speedup_vs_faster_baseline": round(min(us_b, us_r) / us, 4),

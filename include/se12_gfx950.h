@@ -145,6 +145,15 @@ int se12_release(se12_handle* h);
 int se12_handle_shape(const se12_handle* h, int64_t* rows, int64_t* cols, int64_t* tiles,
                       int64_t* fallback_tiles, int32_t* format);
 
+/* What se12_bind derived for an SE12 handle (host only): `raw_tiles` = the
+ * tiles bind decoded once into a raw BF16 buffer of the handle because they
+ * hold more escapes than the per-tile side record lists (the kernels read
+ * those 8,192 bytes per tile besides the tile's streams); `sidecar_bytes` =
+ * the device bytes of the derived data (side records, pair table, that raw
+ * buffer). No counterpart in the reference, whose host precompute is
+ * fallback_offsets / row_escape_offset (lws/adapters/cuda/gemv.py:47-77). */
+int se12_handle_bind_stats(const se12_handle* h, int64_t* raw_tiles, int64_t* sidecar_bytes);
+
 /* The default launch for `batch` (the heuristic of
  * lws/domain/launch/heuristic.py:46-87 re-derived for 256 CUs of wave64). */
 int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out);

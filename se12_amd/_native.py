@@ -110,6 +110,7 @@ SIGNATURES = {
         c_i32,
         [c_void_p, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), ctypes.POINTER(c_i64), ctypes.POINTER(c_i32)],
     ),
+    "se12_handle_bind_stats": (c_i32, [c_void_p, ctypes.POINTER(c_i64), ctypes.POINTER(c_i64)]),
     "se12_default_launch": (c_i32, [c_void_p, c_i32, ctypes.POINTER(Launch)]),
     "se12_set_compute_units": (c_i32, [c_void_p, c_i32]),
     "se12_read_probe": (c_i32, [c_void_p, c_i64, c_void_p, c_i64, c_void_p]),

@@ -176,8 +176,9 @@ static void free_handle(se12_handle* h) {
 static int check_shape(int64_t rows, int64_t cols, int32_t max_batch) {
     if (rows <= 0 || cols <= 0) return fail(SE12_E_INVALID, "shape must be positive, got [%lld, %lld]", (long long)rows, (long long)cols);
     // tile rows index the grid's x dimension; K-tile bounds are computed in
-    // 32 bits as split * tile_cols
-    if (ceil_div(rows, SE12_TILE_ROWS) > INT32_MAX / 2 || ceil_div(cols, SE12_TILE_COLS) > (1 << 25))
+    // 32 bits as split * tile_cols; the decode kernel indexes tiles in 32 bits
+    if (ceil_div(rows, SE12_TILE_ROWS) > INT32_MAX / 2 || ceil_div(cols, SE12_TILE_COLS) > (1 << 25) ||
+        ceil_div(rows, SE12_TILE_ROWS) * ceil_div(cols, SE12_TILE_COLS) > INT32_MAX)
         return fail(SE12_E_INVALID, "shape [%lld, %lld] too large", (long long)rows, (long long)cols);
     if (max_batch < 1 || max_batch > SE12_MAX_BATCH)
         return fail(SE12_E_INVALID, "max_batch must be in [1, %d], got %d", SE12_MAX_BATCH, max_batch);
@@ -283,6 +284,17 @@ int se12_release(se12_handle* h) {
     DeviceScope ds;
     if (ds.enter(h->device) == hipSuccess) (void)hipDeviceSynchronize();
     free_handle(h);
+    return SE12_OK;
+}
+
+int se12_handle_bind_stats(const se12_handle* h, int64_t* raw_tiles, int64_t* sidecar_bytes) {
+    if (!h) return fail(SE12_E_INVALID, "se12_handle_bind_stats: NULL handle");
+    const bool se12 = h->side != nullptr;   // a raw-twin handle derives nothing
+    if (raw_tiles) *raw_tiles = se12 ? h->n_overflow : 0;
+    if (sidecar_bytes)
+        *sidecar_bytes = se12 ? h->T * (int64_t)(se12::kSideWords * sizeof(uint32_t)) + (int64_t)kLutBytes +
+                                    h->n_overflow * SE12_TILE_SIZE * (int64_t)sizeof(int16_t)
+                              : 0;
     return SE12_OK;
 }
 

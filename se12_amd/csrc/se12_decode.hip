@@ -68,38 +68,99 @@ __device__ __forceinline__ void decode_tile(const DecodeArgs& a, const uint32_t*
     decode_loaded(a, lut, side, t, lane, sink);
 }
 
+// 8 decoded weights (4 BF16 pairs) to out_row[col .. col + 8) clipped at K:
+// one 16-byte nontemporal store when the output allows it (streamed: the
+// decoded matrix is written once and read later by another kernel).
+__device__ __forceinline__ void store8(uint16_t* out_row, int64_t col, int64_t K, bool vec_ok, const uint32_t w[4]) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    if (vec_ok && col + 8 <= K) {
+        const u32x4 v = {w[0], w[1], w[2], w[3]};
+        __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out_row + col));
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (col + i < K) out_row[col + i] = (uint16_t)(w[i >> 1] >> (16 * (i & 1)));
+    }
+}
+
 // Whole-matrix decode: nw waves stream the tiles, wave g taking tiles g,
 // g + nw, ... (the waves read a moving window of the tile-major streams),
 // each with the next tile's loads in flight while it decodes and stores the
 // current one. The last tile loads nothing after it (a wave cannot end
 // before its loads land), and every load inside the loop is issued on every
 // path, so the compiler's wait counts stay exact.
+//
+// Lane layout (the half layout): part p = 0..7 of a tile covers tile rows
+// 2p and 2p + 1; lane l takes row 2p + l / 32, columns 8 (l % 32) .. + 7
+// (8 bytes of sm, 4 of ec), so each part's store instruction writes two
+// whole 512-byte row segments, 16 contiguous bytes per lane. (The fused
+// kernels' chunk layout gives each lane 16 columns, whose two 16-byte stores
+// each write alternate halves of 32-byte pieces: 2304x9216 took 19.0 us
+// with it against 15.7 here, the stores nontemporal in both; 14336x3584
+// 39.0 against 33.5.)
 __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_stream_kernel(DecodeArgs a, int64_t nw) {
     SE12_DECLARE_LUT(lut);
     const int tid = threadIdx.x;
     const uint32_t lane = tid & 63;
     const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t g = (int64_t)blockIdx.x * kDecodeWaves + w;
-    const int64_t n = g < nw && g < a.T ? (a.T - 1 - g) / nw + 1 : 0;  // tiles of this wave
+    // tile indices in 32 bits (the library refuses matrices of 2^31 tiles or
+    // more), so the per-tile division is a 32-bit one
+    const uint32_t T = (uint32_t)a.T, NW = (uint32_t)nw, TC = (uint32_t)a.TC;
+    const uint32_t g = blockIdx.x * kDecodeWaves + (uint32_t)w;
+    const uint32_t n = g < NW && g < T ? (T - 1u - g) / NW + 1u : 0u;  // tiles of this wave
     struct Slot {
         TileSide side;
-        TileLoads t;
+        HalfTileLoads t;
     };
-    auto load = [&](Slot& sl, int64_t i) {
-        const int64_t tile = std::min<int64_t>(g + i * nw, a.T - 1);
+    auto load = [&](Slot& sl, uint32_t i) {
+        const uint32_t tile = min(g + i * NW, T - 1u);
         load_side(sl.side, a.side, tile, lane);
-        load_tile(sl.t, a.sm, a.ec, tile, lane);
+        load_tile_half(sl.t, a.sm, a.ec, tile, lane);
     };
     const bool vec_ok = a.out_vec_ok != 0;
-    auto emit = [&](const Slot& sl, int64_t i) {
-        const int64_t tile = g + i * nw;
-        const int tr = (int)(tile / a.TC);
-        const int kt = (int)(tile - (int64_t)tr * a.TC);
-        const int64_t col = (int64_t)kt * kTileCols + 16 * (lane & 15u);
-        decode_loaded(a, lut, sl.side, sl.t, lane, [&](int j, const uint32_t* wv) {
-            const int64_t row = (int64_t)tr * kTileRows + 4 * j + (lane >> 4);
-            if (row < a.N) store16(a.out + row * a.K, col, a.K, vec_ok, wv);
-        });
+    auto emit = [&](const Slot& sl, uint32_t i) {
+        const uint32_t tile = g + i * NW;
+        const int tr = (int)(tile / TC);
+        const int kt = (int)(tile - (uint32_t)tr * TC);
+        const int64_t col = (int64_t)kt * kTileCols + 8 * (lane & 31u);
+        const int64_t row0 = (int64_t)tr * kTileRows + (lane >> 5);
+        const uint32_t info = side_info(sl.side, 0);
+        // wave-uniform: a tile inside the matrix whose rows take whole
+        // 16-byte stores needs no per-lane guard
+        const bool full = vec_ok && (int64_t)(tr + 1) * kTileRows <= a.N && (int64_t)(kt + 1) * kTileCols <= a.K;
+        uint16_t* const out0 = a.out + row0 * a.K + col;
+        auto put = [&](int p, const uint32_t wv[4]) {
+            if (full) {
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 v = {wv[0], wv[1], wv[2], wv[3]};
+                __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(out0 + 2 * p * a.K));
+            } else if (row0 + 2 * p < a.N) {
+                store8(a.out + (row0 + 2 * p) * a.K, col, a.K, vec_ok, wv);
+            }
+        };
+        if (info_is_fallback(info)) {
+            // a tile read as raw BF16 (tile-local row-major, like sm)
+            const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw) + 8 * lane;
+            uint4 r[8];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) r[p] = *reinterpret_cast<const uint4*>(raw + 512 * p);
+            wait_vector_loads();  // rare path: keeps the common path's waits exact
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const uint32_t wv[4] = {r[p].x, r[p].y, r[p].z, r[p].w};
+                put(p, wv);
+            }
+        } else {
+            uint32_t pat[4][8];
+            lookup_tile_half(lut, sl.t, pat);
+            patch_tile_escapes<kHalfLayout>(pat, info, sl.side, 0, lane);
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                uint32_t wv[4];
+                merge_part_half(pat, sl.t, p, wv);
+                put(p, wv);
+            }
+        }
     };
     // the pair table, then the first tile (a wave past the grid's waves
     // re-loads tile g's clamp, so that the table's wait count is exact)
@@ -109,7 +170,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_stream_kernel(Dec
     store_block_lut(lut, lutv, lane);
     lds_barrier();
     if (n == 0) return;
-    int64_t i = 0;
+    uint32_t i = 0;
     while (true) {
         if (i + 1 >= n) {
             emit(s0, i);
@@ -167,10 +228,9 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_kernel(DecodeArgs
     }
 }
 
-// waves of the whole-matrix decode per CU (MI355X, cold HBM: 2304x9216 19.0 us
-// with 4, 21.0 with 8, 20.0 with 16, 25.5 with 2, 21.3 with one wave per
-// tile; 14336x3584 38.8 / 39.9 / 40.6 / 57.3 / 41.7; the 256000x2304 LM head
-// 394 against 389 with one wave per tile)
+// waves of the whole-matrix decode per CU (MI355X, cold HBM, half layout:
+// 2304x9216 15.65 us with 4, 16.6 with 6, 15.6 with 8, 15.55 with 12;
+// 14336x3584 33.5 / 36.5 / 33.6 / 33.9)
 constexpr int kDecodeStreamWavesPerCu = 4;
 
 hipError_t launch_decode(const DecodeArgs& a, bool rows, hipStream_t stream, int cu_count) {

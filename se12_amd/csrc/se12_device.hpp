@@ -299,7 +299,11 @@ __device__ __forceinline__ void or_pattern_word(uint32_t pat[4][8], uint32_t wor
 //     (block % 4);
 //   block layout (se12_gemm_rx.hip): part = block % 4, lane row + 16 (block
 //     / 4).
-enum TileLayout { kChunkLayout, kRowLayout, kBlockLayout };
+// and one of 8 columns per lane in each of 8 parts:
+//   half layout (the decode-only kernel): part p = rows 2p, 2p+1, lane 32
+//     (row % 2) + col / 8, word (col % 8) / 2 of the part's 4, stored as
+//     pattern word 4p + word (pat[p / 2][4 (p % 2) + word]).
+enum TileLayout { kChunkLayout, kRowLayout, kBlockLayout, kHalfLayout };
 
 template <int LAYOUT>
 __device__ __forceinline__ void patch_listed_escapes(uint32_t pat[4][8], uint4 pos, uint4 esc, uint32_t n,
@@ -310,9 +314,11 @@ __device__ __forceinline__ void patch_listed_escapes(uint32_t pat[4][8], uint4 p
         const uint32_t row = (p >> 8) & 15u, col = p & 255u, block = col >> 4;
         const uint32_t owner = LAYOUT == kChunkLayout ? (((row & 3u) << 4) | block)
                                : LAYOUT == kRowLayout ? (row | ((block & 3u) << 4))
-                                                      : (row | ((block >> 2) << 4));
+                               : LAYOUT == kHalfLayout ? (((row & 1u) << 5) | (col >> 3))
+                                                       : (row | ((block >> 2) << 4));
         const uint32_t part = LAYOUT == kChunkLayout ? (row >> 2) : LAYOUT == kRowLayout ? (block >> 2) : (block & 3u);
-        const uint32_t word = (part << 3) | ((col & 15u) >> 1);
+        const uint32_t word = LAYOUT == kHalfLayout ? (((row >> 1) << 2) | ((col & 7u) >> 1))
+                                                    : ((part << 3) | ((col & 15u) >> 1));
         const uint32_t v = esc_byte(esc, k) << ((col & 1u) ? 23u : 7u);
         or_pattern_word(pat, word, lane == owner ? v : 0u);
     }
@@ -464,6 +470,47 @@ __device__ __forceinline__ float row16_sum(float v) {
     v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true));  // row_half_mirror
     v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true));  // row_mirror
     return v;
+}
+
+// The half layout's loads of one tile for one lane: part p reads 8 bytes of
+// `sm` and 4 of `ec` (512 / 256 contiguous bytes per wave instruction).
+struct HalfTileLoads {
+    uint2 sm[8];
+    uint32_t ec[8];
+};
+
+__device__ __forceinline__ void load_tile_half(HalfTileLoads& t, const uint8_t* sm, const uint8_t* ec, int64_t tile,
+                                               uint32_t lane) {
+    const uint8_t* smt = sm + tile * kTile + 8u * lane;
+    const uint8_t* ect = ec + tile * (kTile / 2) + 4u * lane;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        t.sm[p] = *reinterpret_cast<const uint2*>(smt + 512 * p);
+        t.ec[p] = *reinterpret_cast<const uint32_t*>(ect + 256 * p);
+    }
+}
+
+// The 32 pattern lookups of a tile in the half layout (pattern word 4 p + k
+// in pat[p / 2][4 (p % 2) + k]).
+__device__ __forceinline__ void lookup_tile_half(const uint32_t* lut, const HalfTileLoads& t, uint32_t pat[4][8]) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const uint32_t e = t.ec[p];
+        uint32_t* q = &pat[p >> 1][4 * (p & 1)];
+        q[0] = lut[e & 0xFFu];
+        q[1] = lut[(e >> 8) & 0xFFu];
+        q[2] = lut[(e >> 16) & 0xFFu];
+        q[3] = lut[e >> 24];
+    }
+}
+
+// The 4 BF16 pairs of part p of a tile in the half layout.
+__device__ __forceinline__ void merge_part_half(const uint32_t pat[4][8], const HalfTileLoads& t, int p, uint32_t w[4]) {
+    const uint32_t* q = &pat[p >> 1][4 * (p & 1)];
+    w[0] = merge_pair(q[0], dup_lo(t.sm[p].x));
+    w[1] = merge_pair(q[1], dup_hi(t.sm[p].x));
+    w[2] = merge_pair(q[2], dup_lo(t.sm[p].y));
+    w[3] = merge_pair(q[3], dup_hi(t.sm[p].y));
 }
 
 __device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {

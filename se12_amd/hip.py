@@ -218,6 +218,16 @@ class Se12MatVecKernel(_GemvBase):
         self.device = self.tensor.sm.device
         self.handle = bind_se12(self.tensor, max_batch)
 
+    def bind_stats(self) -> dict:
+        """What bind derived (se12_handle_bind_stats): `raw_tiles`, the tiles
+        decoded once to raw BF16 because they hold more escapes than a side
+        record lists (the kernels read their 8,192 raw bytes besides the
+        tile's streams), and `sidecar_bytes`, the device bytes of the
+        derived data."""
+        raw, side = ctypes.c_int64(), ctypes.c_int64()
+        nat.check(nat.lib().se12_handle_bind_stats(self.handle.raw, ctypes.byref(raw), ctypes.byref(side)))
+        return {"raw_tiles": int(raw.value), "sidecar_bytes": int(side.value)}
+
     def decode_into(self, out: torch.Tensor) -> torch.Tensor:
         """Decodes the whole matrix into `out` (row-major BF16 [rows, cols],
         e.g. a view of a scratch buffer shared by many layers)."""

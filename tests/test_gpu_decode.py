@@ -108,3 +108,27 @@ def test_decode_every_escape_count(gpu):
     got = HipSe12WeightDecoder().decode_rows(dt, RowIndices(tuple(rows)))
     assert np.array_equal(got.bit_pattern, bits[rows].reshape(-1))
 
+
+
+def test_bind_stats_count_the_raw_decoded_tiles(gpu):
+    """se12_handle_bind_stats: the tiles holding 9..16 escapes (more than a
+    side record lists, fewer than a fallback tile) are the ones bind decodes
+    to raw BF16; the sidecar bytes are 64 per tile, the 1 KiB pair table and
+    8 KiB per such tile. A raw-twin handle derives nothing."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+
+    bits, counts = escape_count_bf16(seed=11)
+    enc = o.encode(bits.reshape(-1), 64, 1024)
+    st = Se12MatVecKernel(to_device(enc, gpu), max_batch=1).bind_stats()
+    raw = sum(1 for n in counts if 8 < n <= 16)
+    assert raw == 5
+    assert st == {"raw_tiles": raw, "sidecar_bytes": 16 * 64 + 1024 + raw * 8192}
+    import ctypes
+
+    from se12_amd import _native as nat
+
+    w = torch.from_numpy(bits.astype(np.int16)).to(gpu).view(torch.bfloat16)
+    rk = RawBf16MatVecKernel(w, max_batch=1)
+    a, b = ctypes.c_int64(-1), ctypes.c_int64(-1)
+    nat.check(nat.lib().se12_handle_bind_stats(rk.handle.raw, ctypes.byref(a), ctypes.byref(b)))
+    assert (a.value, b.value) == (0, 0)

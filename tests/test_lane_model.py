@@ -167,3 +167,90 @@ def test_tile_info_words_on_the_golden_vectors():
             else:
                 for j in range(4):
                     assert bool(info[t] >> j & 1) == bool((codes[t, 1024 * j:1024 * (j + 1)] == 15).any())
+
+
+def listed_escapes(ec_tile: bytes) -> list[int]:
+    """Tile positions (row * 256 + column) of a tile's escape codes in
+    row-major order: the order in which they take the tile's esc slots."""
+    codes = np.frombuffer(ec_tile, dtype=np.uint8)
+    nib = np.stack([codes & 15, codes >> 4], axis=1).reshape(-1)
+    return [int(p) for p in np.nonzero(nib == 15)[0]]
+
+
+def half_layout_decode_tile(sm_tile: bytes, ec_tile: bytes, esc_tile, lut) -> np.ndarray:
+    """The decode-only kernel's half layout (se12_decode.hip): part p = 0..7
+    covers tile rows 2p, 2p + 1; lane l takes row 2p + l // 32 and columns
+    8 (l % 32) .. + 7 (8 sm bytes at 512 p + 8 l, 4 ec bytes at 256 p + 4 l).
+    Pattern word 4 p + k of a lane (k = column pair) comes from the pair
+    table; escape k of the tile's listed escapes, at (row, col), is ORed into
+    pattern word 4 (row // 2) + (col % 8) // 2 of lane 32 (row % 2) +
+    col // 8 (patch_listed_escapes, kHalfLayout), then the merge."""
+    pats = [[0] * 32 for _ in range(64)]
+    for lane in range(64):
+        for p in range(8):
+            eb = ec_tile[256 * p + 4 * lane: 256 * p + 4 * lane + 4]
+            for k in range(4):
+                pats[lane][4 * p + k] = lut[eb[k]]
+    for k, pos in enumerate(listed_escapes(ec_tile)):
+        row, col = pos >> 8, pos & 255
+        owner = ((row & 1) << 5) | (col >> 3)
+        word = ((row >> 1) << 2) | ((col & 7) >> 1)
+        pats[owner][word] |= int(esc_tile[k]) << (23 if col & 1 else 7)
+    out = np.zeros(4096, dtype=np.uint16)
+    for lane in range(64):
+        for p in range(8):
+            row, col = 2 * p + (lane >> 5), 8 * (lane & 31)
+            o_ = 512 * p + 8 * lane
+            words = [int.from_bytes(sm_tile[o_ + 4 * d: o_ + 4 * d + 4], "little") for d in range(2)]
+            assert o_ == row * 256 + col   # sm's tile-local row-major order
+            for k in range(4):
+                w = words[k >> 1]
+                dup = perm(w, w, 0x03030202 if k & 1 else 0x01010000)
+                pair = (pats[lane][4 * p + k] & 0x7F807F80) | (dup & ~0x7F807F80 & 0xFFFFFFFF)
+                out[row * 256 + col + 2 * k] = pair & 0xFFFF
+                out[row * 256 + col + 2 * k + 1] = pair >> 16
+    return out
+
+
+@pytest.mark.parametrize("name", ["normal_32x512", "mixed_48x768", "ragged_20x300", "edge_1x214"])
+def test_half_layout_reproduces_the_oracle(name):
+    """Every tile the decode kernel decodes (not raw: at most 8 escapes, not
+    a fallback tile) comes out of the half layout equal to the oracle."""
+    g = load_golden(name)
+    enc = golden_as_encoding(g)
+    tiles = o.decode_tiles(enc)
+    ntr, ntc, _ = tiles.shape
+    lut = pair_lut(enc["codebook"])
+    info = tile_info_words(enc)
+    sm, ec = enc["sm"].tobytes(), enc["ec"].tobytes()
+    checked = 0
+    for t in range(ntr * ntc):
+        ect = ec[2048 * t: 2048 * (t + 1)]
+        if info[t] >> 31 or len(listed_escapes(ect)) > 8:
+            continue
+        got = half_layout_decode_tile(sm[4096 * t: 4096 * (t + 1)], ect, enc["esc"][t], lut)
+        assert np.array_equal(got, tiles.reshape(-1, 4096)[t].view(np.uint16)), f"tile {t}"
+        checked += 1
+    assert checked > 0 or name == "edge_1x214"   # its one tile holds more than 8 escapes (read raw)
+
+
+def test_half_layout_patches_escapes_in_both_rows_of_a_part():
+    """Eight escapes spread over both rows of several parts, two in one
+    lane's 8 columns, the first and last weight of the tile."""
+    rng = np.random.default_rng(9)
+    e = rng.choice(np.arange(110, 125, dtype=np.uint8), size=4096)
+    pos = np.array([0, 257, 258, 1023, 1024 + 300, 2048 + 511, 3000, 4095])
+    e[pos] = rng.integers(1, 100, size=len(pos))
+    sign = rng.integers(0, 2, size=4096).astype(np.uint16)
+    mant = rng.integers(0, 0x80, size=4096).astype(np.uint16)
+    bits = ((sign << 15) | (e.astype(np.uint16) << 7) | mant).view(np.int16)
+    enc = o.encode(bits, 16, 256)
+    assert listed_escapes(enc["ec"].tobytes()) == sorted(pos.tolist())
+    got = half_layout_decode_tile(enc["sm"].tobytes(), enc["ec"].tobytes(), enc["esc"][0], pair_lut(enc["codebook"]))
+    assert np.array_equal(got.view(np.int16), bits)
+    # swapped esc slots (a wrong rank) are caught
+    wrong = enc["esc"][0].copy()
+    wrong[[0, 1]] = wrong[[1, 0]]
+    if wrong[0] != enc["esc"][0][0]:
+        got2 = half_layout_decode_tile(enc["sm"].tobytes(), enc["ec"].tobytes(), wrong, pair_lut(enc["codebook"]))
+        assert not np.array_equal(got2.view(np.int16), bits)

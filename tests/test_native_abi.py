@@ -71,6 +71,8 @@ def test_null_arguments_fail_with_a_message_and_no_gpu_call():
     assert "se12_gemv_rmsnorm" in nat.last_error()
     assert lib.se12_gemv_rowss(None, None, 0, 1, None, None, None, None) == nat.SE12_E_INVALID
     assert "se12_gemv_rowss" in nat.last_error()
+    assert lib.se12_handle_bind_stats(None, None, None) == nat.SE12_E_INVALID
+    assert "se12_handle_bind_stats" in nat.last_error()
 
 
 def test_bind_rejects_bad_shapes_before_touching_the_device():
@@ -88,6 +90,10 @@ def test_bind_rejects_bad_shapes_before_touching_the_device():
     s.sm_dev = 17
     assert lib.se12_bind(ctypes.byref(s), 16, 256, 1, None, ctypes.byref(h)) == nat.SE12_E_INVALID
     assert "aligned" in nat.last_error()
+    # 2^31 tiles or more (the decode kernel indexes tiles in 32 bits)
+    s.sm_dev = 16
+    assert lib.se12_bind(ctypes.byref(s), 16 << 17, 256 << 14, 1, None, ctypes.byref(h)) == nat.SE12_E_INVALID
+    assert "too large" in nat.last_error()
 
 
 def test_encoder_rejects_bad_shapes():

@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kDecodeWaves * kWave) void decode_stream_kernel(Dec
             const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw) + 8 * lane;
             uint4 r[8];
 #pragma unroll
-            for (int p = 0; p < 8; ++p) r[p] = *reinterpret_cast<const uint4*>(raw + 512 * p);
+            for (int p = 0; p < 8; ++p) r[p] = stream_load(reinterpret_cast<const uint4*>(raw + 512 * p));
             wait_vector_loads();  // rare path: keeps the common path's waits exact
 #pragma unroll
             for (int p = 0; p < 8; ++p) {

@@ -517,10 +517,27 @@ def roofline_model(device, props, per_shape: dict) -> dict:
     from se12_amd.hip import HipBenchmarkTimer, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
 
     timer = HipBenchmarkTimer(device.index)
-    facts = rl.DeviceFacts(hbm_peak_gbps=props.hbm_peak_gbps, copy_gbps=timer.measure_copy_traffic_gbps(),
-                           stream_read_gbps=timer.measure_stream_read_bandwidth(),
-                           launch_us=timer.measure_graph_launch_us())
     gen = torch.Generator(device=device)
+    # the streaming-read bandwidth: the faster of the library's grid-stride
+    # read probe and the fused product's own stream over a cold 256000x2304
+    # matrix at batch 1 (its tile-order reads go faster than any grid-stride
+    # form), so that no product launch can beat the model's bandwidth
+    probe_gbps = timer.measure_stream_read_bandwidth()
+    gen.manual_seed(78)
+    n_lm, k_lm = 256000, 2304
+    lm = []
+    for _ in range(2):
+        w = (torch.randn((n_lm, k_lm), generator=gen, device=device) * 0.02).to(torch.bfloat16)
+        lm.append(Se12MatVecKernel(encode_on_device(w), max_batch=1))
+        del w
+    x_lm = torch.randn((1, k_lm), generator=gen, device=device).to(torch.bfloat16)
+    y_lm = torch.empty((1, n_lm), dtype=torch.float32, device=device)
+    st_lm = timer.time_cold_rotation([lambda kk=kk: kk.multiply(x_lm, out=y_lm) for kk in lm], 3, 10)
+    lm_gbps = (lm[0].tensor.byte_size() + k_lm * 2 + n_lm * 4) / (st_lm.median_us * 1e-6) / 1e9
+    del lm, y_lm
+    torch.cuda.empty_cache()
+    facts = rl.DeviceFacts(hbm_peak_gbps=props.hbm_peak_gbps, copy_gbps=timer.measure_copy_traffic_gbps(),
+                           stream_read_gbps=max(probe_gbps, lm_gbps), launch_us=timer.measure_graph_launch_us())
     gen.manual_seed(77)
     hot = {"raw": [], "se12": []}
     for n, k in rl.CALIBRATION_SHAPES:
@@ -541,6 +558,8 @@ def roofline_model(device, props, per_shape: dict) -> dict:
         shapes[name] = {kk: round(v, 4) for kk, v in rep.items()}
         shapes[name]["launch_floor_us"] = round(rl.launch_floor_us(*e["shape"], facts), 3)
     out = {"facts": {kk: round(v, 3) for kk, v in dataclasses.asdict(facts).items()},
+           "stream_read": {"probe_gbps": round(probe_gbps, 1), "fused_lm_head_256000x2304_gbps": round(lm_gbps, 1),
+                           "fused_lm_head_us": round(st_lm.median_us, 3)},
            "hbm_peak_published_gbps": rl.HBM_PEAK_PUBLISHED_GBPS,
            "calibration": {"shapes": [list(sh) for sh in rl.CALIBRATION_SHAPES], "batch": 1,
                            "raw_hot_us": [round(v, 3) for v in hot["raw"]],

@@ -10,21 +10,27 @@
 
 namespace {
 
+// 8 loads in flight per thread, nontemporal (each line is read once), 2
+// blocks of 512 threads per CU: the fastest of the grid-stride forms
+// measured on MI355X over 1 GiB buffers (6.09 TB/s, against 5.28-5.80 with
+// plain loads and 5.5-6.0 with other unrolls and block counts).
 constexpr int kProbeUnroll = 8;
 constexpr int kProbeThreads = 512;
-constexpr int kProbeBlocksPerCu = 8;
+constexpr int kProbeBlocksPerCu = 2;
 
 __global__ __launch_bounds__(kProbeThreads) void read_probe_kernel(const uint4* __restrict__ p, int64_t n16,
                                                                    uint32_t* __restrict__ out) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    const u32x4* q = reinterpret_cast<const u32x4*>(p);
     uint32_t acc = 0;
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     for (; i + (kProbeUnroll - 1) * stride < n16; i += kProbeUnroll * stride) {
-        uint4 v[kProbeUnroll];
+        u32x4 v[kProbeUnroll];
 #pragma unroll
-        for (int u = 0; u < kProbeUnroll; ++u) v[u] = p[i + u * stride];
+        for (int u = 0; u < kProbeUnroll; ++u) v[u] = __builtin_nontemporal_load(q + i + u * stride);
 #pragma unroll
-        for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        for (int u = 0; u < kProbeUnroll; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
     }
     for (; i < n16; i += stride) {
         const uint4 v = p[i];

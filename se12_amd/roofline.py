@@ -13,9 +13,16 @@ with eta (overlap efficiency) fitted from a measured raw-kernel latency only,
 so the fused kernel's predicted ratio is an out-of-sample test
 (roofline.py:1-12,77-91). Where the inputs come from here:
 
-- BW: the measured device-to-device copy bandwidth (read + write counted),
-  the reference's calibration bandwidth (adapters/cuda/calibration_probe.py:
-  40-42); the streaming-read bandwidth is measured beside it;
+- BW: the HBM traffic of a device-to-device copy (read + write counted).
+  The reference calibrates with its copy bandwidth with the copied bytes
+  counted once (adapters/cuda/calibration_probe.py:38-40, benchmark_timer.py:
+  55-66), about a third of what a read-only pass streams here; with the
+  traffic figure the fitted model predicts the fused / raw ratios of the
+  Gemma-2-2B shapes within 5-20%, with the fastest streaming read (6.4 TB/s)
+  it puts every shape compute-bound and misses by up to 44%. The streaming
+  read bandwidth, the larger of a grid-stride read probe and the fused
+  product's own stream over a cold LM head, is measured beside it and bounds
+  each launch from below (launch_floor_us);
 - c(format, B): each kernel's time per weight on cache-resident data, as the
   reference defines it (calibration_probe.py:44-63), but as the slope
   between two matrices that fill the GPU and stay in the 256 MB Infinity
@@ -61,7 +68,7 @@ class DeviceFacts:
 
     hbm_peak_gbps: float          # memory clock x transfers per clock x bus width
     copy_gbps: float              # device-to-device copy, read + write counted
-    stream_read_gbps: float       # streaming read of a buffer over 4x L2 + Infinity Cache
+    stream_read_gbps: float       # the fastest streaming read measured (cold, over 4x L2 + Infinity Cache)
     launch_us: float              # one small kernel node of a HIP graph
 
 
@@ -151,7 +158,8 @@ def predict_shape_ratio(rows: int, cols: int, cal: Calibration, eta: float, exac
 
 def launch_floor_us(rows: int, cols: int, facts: DeviceFacts, batch: int = 1) -> float:
     """Lower bound of one fused launch on this GPU: the streams, x and y at
-    the measured streaming-read bandwidth plus one graph launch."""
+    the fastest streaming-read bandwidth measured on it, plus one graph
+    launch."""
     nbytes = packed_byte_size(rows, cols, 0) + batch * cols * 2 + batch * rows * 4
     return facts.launch_us + nbytes / (facts.stream_read_gbps * BYTES_PER_US_PER_GBPS)
 

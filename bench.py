@@ -90,6 +90,9 @@ def parse_args(argv=None):
                         "hardware-counter runs of one kernel")
     p.add_argument("--profile-shape", default="14336x3584", metavar="NxK",
                    help="the matrix shape of --profile-batch (default 14336x3584)")
+    p.add_argument("--profile-blas", default=None, metavar="NxK",
+                   help="only hipBLASLt's BF16 product (F.linear) at batch 1 on an NxK matrix (rotation of cold "
+                        "matrices), then a 256 MiB device copy of known size, for hardware-counter runs of the baseline")
     p.add_argument("--profile-e2e", choices=("se12", "raw", "bf16"), default=None,
                    help="only the Gemma-2-2B decode of one backend: prefill 512, capture, a 0.5 s pause, 32 graph-"
                         "replayed steps (kernel traces of the decode step)")
@@ -155,6 +158,33 @@ def profile_down(args, device) -> int:
     print(json.dumps({"profile": "down_proj 2304x9216 fused GEMV", "us_per_launch": round(ms * 1e3 / len(down), 3),
                       "launches": len(down) * (args.steps + args.warmup + 2), "copy_bytes": src.numel() * 4,
                       "copies": 3}), flush=True)
+    return 0
+
+
+def profile_blas(args, device) -> int:
+    """hipBLASLt's BF16 product (F.linear, batch 1) alone at one shape, over a
+    rotation of distinct BF16 matrices of more than 1 GB so that every launch
+    streams from HBM, then the 256 MiB device copy that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters (as --profile-down)."""
+    n, k = (int(v) for v in args.profile_blas.split("x"))
+    gen = torch.Generator(device=device)
+    ws = []
+    for r in range(cold_rotation(2 * n * k)):
+        gen.manual_seed(r)
+        ws.append((torch.randn((n, k), generator=gen, device=device) * 0.02).to(torch.bfloat16))
+    gen.manual_seed(99)
+    x = torch.randn((1, k), generator=gen, device=device).to(torch.bfloat16)
+    g = capture(lambda: [torch.nn.functional.linear(x, w) for w in ws])
+    ms = time_graph(g, args.steps, args.warmup)
+    src = torch.empty(64 << 20, dtype=torch.float32, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"profile": f"hipBLASLt BF16 product {n}x{k} at batch 1", "us_per_launch": round(ms * 1e3 / len(ws), 3),
+                      "launches": len(ws) * (args.steps + args.warmup + 2), "bf16_bytes": 2 * n * k,
+                      "copy_bytes": src.numel() * 4, "copies": 3}), flush=True)
     return 0
 
 
@@ -651,6 +681,8 @@ def main(argv=None) -> int:
     torch.cuda.set_device(dev)
     if args.profile_down:
         return profile_down(args, dev)
+    if args.profile_blas:
+        return profile_blas(args, dev)
     if args.profile_batch is not None:
         if not 1 <= args.profile_batch <= 32:
             raise SystemExit("--profile-batch takes a batch in 1..32")

@@ -536,14 +536,22 @@ static GemvPlan plan_gemv(int64_t tr, int64_t tc, bool raw, int32_t bl, bool xf3
     return p;
 }
 
-static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool generic, int32_t waves, int32_t splits) {
+static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool generic, int32_t waves, int32_t splits,
+                          int32_t tile_cols, int64_t lds_per_block) {
     GemvPlan p{};
     p.batch = batch;
     p.raw = raw;
     p.generic = generic;
     p.waves = waves;
     p.blocks = (int32_t)(row_blocks * splits);
-    p.lds = gemm_lds_bytes(waves, batch);
+    // steps of a wave: its K group's share of the split's K tiles
+    const int32_t kgroups = std::max(1, waves / gemm_min_waves(batch));
+    const int64_t steps = ceil_div(ceil_div(tile_cols, splits), kgroups);
+    p.slab_ring = !generic && steps >= kGemmSlabRingMinSteps &&
+                          (int64_t)(gemm_lds_bytes(waves, batch, kGemmSlabRing) + kLutBytes) <= lds_per_block
+                      ? kGemmSlabRing
+                      : 0;
+    p.lds = gemm_lds_bytes(waves, batch, p.slab_ring);
     p.g = 1;
     p.pf = 1;
     return p;
@@ -866,7 +874,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         for (int32_t i = count; i <= kMaxGroup; ++i) g.tr_start[i] = start;
         const bool gen = generic || !aligned16(g.m[0].x);
         GemvPlan p = rx     ? plan_rx(raw, bl, rx_rows, rx_splits, waves, rx_blocks, rx_k, rx_lds)
-                     : mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits)
+                     : mfma ? plan_gemm(grid_rows, raw, bl, gen, waves, splits, h0->TC, h0->lds_per_block)
                             : plan_gemv(tr_total, h0->TC, raw, bl, xf32, gen, waves, splits);
         if (fuse_pro) {
             g.pro = *pro;

@@ -488,6 +488,27 @@ __device__ __forceinline__ void chunks_to_blocks(TileLoads& t) {
     }
 }
 
+// Raw BF16 rows in the block layout (the raw twin): lane l, part p = row
+// l % 16, columns 16 (4 (l / 16) + p) .. + 15, as two 16-byte loads.
+__device__ __forceinline__ void load_raw_blocks(uint4 r[4][2], const uint16_t* wraw, int64_t K, int tr, int kt,
+                                                uint32_t lane) {
+    const uint16_t* p = wraw + ((int64_t)tr * kTileRows + (lane & 15u)) * K + (int64_t)kt * kTileCols + 64 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        r[j][0] = reinterpret_cast<const uint4*>(p + 16 * j)[0];
+        r[j][1] = reinterpret_cast<const uint4*>(p + 16 * j)[1];
+    }
+}
+
+// Part p of a raw tile (fallback or bind-decoded; tile-local row-major) in
+// the block layout.
+__device__ __forceinline__ void raw_block_part(const int16_t* tile_raw, int p, uint32_t lane, uint32_t w[8]) {
+    const uint4* q = reinterpret_cast<const uint4*>(tile_raw + (lane & 15u) * kTileCols + 64 * (lane >> 4) + 16 * p);
+    const uint4 a = q[0], b = q[1];
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
 // The block layout's first column of part p for a lane: 16 (4 (l / 16) + p).
 __device__ __forceinline__ int block_layout_col(int p, uint32_t lane) { return 16 * (4 * (int)(lane >> 4) + p); }
 

@@ -14,25 +14,32 @@
 // spans the tallest matrix; blocks past a shorter one's rows leave at once).
 //
 // Per step each K group's waves share one copy of their x slab (batch rows x
-// 256 columns, BF16) in LDS, double-buffered: every thread requests up to 4
-// pieces of 16 bytes of the slabs of step i + 2 while its wave decodes tile
-// i and writes those of step i + 1 to the other buffer after its MFMAs; the
-// block meets once per step. Each wave requests its tile streams two tiles
-// ahead of the decode (the edge-handling variants load and use in turn).
+// 256 columns, BF16) in LDS: every thread requests up to 4 pieces of 16
+// bytes of a later step's slabs while its wave decodes tile i and writes
+// them to LDS after its MFMAs. Double-buffered with a block barrier per step
+// (slabs of step i + 1 written during step i), or, on launches of 12 or more
+// steps where LDS holds it, a ring of 8 slabs written 4 steps ahead with a
+// barrier every 4 steps. Each wave requests its tile streams two tiles ahead
+// of the decode (the edge-handling variants load and use in turn).
 //
-// A wave decodes its 16x256 tile in four parts of 64 columns, lane l taking
-// row l % 16 and the 16 columns 64 p + 16 (l / 16) .. + 15 of part p (the
-// same per-weight decode as the dot2 kernel: pair table, listed escapes, raw
-// tiles). Two lane-row swaps (v_permlane16_swap, v_permlane32_swap) then
-// leave each lane holding exactly its A operands of v_mfma_f32_16x16x32_bf16
-// for the part's two 32-column slices s (lane l: weight row l % 16, columns
-// 32 s + 8 (l / 16) .. + 7), so the decoded tile never goes through memory.
-// The B operand is the x slab (lane l: batch row 16 g + l % 16, the same
-// columns). 8 MFMAs per tile and group of 16 batch rows, FP32 accumulate, in
-// ascending slice order. Rows of the LDS x slabs are padded to 528 bytes so
-// that the 16-byte reads of 8 lanes per cycle hit distinct banks. Batch rows
-// past the batch in a 16-row group read stale LDS: MFMA output column n
-// depends on B column n only, and those columns are not stored.
+// FAST variants load each tile whole-line (a kilobyte of sm holding 4 tile
+// rows per load instruction, as the resident-x kernel does) and move it into
+// the block layout with DPP exchanges: lane l holds, in part p, the 16
+// columns 16 (4 (l / 16) + p) .. + 15 of row l % 16, decoded through the
+// pair table with listed escapes and raw tiles. Each part's first and second
+// 8 columns are the A operands of two v_mfma_f32_16x16x32_bf16 (MFMA row =
+// tile row); their K positions differ between lane groups, and the B
+// operands (lane l: batch row 16 g + l % 16) read the same 8 columns of the
+// x slab. GENERIC variants load row-wise: lane l takes row l % 16 and the 16
+// columns 64 p + 16 (l / 16) .. + 15 of part p, and two lane-row swaps
+// (v_permlane16_swap, v_permlane32_swap) leave each lane holding its A
+// operands for the part's two 32-column slices s (lane l: columns 32 s + 8
+// (l / 16) .. + 7). Either way the decoded tile never goes through memory;
+// 8 MFMAs per tile and group of 16 batch rows, FP32 accumulate, in a fixed
+// order. Rows of the LDS x slabs are padded to 528 bytes so that the 16-byte
+// reads of 8 lanes per cycle hit distinct banks. Batch rows past the batch
+// in a 16-row group read stale LDS: MFMA output column n depends on B column
+// n only, and those columns are not stored.
 //
 // A wave adds its K tiles in ascending order; the K groups of a tile row are
 // added in LDS in ascending group order by the group-0 wave, and for S > 1
@@ -216,6 +223,26 @@ __device__ __forceinline__ void mfma_part(const bf16x8_t& a0, const bf16x8_t& a1
     }
 }
 
+// The MFMAs of part p of a tile in the block layout (FAST variants; lane l
+// holds row l % 16, columns 16 (4 (l / 16) + p) .. + 15 as 8 BF16 pairs):
+// its first and second 8 columns are the A operands of two MFMAs whose B
+// operands are the same 8 columns of the x slab (batch row 16 g + l % 16).
+// The MFMA's K positions differ between lane groups; A and B agree on them.
+template <int BG>
+__device__ __forceinline__ void mfma_block_part(const uint32_t w[8], const char* xb, int p, uint32_t lane,
+                                                floatx4_t acc[BG]) {
+    const int off = (int)(lane & 15u) * kRowBytes + 128 * (int)(lane >> 4) + 32 * p;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, make_uint4(w[4 * h], w[4 * h + 1], w[4 * h + 2], w[4 * h + 3]));
+#pragma unroll
+        for (int g = 0; g < BG; ++g) {
+            const uint4 bv = *reinterpret_cast<const uint4*>(xb + g * 16 * kRowBytes + off + 16 * h);
+            acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, __builtin_bit_cast(bf16x8_t, bv), acc[g], 0, 0, 0);
+        }
+    }
+}
+
 template <bool RAW>
 struct GemmTile {
     TileSide side;
@@ -223,9 +250,10 @@ struct GemmTile {
     uint4 r[RAW ? 4 : 1][2];
 };
 
-template <int BG, bool RAW, bool GENERIC>
+template <int BG, bool RAW, bool GENERIC, int M>
 __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads) void gemm_kernel(GemvGroupArgs ga,
                                                                                                   int batch) {
+    static_assert(M == 0 || (!GENERIC && M >= 1), "the slab ring serves the FAST variants");
     SE12_DECLARE_LUT(lut);
     extern __shared__ __attribute__((aligned(16))) char gsm[];
     // the matrix comes from the grid; every argument the block needs goes out
@@ -254,7 +282,10 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     const int steps = (n + KG - 1) / KG;  // K group kg takes the split's tiles kg, kg + KG, ...
     const int64_t row_tiles = (int64_t)trl * a.TC;
     const int slab_bytes = x_slab_bytes<BG>();
-    char* xbuf = gsm;  // [2 buffers][KG slabs]
+    // [NB buffers][KG slabs] of x: two with a block barrier per step, or a
+    // ring of 2 M with a barrier every M steps
+    constexpr int NB = M > 0 ? 2 * M : 2;
+    char* xbuf = gsm;
 
     floatx4_t acc[BG];
 #pragma unroll
@@ -263,30 +294,65 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     auto load_tile_i = [&](GemmTile<RAW>& t, int i) {
         const int j = kg + KG * i;
         const int kt = kb + (j < n ? j : n - 1);
-        if constexpr (RAW) {
-            load_raw_rows<GENERIC>(t.r, a, trl, kt, lane);
-        } else {
+        if constexpr (RAW && GENERIC) {
+            load_raw_rows<true>(t.r, a, trl, kt, lane);
+        } else if constexpr (RAW) {
+            load_raw_blocks(t.r, a.wraw, a.K, trl, kt, lane);
+        } else if constexpr (GENERIC) {
             load_side(t.side, a.side, row_tiles + kt, lane);
             load_tile_rows(t.t, a.sm, a.ec, row_tiles + kt, lane);
+        } else {
+            load_tile_block_order(t.t, t.side, a.sm, a.ec, a.side, row_tiles + kt, lane);
         }
     };
-    auto use_tile = [&](const GemmTile<RAW>& t, int i) {
+    auto use_tile = [&](GemmTile<RAW>& t, int i) {
         const int kt = kb + kg + KG * i;
-        const int lim = GENERIC ? (int)(a.K - (int64_t)kt * kTileCols) : kTileCols;
-        const char* xb = xbuf + ((i & 1) * KG + kg) * slab_bytes;
-        // one part: weights (row layout) -> A operands -> the part's MFMAs
-        auto part = [&](int p, uint32_t wv[8]) {
-            if constexpr (GENERIC) zero_past_k(wv, row_layout_col(p, lane), lim);
-            bf16x8_t a0, a1;
-            rows_to_operands(wv, a0, a1);
-            mfma_part<BG>(a0, a1, xb, p, lane, acc);
-        };
-        if constexpr (RAW) {
+        const char* xb = xbuf + ((i % NB) * KG + kg) * slab_bytes;
+        if constexpr (GENERIC) {
+            const int lim = (int)(a.K - (int64_t)kt * kTileCols);
+            // one part: weights (row layout) -> A operands -> the part's MFMAs
+            auto part = [&](int p, uint32_t wv[8]) {
+                zero_past_k(wv, row_layout_col(p, lane), lim);
+                bf16x8_t a0, a1;
+                rows_to_operands(wv, a0, a1);
+                mfma_part<BG>(a0, a1, xb, p, lane, acc);
+            };
+            if constexpr (RAW) {
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    uint32_t wv[8] = {t.r[p][0].x, t.r[p][0].y, t.r[p][0].z, t.r[p][0].w,
+                                      t.r[p][1].x, t.r[p][1].y, t.r[p][1].z, t.r[p][1].w};
+                    part(p, wv);
+                }
+            } else {
+                const uint32_t info = side_info(t.side, 0);
+                if (info_is_fallback(info)) {
+                    const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
+                    uint32_t wv[4][8];
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) load_raw_part(raw, p, lane, wv[p]);
+                    wait_vector_loads();  // rare path: keeps the common path's waits exact
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) part(p, wv[p]);
+                } else {
+                    uint32_t pat[4][8];
+                    lookup_tile(lut, t.t, pat);
+                    patch_tile_escapes<kRowLayout>(pat, info, t.side, 0, lane);
+#pragma unroll
+                    for (int p = 0; p < 4; ++p) {
+                        uint32_t wv[8];
+                        merge_chunk(pat[p], t.t.sm[p], wv);
+                        part(p, wv);
+                    }
+                }
+            }
+        } else if constexpr (RAW) {
+            // block layout: each part's 16 columns are the A operands as loaded
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                uint32_t wv[8] = {t.r[p][0].x, t.r[p][0].y, t.r[p][0].z, t.r[p][0].w,
-                                  t.r[p][1].x, t.r[p][1].y, t.r[p][1].z, t.r[p][1].w};
-                part(p, wv);
+                const uint32_t wv[8] = {t.r[p][0].x, t.r[p][0].y, t.r[p][0].z, t.r[p][0].w,
+                                        t.r[p][1].x, t.r[p][1].y, t.r[p][1].z, t.r[p][1].w};
+                mfma_block_part<BG>(wv, xb, p, lane, acc);
             }
         } else {
             const uint32_t info = side_info(t.side, 0);
@@ -294,20 +360,27 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
                 const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
                 uint32_t wv[4][8];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) load_raw_part(raw, p, lane, wv[p]);
+                for (int p = 0; p < 4; ++p) raw_block_part(raw, p, lane, wv[p]);
                 wait_vector_loads();  // rare path: keeps the common path's waits exact
 #pragma unroll
-                for (int p = 0; p < 4; ++p) part(p, wv[p]);
+                for (int p = 0; p < 4; ++p) mfma_block_part<BG>(wv[p], xb, p, lane, acc);
             } else {
-                uint32_t pat[4][8];
-                lookup_tile(lut, t.t, pat);
-                patch_tile_escapes<kRowLayout>(pat, info, t.side, 0, lane);
+                // whole-line loads (4 tile rows per instruction) into the block
+                // layout, in place (the slot is reloaded next); each part's
+                // patterns merged with its sm bytes as soon as looked up;
+                // escapes only set exponent bits, which the merge takes from
+                // the patterns, so they patch the merged words
+                chunks_to_blocks(t.t);
+                uint32_t wv[4][8];
 #pragma unroll
                 for (int p = 0; p < 4; ++p) {
-                    uint32_t wv[8];
-                    merge_chunk(pat[p], t.t.sm[p], wv);
-                    part(p, wv);
+                    uint32_t pat[8];
+                    lookup_chunk(lut, t.t.ec[p], pat);
+                    merge_chunk(pat, t.t.sm[p], wv[p]);
                 }
+                patch_tile_escapes<kBlockLayout>(wv, info, t.side, 0, lane);
+#pragma unroll
+                for (int p = 0; p < 4; ++p) mfma_block_part<BG>(wv[p], xb, p, lane, acc);
             }
         }
     };
@@ -328,7 +401,48 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     constexpr int D = GENERIC ? 1 : 3;
     auto x_step = [&](int i) { return load_x_slab<GENERIC>(a, batch, kb, n, KG, i, tid, threads); };
     auto has_tile = [&](int i) { return kg + KG * i < n; };
-    if constexpr (D == 3) {
+    if constexpr (M > 0) {
+        // Slab ring: the slabs of step j sit in buffer j % NB (NB = 2 M);
+        // every thread stores its pieces of the slabs of step j during step
+        // j - M (pieces requested one step before; the prologue stores steps
+        // 0 .. M - 1), and the block meets only before steps M, 2 M, ...
+        // Slab j is read at step j after the meeting before the multiple of M
+        // in (j - M, j], so after every wave's store of it; storing slab j
+        // during step j - M overwrites slab j - 2 M, which every wave read
+        // before the meeting before the multiple of M in (j - 2 M, j - M].
+        // Fewer meetings let the waves' tile
+        // arrivals even out (14336x3584 B = 32: 24.5 us against 26.0 with one
+        // per step).
+        constexpr int L = M;
+        auto buf = [&](int j) { return xbuf + (j % NB) * KG * slab_bytes; };
+        GemmTile<RAW> t0, t1, t2;
+        load_tile_i(t0, 0);
+        load_tile_i(t1, 1);
+        XPieces xp[L];
+#pragma unroll
+        for (int j = 0; j < L; ++j) xp[j] = x_step(j);
+        XPieces x0 = x_step(L), x1, x2;
+        if constexpr (!RAW) store_block_lut(lut, lutv, lane);
+#pragma unroll
+        for (int j = 0; j < L; ++j) store_x_slab(buf(j), slab_bytes, xp[j], batch, KG, tid, threads);
+        lds_barrier();  // the pair table and the slabs of steps 0 .. L - 1 are in LDS
+        auto step = [&](GemmTile<RAW>& cur, GemmTile<RAW>& ahead, const XPieces& x_next, XPieces& x_ahead, int i) {
+            x_ahead = x_step(i + L + 1);
+            load_tile_i(ahead, i + 2);
+            if (i > 0 && i % M == 0) lds_barrier();
+            if (has_tile(i)) use_tile(cur, i);  // an idle wave decodes row trl; its sums are dropped
+            store_x_slab(buf(i + L), slab_bytes, x_next, batch, KG, tid, threads);
+        };
+        int i = 0;
+        while (true) {
+            step(t0, t2, x0, x1, i);
+            if (++i >= steps) break;
+            step(t1, t0, x1, x2, i);
+            if (++i >= steps) break;
+            step(t2, t1, x2, x0, i);
+            if (++i >= steps) break;
+        }
+    } else if constexpr (D == 3) {
         GemmTile<RAW> t0, t1, t2;
         load_tile_i(t0, 0);
         XPieces x0 = x_step(0);
@@ -338,7 +452,7 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
         if constexpr (!RAW) store_block_lut(lut, lutv, lane);
         store_x_slab(xbuf, slab_bytes, x0, batch, KG, tid, threads);
         lds_barrier();
-        auto step = [&](const GemmTile<RAW>& cur, GemmTile<RAW>& ahead, const XPieces& x_next, XPieces& x_ahead,
+        auto step = [&](GemmTile<RAW>& cur, GemmTile<RAW>& ahead, const XPieces& x_next, XPieces& x_ahead,
                         int i) {
             x_ahead = x_step(i + 2);
             load_tile_i(ahead, i + 2);
@@ -375,7 +489,10 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
     // through LDS (the x slabs are no longer read: every wave passed the
     // last step's barrier), which adds them in ascending group order
     if (KG > 1) {
-        float* red = reinterpret_cast<float*>(gsm);  // [KG - 1][R][64 lanes][BG][4]
+        // [KG - 1][R][64 lanes][BG][4]: over the x slabs, which every wave
+        // has passed the last barrier of, or past the slab ring, whose last
+        // slabs other waves may still read
+        float* red = reinterpret_cast<float*>(gsm + (M > 0 ? NB * KG * slab_bytes : 0));
         const int rw = w - kg * R;
         if (kg > 0) {
 #pragma unroll
@@ -443,19 +560,22 @@ template <int BG, bool RAW>
 hipError_t gemm_b(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream) {
     const dim3 grid(group_grid_x(a), a.m[0].S, a.count), block(p.waves * 64);
     if (p.generic)
-        hipLaunchKernelGGL((gemm_kernel<BG, RAW, true>), grid, block, p.lds, stream, a, batch);
+        hipLaunchKernelGGL((gemm_kernel<BG, RAW, true, 0>), grid, block, p.lds, stream, a, batch);
+    else if (p.slab_ring == kGemmSlabRing)
+        hipLaunchKernelGGL((gemm_kernel<BG, RAW, false, kGemmSlabRing>), grid, block, p.lds, stream, a, batch);
     else
-        hipLaunchKernelGGL((gemm_kernel<BG, RAW, false>), grid, block, p.lds, stream, a, batch);
+        hipLaunchKernelGGL((gemm_kernel<BG, RAW, false, 0>), grid, block, p.lds, stream, a, batch);
     return hipGetLastError();
 }
 
 }  // namespace
 
-size_t gemm_lds_bytes(int waves, int batch) {
+size_t gemm_lds_bytes(int waves, int batch, int slab_ring) {
     const int bg = batch > 16 ? 2 : 1;
     const int rows = gemm_min_waves(batch), kgroups = std::max(1, waves / rows);
-    const size_t slabs = (size_t)2 * kgroups * 16 * bg * kRowBytes;
     const size_t sums = (size_t)(kgroups - 1) * rows * 64 * bg * 4 * sizeof(float);
+    if (slab_ring > 0) return (size_t)2 * slab_ring * kgroups * 16 * bg * kRowBytes + sums;
+    const size_t slabs = (size_t)2 * kgroups * 16 * bg * kRowBytes;
     return std::max(slabs, sums);
 }
 

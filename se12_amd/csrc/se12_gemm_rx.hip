@@ -73,28 +73,6 @@ struct RxTile {
     uint4 xg[XG ? 8 : 1];  // batch group 1's B operands (x from global memory)
 };
 
-// Part p of a tile's sm (ec) is its contiguous kilobyte (512 bytes) of rows
-// 4p..4p+3, loaded whole by one instruction: lane l takes column block l / 4
-// of row 4p + l % 4. Full cache lines, in order, per load.
-// raw BF16 twin: lane l, part p = row l % 16, block 4 (l / 16) + p
-__device__ __forceinline__ void rx_load_raw_blocks(uint4 r[4][2], const uint16_t* wraw, int64_t K, int tr, int kt,
-                                                   uint32_t lane) {
-    const uint16_t* p = wraw + ((int64_t)tr * kTileRows + (lane & 15u)) * K + (int64_t)kt * kTileCols + 64 * (lane >> 4);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        r[j][0] = reinterpret_cast<const uint4*>(p + 16 * j)[0];
-        r[j][1] = reinterpret_cast<const uint4*>(p + 16 * j)[1];
-    }
-}
-
-// a raw tile (fallback or overflow) in the block layout
-__device__ __forceinline__ void rx_raw_part(const int16_t* tile_raw, int p, uint32_t lane, uint32_t w[8]) {
-    const uint4* q = reinterpret_cast<const uint4*>(tile_raw + (lane & 15u) * kTileCols + 64 * (lane >> 4) + 16 * p);
-    const uint4 a = q[0], b = q[1];
-    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-}
-
 }  // namespace
 
 // byte offset in the resident x of piece q (8 columns) of batch row b
@@ -160,7 +138,7 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
     auto load = [&](RxTile<RAW, XG>& t, const Cursor& c) {
         const int tr = row_of(c), kt = c.kt;
         if constexpr (RAW) {
-            rx_load_raw_blocks(t.r, a.wraw, a.K, tr, kt, lane);
+            load_raw_blocks(t.r, a.wraw, a.K, tr, kt, lane);
         } else {
             load_tile_block_order(t.t, t.side, a.sm, a.ec, a.side, (int64_t)tr * TC + kt, lane);
         }
@@ -354,7 +332,7 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
                 const int16_t* raw = raw_tile_ptr(info, a.fb_raw, a.ovf_raw);
                 uint32_t wv[4][8];
 #pragma unroll
-                for (int p = 0; p < 4; ++p) rx_raw_part(raw, p, lane, wv[p]);
+                for (int p = 0; p < 4; ++p) raw_block_part(raw, p, lane, wv[p]);
                 wait_vector_loads();  // rare path: keeps the common path's waits exact
 #pragma unroll
                 for (int p = 0; p < 4; ++p) mfma_part(wv[p], kt, p, t.xg);

@@ -131,6 +131,7 @@ struct GemvPlan {
     size_t lds;
     int xg;       // resident-x kernel: batch group 1's x from global memory (0 / 1)
     int ksplits;  // resident-x kernel: K splits (grid y), each holding its columns of x
+    int slab_ring;  // x-slab kernel: steps between block barriers (0: one per step)
 };
 
 struct DecodeArgs {
@@ -230,7 +231,18 @@ constexpr int gemm_min_waves(int batch) {
                                                                             : (batch * 32 + 64 * kGemmXPieces - 1) /
                                                                                   (64 * kGemmXPieces);
 }
-size_t gemm_lds_bytes(int waves, int batch);
+// The FAST variants' x slabs on launches of kGemmSlabRingMinSteps or more
+// steps, where LDS allows: a ring of 2 M buffers per K group (M =
+// kGemmSlabRing), each step's slab stored M steps before its use and one
+// block barrier every M steps (se12_gemm.hip); otherwise two buffers and a
+// barrier per step (slab_ring 0). Shorter launches keep the short prologue
+// (2304x9216 B = 16, 6 steps: 17.0 us with a barrier per step against 17.8
+// with the ring), and so do launches whose ring of 8 does not fit (a ring of
+// 4 with two K groups was slower than a barrier per step: 4608x36864 B = 24
+// / 32 78.4 / 81.5 us against 76.3 / 79.8).
+constexpr int kGemmSlabRing = 4;
+constexpr int kGemmSlabRingMinSteps = 12;
+size_t gemm_lds_bytes(int waves, int batch, int slab_ring);
 hipError_t launch_gemm(const GemvGroupArgs& a, int batch, const GemvPlan& p, hipStream_t stream);
 
 // Resident-x batched path (se12_gemm_rx.hip): BF16 x with up to 32 rows on

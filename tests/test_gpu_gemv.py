@@ -182,6 +182,50 @@ def test_every_launch_configuration_is_correct_and_deterministic(gpu, rows, cols
         assert max_rel_error(y1, ref) <= REL_TOL, cfg
 
 
+@pytest.mark.parametrize("batch", [17, 24])
+def test_x_slab_launches_with_and_without_the_slab_ring(gpu, batch):
+    """The x-slab kernel under every launch the tuner would try, on a library
+    told of 132 compute units (the x-slab kernel then serves 2128x6144 at 17
+    and 24 batch rows: 133 tile rows, x fits neither whole nor as its first
+    16 rows, and two K splits are refused at this size).
+    Long launches (12+ steps per wave) whose ring of 8 slabs fits LDS keep
+    their slabs in it with a block barrier every 4 steps, the others a
+    barrier per step: every launch within REL_TOL of the oracle, run to run
+    identical, the raw twin bit-identical."""
+    from se12_amd import _native as nat
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+    from se12_amd.launch import candidate_configurations, grid_rows, k_tiles, mfma_min_waves, uses_rx
+
+    rows, cols, cus = 2128, 6144, 132
+    assert not uses_rx(rows, cols, batch, compute_units=cus)
+    bits = heavy_tailed_bf16(rows, cols, seed=35)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    r = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
+    for kern in (k, r):
+        nat.check(nat.lib().se12_set_compute_units(kern.handle.raw, cus))
+    xb = _x(batch, cols, seed=36)
+    x = bf16_tensor(xb, gpu)
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+    cfgs = candidate_configurations(rows, cols, batch=batch, compute_units=cus)
+    steps = set()
+    for cfg in cfgs:
+        waves = cfg.threads_per_block.value // 64
+        splits = cfg.blocks.value // grid_rows(rows, waves, batch)
+        share = -(-k_tiles(cols) // splits)                        # K tiles per split
+        steps.add(-(-share // (waves // mfma_min_waves(batch))))  # per K group
+        y1 = k.multiply(x, launch=cfg).clone()
+        y2 = k.multiply(x, launch=cfg)
+        yr = r.multiply(x, launch=cfg)
+        torch.cuda.synchronize()
+        assert torch.equal(y1, y2), cfg
+        assert torch.equal(y1, yr), cfg
+        assert max_rel_error(y1, ref) <= REL_TOL, cfg
+    # one K group over 24 and 12 steps (ring of 8), two K groups over 12
+    # steps (no room for the ring) and short launches all ran
+    assert 24 in steps and 12 in steps and min(steps) < 12, sorted(steps)
+
+
 def test_every_batch1_launch_configuration(gpu):
     from se12_amd.hip import Se12MatVecKernel
 

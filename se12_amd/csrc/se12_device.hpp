@@ -488,6 +488,28 @@ __device__ __forceinline__ void chunks_to_blocks(TileLoads& t) {
     }
 }
 
+// Split-K partial sums that other blocks read (any XCD): device-scope
+// relaxed atomics, which bypass the XCD's own L2. Four consecutive floats
+// (16-byte aligned) go as two 64-bit accesses: each access is a separate
+// transaction past L2, so fewer, wider ones cost less (2304x9216 B = 32, 4
+// splits: 20.6 us with four 32-bit stores and loads against 19.4). The
+// reader issues every split's loads before the first add (a loop that added
+// as it loaded would wait one round trip per split: 3584x14336 B = 24, 5
+// splits, 29.1 against 27.3 us); it adds them in ascending split order.
+__device__ __forceinline__ void store_partial4(float* p, const float v[4]) {
+    uint64_t* q = reinterpret_cast<uint64_t*>(p);
+    __hip_atomic_store(q, ((uint64_t)__float_as_uint(v[1]) << 32) | __float_as_uint(v[0]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(q + 1, ((uint64_t)__float_as_uint(v[3]) << 32) | __float_as_uint(v[2]), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t load_partial2(const float* p) {
+    return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float partial_lo(uint64_t v) { return __uint_as_float((uint32_t)v); }
+__device__ __forceinline__ float partial_hi(uint64_t v) { return __uint_as_float((uint32_t)(v >> 32)); }
+
 // Raw BF16 rows in the block layout (the raw twin): lane l, part p = row
 // l % 16, columns 16 (4 (l / 16) + p) .. + 15, as two 16-byte loads.
 __device__ __forceinline__ void load_raw_blocks(uint4 r[4][2], const uint16_t* wraw, int64_t K, int tr, int kt,

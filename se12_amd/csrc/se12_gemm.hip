@@ -527,11 +527,10 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
 #pragma unroll
     for (int g = 0; g < BG; ++g) {
         const int b = 16 * g + (int)(lane & 15u);
-        if (b < batch)
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                __hip_atomic_store(&a.partial[((int64_t)s * batch + b) * a.Np + n0 + e], acc[g][e], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+        if (b < batch) {
+            const float v[4] = {acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+            store_partial4(&a.partial[((int64_t)s * batch + b) * a.Np + n0], v);
+        }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     int old = 0;
@@ -541,15 +540,34 @@ __global__ __launch_bounds__(GENERIC ? kGemmMaxThreadsGeneric : kGemmMaxThreads)
 #pragma unroll
     for (int g = 0; g < BG; ++g) {
         const int b = 16 * g + (int)(lane & 15u);
-        if (b < batch)
+        if (b < batch) {
+            // every split's loads first (in groups of 8), then the adds in
+            // ascending split order
+            float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            for (int s0 = 0; s0 < S; s0 += 8) {
+                uint64_t lo[8], hi[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                float sum = 0.0f;
-                for (int ss = 0; ss < S; ++ss)
-                    sum += __hip_atomic_load(&a.partial[((int64_t)ss * batch + b) * a.Np + n0 + e], __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-                if (n0 + e < a.N) a.y[(int64_t)b * a.N + n0 + e] = sum;
+                for (int k = 0; k < 8; ++k) {
+                    lo[k] = hi[k] = 0;
+                    if (s0 + k < S) {
+                        const float* pp = &a.partial[((int64_t)(s0 + k) * batch + b) * a.Np + n0];
+                        lo[k] = load_partial2(pp);
+                        hi[k] = load_partial2(pp + 2);
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (s0 + k < S) {
+                        sum[0] += partial_lo(lo[k]);
+                        sum[1] += partial_hi(lo[k]);
+                        sum[2] += partial_lo(hi[k]);
+                        sum[3] += partial_hi(hi[k]);
+                    }
             }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (n0 + e < a.N) a.y[(int64_t)b * a.N + n0 + e] = sum[e];
+        }
     }
     if (lane == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

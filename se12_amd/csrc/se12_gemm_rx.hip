@@ -245,11 +245,8 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
             for (int e = 0; e < 4; ++e)
                 v[e] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(acc[g][e])));
             const int b = 16 * g + (int)(lane >> 2);
-            if (b < batch) {
-                float* pp = a.partial + ((int64_t)s * batch + b) * a.Np + (int64_t)tr * kTileRows + 4 * (int)(lane & 3u);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) __hip_atomic_store(pp + e, v[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            if (b < batch)
+                store_partial4(a.partial + ((int64_t)s * batch + b) * a.Np + (int64_t)tr * kTileRows + 4 * (int)(lane & 3u), v);
         }
     };
     // Once the wave's partial stores have completed, one lane per row arrives
@@ -279,12 +276,24 @@ __attribute__((amdgpu_waves_per_eu(XG ? 2 : 3))) void gemm_rx_kernel(GemvGroupAr
                     if (b < batch) {
                         const int64_t n = (int64_t)tr * kTileRows + 4 * (int)(lane & 3u);
                         float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                        for (int ss = 0; ss < S; ++ss) {
-                            const float* pp = a.partial + ((int64_t)ss * batch + b) * a.Np + n;
+                        uint64_t lo[kRxMaxSplits], hi[kRxMaxSplits];
 #pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                v[e] += __hip_atomic_load(pp + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (int ss = 0; ss < kRxMaxSplits; ++ss) {
+                            lo[ss] = hi[ss] = 0;
+                            if (ss < S) {
+                                const float* pp = a.partial + ((int64_t)ss * batch + b) * a.Np + n;
+                                lo[ss] = load_partial2(pp);
+                                hi[ss] = load_partial2(pp + 2);
+                            }
                         }
+#pragma unroll
+                        for (int ss = 0; ss < kRxMaxSplits; ++ss)
+                            if (ss < S) {
+                                v[0] += partial_lo(lo[ss]);
+                                v[1] += partial_hi(lo[ss]);
+                                v[2] += partial_lo(hi[ss]);
+                                v[3] += partial_hi(hi[ss]);
+                            }
                         float* yp = a.y + (int64_t)b * a.N + n;
                         if (y_vec) {
                             *reinterpret_cast<float4*>(yp) = make_float4(v[0], v[1], v[2], v[3]);

@@ -679,8 +679,20 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         __syncthreads();
         if (!*flag) return;
         if (tid < 16 * B) {
+            // the splits' partials in groups of 8 loads issued together, added
+            // in ascending split order (a load per add waits a round trip per
+            // split)
+            const float* pp = &a.partial[(int64_t)b * a.Np + n];
+            const int64_t stride = (int64_t)B * a.Np;
             v = 0.0f;
-            for (int ss = 0; ss < S; ++ss) v += load_dev(&a.partial[((int64_t)ss * B + b) * a.Np + n]);
+            for (int s0 = 0; s0 < S; s0 += 8) {
+                float q[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) q[k] = s0 + k < S ? load_dev(pp + (s0 + k) * stride) : 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (s0 + k < S) v += q[k];
+            }
         }
         if (tid == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

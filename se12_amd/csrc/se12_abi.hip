@@ -357,15 +357,14 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
     } else if (tc > 32) {
         // long rows on many tile rows (4608x36864): one wave per block and
-        // splits of ~36 K tiles (B = 1: 48.2 us against 49.8 with 8 waves),
-        // half again as many from 3 rows per launch (B = 2: 48.5 against
-        // 58.3; B = 4: 51.3 against 65.9)
+        // splits of ~36 K tiles (B = 1: 42.4 us against 42.7 with 6 splits,
+        // 43.3 with 3 and 44.2 with 2 waves x 6), half again as many from 2
+        // rows per launch (B = 2 / 3 / 4: 42.9 / 44.0 / 46.9 against 44.2 /
+        // 45.7 / 48.4 with 3 splits; before the splits' partial sums were
+        // read in one round trip, 3 splits were the best at B = 2)
         waves = 1;
         splits = std::max<int64_t>(1, (tc + 18) / 36);
-        if (bl >= 3) splits = splits * 3 / 2;
-        // 2 rows: ~48 tiles per split (4608x36864: 3 splits 47.6 us against
-        // 49.7 with 4)
-        if (bl == 2) splits = std::max<int64_t>(1, (tc + 24) / 48);
+        if (bl >= 2) splits = splits * 3 / 2;
     } else if (tiles <= 10 * cus) {
         waves = std::min<int64_t>(16, tc);
     } else if (tiles <= 32 * cus) {

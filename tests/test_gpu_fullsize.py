@@ -176,13 +176,18 @@ def test_down_27b_heavy_tailed_full_size(gpu):
     enc = o.encode(bits.reshape(-1), rows, cols)
     _assert_same_streams(_host_streams(dt), enc)
     assert int((o.unpack_codes(enc["ec"]) == o.ESCAPE_CODE).sum()) > 0   # the escape path is exercised
-    xb = o.normal_bf16(1, cols, seed=28, std=1.0)
-    x = bf16_tensor(xb, gpu)
-    y = Se12MatVecKernel(dt).multiply(x)
-    yr = RawBf16MatVecKernel(w).multiply(x)
-    torch.cuda.synchronize()
-    assert torch.equal(y, yr)
-    assert max_rel_error(y, o.gemv_reference(enc, o.bf16_bits_to_f32(xb))) <= REL_TOL
+    # batch 1 and 2 under their default launches (one wave per block, 4 and
+    # 6 K splits)
+    xb = o.normal_bf16(2, cols, seed=28, std=1.0)
+    ref = o.gemv_reference(enc, o.bf16_bits_to_f32(xb))
+    fused, raw = Se12MatVecKernel(dt), RawBf16MatVecKernel(w)
+    for b in (1, 2):
+        x = bf16_tensor(xb[:b], gpu)
+        y = fused.multiply(x)
+        yr = raw.multiply(x)
+        torch.cuda.synchronize()
+        assert torch.equal(y, yr), b
+        assert max_rel_error(y, ref[:b]) <= REL_TOL, b
 
 
 def test_lm_head_heavy_tailed_full_size(gpu):

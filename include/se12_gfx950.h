@@ -189,18 +189,20 @@ int se12_gemv(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch,
 /* se12_gemv for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid allocation): the same product,
  * launch shapes and results as se12_gemv on the same handle, but its kernels
- * keep their split-K partial sums and arrival counters in the library's own
- * static device scratch (8 MiB per GPU, held until the process ends: 65,536
- * arrival counters, i.e. up to 32,767 tile rows, and 2,031,616 partial
- * sums, i.e. K splits x min(batch, 4 on the dot2 path or the whole batch on
- * the MFMA path) x padded rows) instead of the handle's workspace. A shape
- * or launch beyond those limits fails with SE12_E_CAPACITY before any launch.
+ * keep their split-K partial sums, pair slots and arrival counters in the
+ * library's own static device scratch (8 MiB per GPU, held until the process
+ * ends: 65,536 arrival counters, i.e. up to 32,767 tile rows; 262,144 pair
+ * slots, i.e. (K splits - 1) x min(batch, 4) x padded rows on the dot2 path;
+ * and 1,507,328 partial sums, i.e. K splits x the whole batch x padded rows
+ * on the MFMA path) instead of the handle's workspace. A shape or launch
+ * beyond those limits fails with SE12_E_CAPACITY before any launch.
  * The call allocates nothing and calls no allocating routine; its first call
- * on a device looks up the scratch and clears its counters with a kernel on
- * `stream` (make that first call outside a capture). Every call on one GPU
- * shares that GPU's scratch, whose counters return to zero after each
- * launch: calls that overlap on one GPU (other streams, other threads) race
- * and must be ordered by the caller. No counterpart in the reference. */
+ * on a device looks up the scratch and clears its counters and pair slots
+ * with a kernel on `stream` (make that first call outside a capture). Every
+ * call on one GPU shares that GPU's scratch, whose counters and slots return
+ * to zero after each launch: calls that overlap on one GPU (other streams,
+ * other threads) race and must be ordered by the caller. No counterpart in
+ * the reference. */
 int se12_gemv_noalloc(se12_handle* h, const void* x_dev, int32_t x_dtype, int32_t batch, float* y_dev,
                       const se12_launch* launch, void* stream);
 

@@ -86,6 +86,8 @@ struct se12_handle {
     float* partial;
     int64_t partial_elems;
     int32_t* counters;
+    uint64_t* pairs;     // [s_cap - 1, 4, Np] dot2 split-K pair slots (zero between launches)
+    int64_t pair_elems;
     int32_t max_batch;
     int32_t s_cap;
     int32_t cu_count;
@@ -153,6 +155,10 @@ static int bind_common(se12_handle* h, int64_t rows, int64_t cols, int32_t max_b
         if (max_batch >= kGemmMinBatch) pe = std::max<int64_t>(pe, (int64_t)std::min(h->s_cap, kGemmMaxSplits) * max_batch);
         h->partial_elems = pe * h->Np;
         SE12_HIP(hipMalloc(&h->partial, (size_t)h->partial_elems * sizeof(float)));
+        // the dot2 kernel's pair slots: S - 1 per output, zero between launches
+        h->pair_elems = (int64_t)(h->s_cap - 1) * std::min<int32_t>(max_batch, kGemvMaxBatchPerLaunch) * h->Np;
+        SE12_HIP(hipMalloc(&h->pairs, (size_t)h->pair_elems * sizeof(uint64_t)));
+        SE12_HIP(hipMemset(h->pairs, 0, (size_t)h->pair_elems * sizeof(uint64_t)));
     }
     // arrival counters: split-K per tile row and the fused step tails'
     const size_t counter_bytes = (size_t)gemv_counter_count(h->TR) * sizeof(int32_t);
@@ -170,6 +176,7 @@ static void free_handle(se12_handle* h) {
     if (h->lut) (void)hipFree(h->lut);
     if (h->partial) (void)hipFree(h->partial);
     if (h->counters) (void)hipFree(h->counters);
+    if (h->pairs) (void)hipFree(h->pairs);
     delete h;
 }
 
@@ -326,83 +333,118 @@ static int max_threads_for(int32_t bl, bool xf32, bool generic) {
 
 // The default launch, re-derived for MI355X (256 CUs in 8 XCDs, wave64) from
 // sweeps of every (waves, splits) pair on cold data at the Gemma-2 2B/9B/27B
-// shapes, the grouped q/k/v and gate/up shapes and the 256000x2304 LM head.
-// A batch-1 GEMV is one pass over the streams. What pays: enough tiles in
-// flight per CU to cover HBM latency but not so many that every wave's data
-// lands at the end of the pass (the decode would then all run after the last
-// byte arrives), and no cross-block K reduction (S > 1 adds a store ->
-// counter -> reload round trip to the end of every block) unless rows are
-// very long. By tiles per CU (T / CUs), for rows of at most 32 tiles:
+// shapes, the grouped q/k/v and gate/up shapes and the LM heads. A batch-1
+// GEMV is one pass over the streams. What pays: enough tiles in flight per
+// CU to cover HBM latency but not so many that every wave's data lands at
+// the end of the pass (the decode would then all run after the last byte
+// arrives). K splits meet in the pair tree (one exchange round trip per
+// level at the end of a block), which pays where a launch has too few tile
+// rows to spread 2-4 batch rows' decode over the CUs. By tiles per CU
+// (T / CUs), for rows of at most 32 tiles:
 //  - fewer tile rows than CUs, or at most 10 tiles per CU: one wave per K
 //    tile (rows longer than 16 tiles: 8 waves streaming with prefetch);
 //  - up to 32 tiles per CU: 3 waves; up to 64: about 2 tiles per wave;
 //    more (very tall matrices such as an LM head): 6 waves;
 // rows longer than 32 tiles on many tile rows: 8 waves and splits of ~36
 // tiles; very long rows on very few tile rows are split so that every CU
-// gets a block.
+// gets a block. At batch 1, 3 to 8 tile rows per CU on rows of up to 18
+// tiles take one wave per block (a block per tile row, streaming its row
+// with prefetch), except under a fused norm head (`head`), whose x rebuild
+// wants the block's threads, and in the edge-handling variants, which do
+// not prefetch.
 static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_cap, int32_t batch, bool xf32,
-                           bool generic, int32_t* waves_out, int32_t* splits_out) {
+                           bool generic, bool head, int32_t* waves_out, int32_t* splits_out) {
     const int32_t bl = std::min<int32_t>(batch, kGemvMaxBatchPerLaunch);
     const int64_t mw = max_threads_for(bl, xf32, generic) / 64;
     const int64_t cus = std::max<int32_t>(1, cu_count);
     const int64_t tiles = tr * tc;
     int64_t waves, splits = 1;
-    if (tr < cus) {
+    if (!head && !generic && bl == 1 && tr >= 3 * cus && tr <= 8 * cus && tc <= 18) {
+        // 2B gate/up grouped (1152 x 9 tiles) 12.45 us against 13.06 with 5
+        // waves, 9B gate/up grouped (1792 x 14) 25.7 against 27.4 with 8, 9B
+        // gate (896 x 14) 14.55 against 14.7 with 2; 27B gate (2304 x 18, 9
+        // rows per CU) keeps 8 (41.1 against 41.7), the LM heads 6 (256000 x
+        // 2304: 132.9 either way; 256000x3584: 195-200 against 210)
+        waves = 1;
+    } else if (tr < cus) {
         // one wave per K tile up to 9 (Gemma-2 2B), else 8 (2048x3584: 5.4 us
         // against 14 waves' slower launch; 3584x4096: 6.3 against 7.4 with
-        // 16), 4 at 4 rows per launch (2304x9216 11.4 against 11.8, 3584x4096
-        // 7.7-8.0 against 8.1, 3584x14336 18.5-19.0 against 19.1; at 3 rows
-        // 2304x9216 10.9 against 10.7)
+        // 16), 4 at 4 rows per launch (3584x4096 7.7-8.0 against 8.1,
+        // 3584x14336 16.7 against 17.0 with 8). Rows of 17-48 K tiles on at
+        // most two thirds of the CUs' worth of tile rows take 3 splits of 4
+        // waves at 2-4 rows per launch (2304x9216 B = 2 / 3 / 4: 8.8 / 9.6 /
+        // 10.3 us against 9.2 / 10.35 / 11.1 unsplit; B = 1 8.3 either way).
+        // (Rows of 9 K tiles on a quarter of the CUs' tile rows, Gemma-2 2B
+        // k/v alone, measured 4.13 us against 4.47 with 3 splits of 3 waves
+        // in a rotation of 300 back-to-back launches, but 4.65 against 4.50
+        // in 26 launches after an eviction, so they stay unsplit.)
         waves = tc <= 9 ? tc : (bl >= 4 ? 4 : 8);
         if (tc > 64 && tr * 2 <= cus) splits = std::min<int64_t>(ceil_div(cus, tr), ceil_div(tc, 16));
+        if (bl >= 2 && tc > 16 && tc <= 48 && tr * 3 <= cus * 2) {
+            waves = 4;
+            splits = 3;
+        }
     } else if (tc > 32) {
         // long rows on many tile rows (4608x36864): one wave per block and
-        // splits of ~36 K tiles (B = 1: 42.4 us against 42.7 with 6 splits,
-        // 43.3 with 3 and 44.2 with 2 waves x 6), half again as many from 2
-        // rows per launch (B = 2 / 3 / 4: 42.9 / 44.0 / 46.9 against 44.2 /
-        // 45.7 / 48.4 with 3 splits; before the splits' partial sums were
-        // read in one round trip, 3 splits were the best at B = 2)
+        // splits of ~36 K tiles (B = 1: 42.3 us against 42.2 with 6 splits,
+        // 42.8 with 3 and 43.4 with 2 waves x 6), half again as many from 2
+        // rows per launch (B = 2 / 3 / 4: 43.0 / 44.0 / 46.9 against 43.5 /
+        // 45.1 / 47.7 with 3 splits)
         waves = 1;
         splits = std::max<int64_t>(1, (tc + 18) / 36);
         if (bl >= 2) splits = splits * 3 / 2;
     } else if (tiles <= 10 * cus) {
+        // one wave per K tile; at 4 rows per launch 3 splits of 3 waves for
+        // rows of 9 K tiles (2B q/k/v grouped, 256 x 9 tiles: 7.5 us against
+        // 7.75 with 8 waves; at 1-3 rows 9 waves stay best)
         waves = std::min<int64_t>(16, tc);
+        if (bl >= 4 && tc == 9) {
+            waves = 3;
+            splits = 3;
+        }
     } else if (tiles <= 32 * cus) {
-        // 3 waves for 9 K tiles (9216x2304), 2 at 4 rows per launch (11.0 us
-        // against 11.3; at 3 rows 10.5 against 10.4); longer rows 8 waves at 1..2 rows per
-        // launch when the tile rows fill the CUs evenly (4096x3584: 6.3 us
-        // against 7.2 with 3; 4096x4608: 7.3 against 8.3; 9B q/k/v grouped,
-        // 512 tile rows: 10.0 against 10.9 with 4), 4 where some CUs take
-        // two blocks and others one (4608x4096: 8.6 against 9.0 with 8) and
-        // at 3..4 rows (7.95 / 9.0 against 8.2 / 9.2)
-        waves = tc <= 9 ? (bl >= 4 ? 2 : 3) : (bl >= 3 || (tr > cus && tr % cus != 0) ? 4 : 8);
+        // 3 waves for 9 K tiles (9216x2304), 3 splits of them at 2-4 rows
+        // per launch (B = 2 / 3 / 4: 8.6 / 9.2 / 9.8 us against 8.8 / 9.6 /
+        // 10.4 unsplit); longer rows 8 waves at 1..2 rows per launch when
+        // the tile rows fill the CUs evenly (4096x3584: 6.3 us against 7.2
+        // with 3; 4096x4608: 7.3 against 8.3; 9B q/k/v grouped, 512 tile
+        // rows: 9.6 against 10.0 with 2), 4 where some CUs take two blocks
+        // and others one (4608x4096: 8.6 against 9.0 with 8) and at 3..4
+        // rows (7.95 / 9.0 against 8.2 / 9.2)
+        if (tc == 9 && bl >= 2) {
+            waves = 3;
+            splits = 3;
+        } else {
+            waves = tc <= 9 ? (bl >= 4 ? 2 : 3) : (bl >= 3 || (tr > cus && tr % cus != 0) ? 4 : 8);
+        }
         waves = std::min<int64_t>(waves, tc);
     } else if (tiles <= 64 * cus) {
-        // 3..4 rows per launch: 1 wave (14336x3584, B = 3 / 4: 17.4-17.7 /
-        // 18.3 us against 18.6-18.9 / 19.1 with 2); 2 rows: 1 wave where the
-        // tile rows give each CU 3+ blocks (14336x3584 16.1 against 16.6-17.4
-        // with 2; 2B gate/up grouped 14.4 against 15.2), else 2 (27B q/k/v
-        // grouped, 512 tile rows: 13.6 against 16.5 with 1); one row: two
-        // tiles per wave for an odd count (2B gate/up grouped, 9 K tiles: 5
-        // waves 13.6 us against 14.2 with 4 and 15.2 with 6), for an even
-        // count 2 waves on 3+ blocks per CU (14336x3584: 15.9 against 16.3
-        // with 8) and 8 on fewer (27B q/k/v grouped: 12.1 against 12.5 with 2
-        // and 13.4 with 10)
+        // 3..4 rows per launch: 1 wave (14336x3584, B = 3 / 4: 15.5 / 16.4
+        // us against 16.0 / 17.1 with 2), 2B gate/up grouped at 4 rows 3
+        // (15.1 against 15.6); 2 rows: 1 wave where the tile rows give each
+        // CU 3+ blocks (14336x3584 14.9 against 15.4 with 2; 2B gate/up
+        // grouped 13.2 against 13.8 with 3), else 2 (27B q/k/v grouped, 512
+        // tile rows: 13.6 against 16.5 with 1); one row on fewer than 3 tile
+        // rows per CU: two tiles per wave for an odd count, 8 waves for an
+        // even one (27B q/k/v grouped: 11.4 against 12.0 with 2)
         if (bl >= 3)
-            waves = 1;
+            waves = bl >= 4 && tc == 9 ? 3 : 1;
         else if (bl == 2)
             waves = tr >= 3 * cus ? 1 : 2;
         else
             waves = tc % 2 == 1 ? (tc + 1) / 2 : (tr >= 3 * cus ? 2 : 8);
         waves = std::max<int64_t>(1, std::min<int64_t>(tc, waves));
     } else {
-        // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1
-        // and 3 at B = 2..4 (B = 4: 154 us against 209 with 6); rows over
-        // 12 K tiles 8 waves (36864x4608 B = 1 / 2: 45.0 / 45.3 us against
-        // 45.4 / 45.8 with 4; 256000x3584: 216.8 / 217.0 against 225.6 /
-        // 223.2), at B = 3..4 on 256+ tiles per CU 2 (256000x3584 B = 4: 231
-        // against 258 with 8)
-        if (tc <= 12)
+        // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1,
+        // 4 at B = 2 (129.9 us against 132.4 with 3) and 3 at B = 3..4
+        // (B = 4: 154 against 209 with 6); rows over 12 K tiles 8 waves
+        // (36864x4608 B = 1: 41.1 us against 41.5 with 6; 256000x3584: 200
+        // against 210 with 1), 4 at B = 2 (256000x3584: 198.5 against 202
+        // with 8), at B = 3..4 on 256+ tiles per CU 2 (256000x3584 B = 4:
+        // 231 against 258 with 8)
+        if (bl == 2)
+            waves = 4;
+        else if (tc <= 12)
             waves = bl >= 2 ? 3 : 6;
         else
             waves = bl >= 3 && tiles >= 256 * cus ? 2 : 8;
@@ -510,7 +552,7 @@ int se12_default_launch(const se12_handle* h, int32_t batch, se12_launch* out) {
         out->blocks = (int32_t)(gemm_row_blocks(hs, 1, gemm_min_waves(batch)) * splits);
         return SE12_OK;
     }
-    default_launch(h->TR, h->TC, h->cu_count, h->s_cap, batch, false, generic, &waves, &splits);
+    default_launch(h->TR, h->TC, h->cu_count, h->s_cap, batch, false, generic, false, &waves, &splits);
     out->threads_per_block = waves * 64;
     out->blocks = h->TR * splits;
     return SE12_OK;
@@ -705,6 +747,8 @@ struct Workspace {
     int64_t partial_elems;
     int32_t* counters;
     int64_t counter_elems;
+    uint64_t* pairs;
+    int64_t pair_elems;
 };
 
 static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, const void* x, int32_t x_dtype,
@@ -789,7 +833,8 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             gemm_default_launch(hs, count, batch, generic, &waves, &splits);
             grid_rows = gemm_row_blocks(hs, count, gemm_min_waves(batch));
         } else {
-            default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, &waves, &splits);
+            default_launch(tr_total, h0->TC, h0->cu_count, h0->s_cap, batch, xf32, generic, pro != nullptr, &waves,
+                           &splits);
             // a launch with the norm in its head: one or two waves fewer where
             // that splits the K tiles evenly (Gemma-2-2B gate/up, 9 K tiles: 3
             // waves instead of 4 measured 15 us less per decoded token)
@@ -809,13 +854,18 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
         if (gemv_counter_count(h0->TR) > ws->counter_elems)
             return fail(SE12_E_CAPACITY, "%s: %d tile rows need %lld arrival counters, the scratch holds %lld", fn,
                         h0->TR, (long long)gemv_counter_count(h0->TR), (long long)ws->counter_elems);
-        if (splits > 1 && (int64_t)splits * b_first * h0->Np > ws->partial_elems)
+        if (mfma && splits > 1 && (int64_t)splits * b_first * h0->Np > ws->partial_elems)
             return fail(SE12_E_CAPACITY, "%s: %d K splits x %d batch rows x %lld rows need %lld partial sums, the "
                         "scratch holds %lld", fn, splits, b_first, (long long)h0->Np,
                         (long long)splits * b_first * h0->Np, (long long)ws->partial_elems);
+        if (!mfma && splits > 1 && (int64_t)(splits - 1) * b_first * h0->Np > ws->pair_elems)
+            return fail(SE12_E_CAPACITY, "%s: %d K splits x %d batch rows x %lld rows need %lld pair slots, the "
+                        "scratch holds %lld", fn, splits, b_first, (long long)h0->Np,
+                        (long long)(splits - 1) * b_first * h0->Np, (long long)ws->pair_elems);
     } else if (splits > 1) {
         for (int32_t i = 0; i < count; ++i)
-            if ((int64_t)splits * b_first * hs[i]->Np > hs[i]->partial_elems)
+            if ((int64_t)splits * b_first * hs[i]->Np > hs[i]->partial_elems ||
+                (!mfma && (int64_t)(splits - 1) * b_first * hs[i]->Np > hs[i]->pair_elems))
                 return fail(SE12_E_CAPACITY, "%s: %d K splits at batch %d exceed handle %d's split-K workspace", fn,
                             splits, batch, i);
     }
@@ -860,6 +910,7 @@ static int gemv_group(const char* fn, se12_handle* const* hs, int32_t count, con
             a.y = ys[i] + (size_t)b0 * h->N;
             a.partial = ws ? ws->partial : h->partial;
             a.counters = ws ? ws->counters : h->counters;
+            a.pairs = ws ? ws->pairs : h->pairs;
             a.N = h->N;
             a.K = h->K;
             a.Np = h->Np;
@@ -928,13 +979,18 @@ int se12_gemv(se12_handle* h, const void* x, int32_t x_dtype, int32_t batch, flo
 
 // The zero-allocation product's scratch: one array per device (each GPU the
 // library runs on holds its own copy until the process ends), arrival
-// counters first, split-K partial sums after them. In host code `scratch`
+// counters first, then the dot2 kernel's split-K pair slots, then split-K
+// partial sums; the counters and slots start at zero and every launch leaves
+// them so. In host code `scratch`
 // names a host-side stand-in, not device memory: only the address
 // hipGetSymbolAddress returns for the current device may reach a kernel or
 // any HIP call.
 constexpr size_t kScratchBytes = size_t(8) << 20;
 constexpr size_t kScratchCounterBytes = size_t(256) << 10;
-static_assert(kScratchCounterBytes % 256 == 0 && kScratchCounterBytes < kScratchBytes, "scratch layout");
+constexpr size_t kScratchPairBytes = size_t(2) << 20;
+constexpr size_t kScratchZeroBytes = kScratchCounterBytes + kScratchPairBytes;  // cleared at set-up
+static_assert(kScratchCounterBytes % 256 == 0 && kScratchPairBytes % 256 == 0 && kScratchZeroBytes < kScratchBytes,
+              "scratch layout");
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 namespace {
@@ -949,9 +1005,9 @@ __global__ void scratch_clear_kernel(uint32_t* p, int64_t words) {
 }
 
 // The device address of `scratch` on `device` (current), set up on the
-// first call there: hipGetSymbolAddress, then the counters cleared by a
-// kernel on `stream` (a fill kernel, so that a caller capturing the call
-// records no memset node).
+// first call there: hipGetSymbolAddress, then the counters and pair slots
+// cleared by a kernel on `stream` (a fill kernel, so that a caller capturing
+// the call records no memset node).
 int scratch_for_device(int device, hipStream_t stream, uint8_t** out) {
     if (device < 0 || device >= kScratchMaxDevices)
         return fail(SE12_E_DEVICE, "se12_gemv_noalloc: device %d beyond the %d the scratch table serves", device,
@@ -962,7 +1018,7 @@ int scratch_for_device(int device, hipStream_t stream, uint8_t** out) {
         SE12_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         if (!p) return fail(SE12_E_HIP, "se12_gemv_noalloc: hipGetSymbolAddress gave NULL");
         hipLaunchKernelGGL(scratch_clear_kernel, dim3(64), dim3(256), 0, stream, static_cast<uint32_t*>(p),
-                           (int64_t)(kScratchCounterBytes / sizeof(uint32_t)));
+                           (int64_t)(kScratchZeroBytes / sizeof(uint32_t)));
         SE12_HIP(hipGetLastError());
         g_scratch_ptr[device] = static_cast<uint8_t*>(p);
     }
@@ -984,9 +1040,12 @@ int se12_gemv_noalloc(se12_handle* h, const void* x, int32_t x_dtype, int32_t ba
         SE12_HIP(ds.enter(h->device));
         if (int rc = scratch_for_device(h->device, static_cast<hipStream_t>(stream), &base)) return rc;
     }
-    Workspace ws{reinterpret_cast<float*>(base + kScratchCounterBytes),
-                 (int64_t)((kScratchBytes - kScratchCounterBytes) / sizeof(float)), reinterpret_cast<int32_t*>(base),
-                 (int64_t)(kScratchCounterBytes / sizeof(int32_t))};
+    Workspace ws{reinterpret_cast<float*>(base + kScratchZeroBytes),
+                 (int64_t)((kScratchBytes - kScratchZeroBytes) / sizeof(float)),
+                 reinterpret_cast<int32_t*>(base),
+                 (int64_t)(kScratchCounterBytes / sizeof(int32_t)),
+                 reinterpret_cast<uint64_t*>(base + kScratchCounterBytes),
+                 (int64_t)(kScratchPairBytes / sizeof(uint64_t))};
     se12_handle* hs[1] = {h};
     float* ys[1] = {y};
     return gemv_group("se12_gemv_noalloc", hs, 1, x, x_dtype, batch, ys, launch, stream, nullptr, nullptr, &ws);

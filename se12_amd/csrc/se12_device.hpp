@@ -504,6 +504,38 @@ __device__ __forceinline__ void store_partial4(float* p, const float v[4]) {
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Split-K sums without an arrival counter: the S partial sums of one output
+// meet in a fixed binary tree (level 0 pairs splits 2i and 2i + 1, each level
+// pairs the sums of the one below, an odd last one moves up unpaired). A
+// pair meets in one 64-bit slot through one device-scope exchange: the first
+// of the two to arrive leaves (1 << 32) | its bits there and is done; the
+// second gets them back, adds them (a + b == b + a exactly, so the order of
+// arrival changes no bit of the result), clears the slot and carries the sum
+// up. A thread pays one round trip per level it climbs, where a counter
+// costs three (partial store and its wait, counter, reload). Slots are zero
+// between launches: every slot a launch fills, the same launch clears.
+// `slot0` = this output's slot of node 0, `stride` = elements between nodes.
+// Returns true for the one split that ends with the total in v.
+__device__ __forceinline__ bool pair_tree_sum(uint64_t* slot0, int64_t stride, int s, int S, float& v) {
+    int c = s, n = S;
+    int64_t node = 0;  // the level's first node
+    while (n > 1) {
+        if ((c ^ 1) < n) {
+            uint64_t* p = slot0 + (node + (c >> 1)) * stride;
+            const uint64_t old = __hip_atomic_exchange(p, (uint64_t(1) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT);
+            if (old == 0u) return false;
+            const float o = __uint_as_float((uint32_t)old);
+            v = (c & 1) ? o + v : v + o;
+            __hip_atomic_store(p, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        node += n >> 1;
+        c >>= 1;
+        n = (n + 1) >> 1;
+    }
+    return true;
+}
+
 __device__ __forceinline__ uint64_t load_partial2(const float* p) {
     return __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }

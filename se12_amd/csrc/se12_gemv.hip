@@ -489,6 +489,7 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         a.y = m.y;
         a.partial = m.partial;
         a.counters = m.counters;
+        a.pairs = m.pairs;
         a.N = m.N;
         a.K = m.K;
         a.Np = m.Np;
@@ -661,6 +662,13 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         for (int ww = 0; ww < W; ++ww) v += red[(ww * B + b) * 16 + rr];
     }
     const bool epi = epi_kind != kEpiNone;
+    if (S > 1 && !epi && !row_ss) {
+        // each output's S partials meet in the pair tree; the split holding
+        // the total stores it
+        if (tid < 16 * B && pair_tree_sum(a.pairs + (int64_t)b * a.Np + n, (int64_t)B * a.Np, s, S, v) && n < a.N)
+            a.y[(int64_t)b * a.N + n] = v;
+        return;
+    }
     if (S > 1) {
         // Cross-block reduction without cache-wide maintenance: the partials
         // are written with device-scope stores, each thread waits for its

@@ -19,6 +19,7 @@ struct GemvArgs {
     float* y;                 // [B, N]
     float* partial;           // [S, B, Np] split-K partial sums
     int32_t* counters;        // [TR] arrival counters (zero between launches)
+    uint64_t* pairs;          // [S - 1, B, Np] split-K pair slots (zero between launches)
     int64_t N, K, Np;
     int32_t TR, TC;
     int32_t S;                // K splits per tile row

@@ -21,9 +21,10 @@ tests/test_spec_fused_gemv.py:135-180):
   raw-BF16 twin give identical logits at every step and identical tokens,
   and the hipBLASLt BF16 run's tokens are identical up to a first
   divergence at a near-tie (top-2 logits < 0.05 apart).
-- Every product launch of the Gemma-2-2B step at batch 1 and 2 under the
+- Every product launch of the Gemma-2-2B step at batch 1 to 4 under the
   default launch (q/k/v and gate/up grouped, o, down_proj) against the
-  oracle.
+  oracle; the 9B gate grouped with itself (the gate/up shape, one wave per
+  block at batch 1) likewise.
 """
 
 from __future__ import annotations
@@ -98,6 +99,23 @@ def test_gate_9b_batch_sweep_default_launch(gpu, gate_9b, batch):
     torch.cuda.synchronize()
     assert max_rel_error(y, refs[batch]) <= REL_TOL
     assert torch.equal(y, yr)
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4])
+def test_9b_gate_up_grouped_default_launch(gpu, gate_9b, batch):
+    """The 9B gate/up launch shape (two 14336x3584 matrices, 1,792 tile
+    rows of 14 K tiles, one wave per block at batch 1), here the gate matrix
+    twice: both products within REL_TOL of the oracle, the raw twin's grouped
+    launch bit-identical."""
+    from se12_amd.hip import multiply_grouped
+
+    fused, raw, xs, refs = gate_9b
+    x = bf16_tensor(xs[batch], gpu)
+    ys, yrs = multiply_grouped([fused, fused], x), multiply_grouped([raw, raw], x)
+    torch.cuda.synchronize()
+    for y, yr in zip(ys, yrs):
+        assert max_rel_error(y, refs[batch]) <= REL_TOL
+        assert torch.equal(y, yr)
 
 
 def test_q_9b_wide_batches_x_partly_from_global(gpu):
@@ -272,7 +290,7 @@ GEMMA2_2B_LAUNCHES = {
 }
 
 
-@pytest.mark.parametrize("batch", [1, 2])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("name", sorted(GEMMA2_2B_LAUNCHES))
 def test_gemma2_2b_step_launches_default_launch(gpu, name, batch):
     """Every product launch of the Gemma-2-2B step that bench.py times, at

@@ -77,15 +77,22 @@ def test_noalloc_refuses_what_the_scratch_cannot_hold(gpu):
     from se12_amd.launch import configuration
 
     lib = nat.lib()
-    # 36 K splits x 4 batch rows x 16384 rows = 2,359,296 partial sums > 2,031,616
+    # dot2: 35 pair slots x 4 batch rows x 16384 rows = 2,293,760 > 262,144
     w = torch.randn((16384, 9216), device=gpu).mul_(0.02).to(torch.bfloat16)
-    kern = Se12MatVecKernel(encode_on_device(w), max_batch=4)
+    kern = Se12MatVecKernel(encode_on_device(w), max_batch=32)
     del w
     x = torch.randn((4, 9216), device=gpu).to(torch.bfloat16)
     y = torch.zeros((4, 16384), dtype=torch.float32, device=gpu)
     rc = _call(lib.se12_gemv_noalloc, kern, x, y, configuration(4, 36, 16384, 4))
-    assert rc == nat.SE12_E_CAPACITY and "partial sums" in nat.last_error()
+    assert rc == nat.SE12_E_CAPACITY and "pair slots" in nat.last_error()
     assert torch.count_nonzero(y).item() == 0           # nothing launched
+    # MFMA (resident-x, 4 K splits): 4 x 32 batch rows x 16384 rows =
+    # 2,097,152 partial sums > 1,507,328
+    x32 = torch.randn((32, 9216), device=gpu).to(torch.bfloat16)
+    y32 = torch.zeros((32, 16384), dtype=torch.float32, device=gpu)
+    rc = _call(lib.se12_gemv_noalloc, kern, x32, y32, None)
+    assert rc == nat.SE12_E_CAPACITY and "partial sums" in nat.last_error()
+    assert torch.count_nonzero(y32).item() == 0
     # 32,768 tile rows need 65,537 arrival counters > 65,536
     w = torch.randn((32768 * 16, 256), device=gpu).mul_(0.02).to(torch.bfloat16)
     tall = Se12MatVecKernel(encode_on_device(w), max_batch=1)

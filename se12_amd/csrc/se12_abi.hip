@@ -608,7 +608,8 @@ static GemvPlan plan_gemm(int64_t row_blocks, bool raw, int32_t batch, bool gene
 // Since its waits and launch were refitted it beats the x-slab kernel at 5-8
 // rows too (default launches, cold: 9216x4096 B = 5 18.5 against 21.0 us,
 // 2304x2304 8.5 against 10.2, 3584x14336 22.6 against 24.3, 14336x3584 B = 8
-// 20.3 against 20.4). With 17..32 rows whose x does not fit but 16 rows do
+// 20.3 against 20.4), except on few tile rows of long rows (below). With
+// 17..32 rows whose x does not fit but 16 rows do
 // (K = 3584..4608), on matrices of at most one tile row per CU, LDS holds the
 // first 16 rows and batch group 1's operands come from global memory
 // (4096x3584 B = 24 / 32: 13.6 / 14.7 us against the x-slab kernel's 18.8 /
@@ -631,9 +632,20 @@ static RxLayout rx_layout(se12_handle* const* hs, int32_t count, int32_t batch) 
         rows += hs[i]->TR;
     }
     const int64_t lds = hs[0]->lds_per_block;
-    if ((int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= lds) return {batch, 1};
+    const int64_t cus = std::max<int32_t>(1, hs[0]->cu_count);
+    if ((int64_t)(rx_lds_bytes(hs[0]->K, batch) + kLutBytes) <= lds) {
+        // rows of 32+ K tiles on at most 5/8 of the CUs' worth of tile rows:
+        // one resident-x block per tile row leaves CUs idle where the x-slab
+        // kernel's K splits reach them all (2304x9216 B = 5 / 6 / 7 / 8: 15.0
+        // / 14.9 / 15.0 / 15.1 us against 15.2 / 15.6 / 15.9 / 16.2; 2048x9216
+        // B = 8: 13.9 against 16.4; with more rows or shorter ones the
+        // resident-x kernel stays ahead: 3584x14336 B = 5 21.5 against 23.6,
+        // 2304x6144 B = 8 11.9 against 12.4)
+        if (rows * 8 <= cus * 5 && hs[0]->TC >= 32) return {0, 0};
+        return {batch, 1};
+    }
     if (batch > 16 && (int64_t)(rx_lds_bytes(hs[0]->K, 16) + kLutBytes) <= lds &&
-        rows <= std::max<int32_t>(1, hs[0]->cu_count))
+        rows <= cus)
         return {16, 1};
     const int32_t tc = hs[0]->TC;
     int32_t sp = 2;

@@ -101,14 +101,17 @@ def rx_lds_bytes(k: int, batch: int) -> int:
 def rx_layout(output_rows: int, k: int, batch: int, float32_activations: bool = False, aligned_x: bool = True,
               compute_units: int = COMPUTE_UNITS) -> tuple[int, int]:
     """(rows of x the resident-x kernel keeps in LDS, K splits) of a launch
-    over one matrix (the library's rule): (batch, 1) where x fits; (16, 1) for
-    17..32 rows whose first 16 fit on a matrix of at most one tile row per
-    CU; (batch, S) with the fewest K splits S whose share of x's columns fits,
-    where splits pay; else (0, 0), the x-slab kernel."""
+    over one matrix (the library's rule): (batch, 1) where x fits, except
+    on rows of 32+ K tiles with at most 5/8 of the CUs' worth of tile rows;
+    (16, 1) for 17..32 rows whose first 16 fit on a matrix of at most one
+    tile row per CU; (batch, S) with the fewest K splits S whose share of x's
+    columns fits, where splits pay; else (0, 0), the x-slab kernel."""
     if not (uses_mfma(batch, float32_activations) and aligned_x
             and not runs_generic(output_rows, k, float32_activations)):
         return 0, 0
     if rx_lds_bytes(k, batch) + LUT_BYTES <= LDS_PER_BLOCK:
+        if 8 * tile_rows(output_rows) <= 5 * compute_units and k_tiles(k) >= 32:
+            return 0, 0
         return batch, 1
     if batch > 16 and rx_lds_bytes(k, 16) + LUT_BYTES <= LDS_PER_BLOCK and tile_rows(output_rows) <= compute_units:
         return 16, 1

@@ -136,11 +136,14 @@ def test_launch_candidates_respect_each_kernels_limits():
         assert max(w for w, _ in pairs) == max_waves_per_block(batch, f32)
     # 5 or more BF16 rows of x that fit a block's LDS (9 x 2304: 41 KiB): the
     # resident-x kernel, (waves 1..12, blocks 1..tile rows); 9 rows at K =
-    # 9216 (162 KiB) do not fit, 6 (108 KiB) do
+    # 9216 (162 KiB) do not fit, 6 (108 KiB) do, but rows of 32+ K tiles on
+    # at most 160 tile rows (5/8 of 256 CUs) take the x-slab kernel
     from se12_amd.launch import rx_lds_bytes, uses_rx
 
     assert uses_rx(2304, 2304, 9) and not uses_rx(2304, 9216, 9) and not uses_rx(2304, 2304, 9, float32_activations=True)
-    assert uses_rx(2304, 9216, 6) and uses_rx(4096, 14336, 5) and not uses_rx(4096, 14336, 6) and uses_rx(256000, 2304, 5)
+    assert uses_rx(4608, 9216, 6) and uses_rx(4096, 14336, 5) and not uses_rx(4096, 14336, 6) and uses_rx(256000, 2304, 5)
+    assert not uses_rx(2304, 9216, 6) and not uses_rx(2560, 8192, 8) and uses_rx(2576, 8192, 8)
+    assert uses_rx(2304, 6144, 8) and uses_rx(2304, 9216, 8, compute_units=128)  # 144 rows > 5/8 of 128 CUs
     assert uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and not uses_rx(14336, 3584, 24)
     # 17..32 rows whose first 16 fit, on at most one tile row per CU: 16 rows
     # in LDS, batch group 1 from global memory, at most 8 waves

@@ -179,12 +179,15 @@ constexpr int kLutBytes = 1024;
 // (512 VGPRs per SIMD lane: 1024 threads = 4 waves per SIMD = 128 VGPRs
 // each, 512 threads = 256). The FAST estimates are fitted to hipcc's
 // allocation (per round: a tile's streams + its x slice, 37 VGPRs at batch 1,
-// 40 for the raw twin; 8 more per extra batch row); the GENERIC variants run
-// one tile per round without prefetch. The build fails if any variant spills.
+// 40 for the raw twin; 8 more per extra batch row; the fused batch-1 kernel
+// takes 85 / 122 without / with prefetch, so its prefetching variant fits
+// 1,024 threads); the GENERIC variants run one tile per round without
+// prefetch. The build fails if any variant spills.
 // `pf` = rounds kept in flight ahead of the one being decoded (0 or 1).
 constexpr int gemv_vgpr_estimate(int batch, bool raw, int g, int pf) {
-    return raw ? 24 + 4 * (batch - 1) + (pf + 1) * g * (40 + 8 * (batch - 1))
-               : 57 + 4 * (batch - 1) + (pf + 1) * g * (37 + 8 * (batch - 1));
+    return raw          ? 24 + 4 * (batch - 1) + (pf + 1) * g * (40 + 8 * (batch - 1))
+           : batch == 1 ? 48 + (pf + 1) * g * 37
+                        : 57 + 4 * (batch - 1) + (pf + 1) * g * (37 + 8 * (batch - 1));
 }
 constexpr int gemv_max_threads(int batch, bool xf32, bool raw, int g, int pf, bool generic) {
     return generic ? (batch >= 2 ? 512 : 1024)

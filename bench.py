@@ -440,11 +440,18 @@ def stress(device) -> dict:
     paths), against hipBLASLt BF16 and the raw twin: each timed over a
     rotation of cold copies in one graph (at least 8 launches per replay, so
     the replay's fixed cost of ~10 us spreads; HipBenchmarkTimer.
-    time_cold_rotation), median / p10 / p90 per launch."""
+    time_cold_rotation), median / p10 / p90 per launch of the run whose
+    median is the median of three runs (the first run over freshly written
+    copies read up to 10% high: 4608x36864 48.4 against 43.4 us)."""
     from se12_amd.hip import HipBenchmarkTimer, RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
     from se12_amd.micro import cold_copies
 
     timer = HipBenchmarkTimer(device.index)
+
+    def settled(ops):
+        runs = sorted((timer.time_cold_rotation(ops, 3, 10) for _ in range(3)), key=lambda r: r.median_us)
+        return runs[1]
+
     out = {}
     for name, n, k, seed in (("lm_head", 256000, 2304, 11), ("down_27b", 4608, 36864, 12)):
         w = heavy_tailed(n, k, seed, device)
@@ -456,11 +463,11 @@ def stress(device) -> dict:
         gen.manual_seed(seed + 100)
         x = torch.randn((1, k), generator=gen, device=device).to(torch.bfloat16)
         ys = [torch.empty((1, n), dtype=torch.float32, device=device) for _ in range(copies)]
-        st = timer.time_cold_rotation([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(kerns, ys)], 3, 10)
+        st = settled([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(kerns, ys)])
         del kerns
-        st_b = timer.time_cold_rotation([lambda m=m: torch.nn.functional.linear(x, m) for m in ws], 3, 10)
+        st_b = settled([lambda m=m: torch.nn.functional.linear(x, m) for m in ws])
         raws = [RawBf16MatVecKernel(m, max_batch=1) for m in ws]
-        st_r = timer.time_cold_rotation([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(raws, ys)], 3, 10)
+        st_r = settled([lambda kk=kk, y=y: kk.multiply(x, out=y) for kk, y in zip(raws, ys)])
         del raws
         us, us_b, us_r = st.median_us, st_b.median_us, st_r.median_us
         k0 = Se12MatVecKernel(enc, max_batch=1)

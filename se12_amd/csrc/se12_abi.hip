@@ -386,13 +386,12 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
         }
     } else if (tc > 32) {
         // long rows on many tile rows (4608x36864): one wave per block and
-        // splits of ~36 K tiles (B = 1: 42.3 us against 42.2 with 6 splits,
-        // 42.8 with 3 and 43.4 with 2 waves x 6), half again as many from 2
-        // rows per launch (B = 2 / 3 / 4: 43.0 / 44.0 / 46.9 against 43.5 /
-        // 45.1 / 47.7 with 3 splits)
+        // splits of ~24 K tiles (B = 1, heavy-tailed weights: 42.4 us
+        // against 43.4 with 4 splits of ~36 and 42.6 with 4 waves x 6;
+        // Gaussian weights 42.1-42.5 either way; B = 2 / 3 / 4: 43.0 / 44.0
+        // / 46.9 against 43.5 / 45.1 / 47.7 with 3 splits)
         waves = 1;
-        splits = std::max<int64_t>(1, (tc + 18) / 36);
-        if (bl >= 2) splits = splits * 3 / 2;
+        splits = std::max<int64_t>(1, (tc + 18) / 36) * 3 / 2;
     } else if (tiles <= 10 * cus) {
         // one wave per K tile; at 4 rows per launch 3 splits of 3 waves for
         // rows of 9 K tiles (2B q/k/v grouped, 256 x 9 tiles: 7.5 us against
@@ -435,17 +434,18 @@ static void default_launch(int64_t tr, int64_t tc, int32_t cu_count, int32_t s_c
             waves = tc % 2 == 1 ? (tc + 1) / 2 : (tr >= 3 * cus ? 2 : 8);
         waves = std::max<int64_t>(1, std::min<int64_t>(tc, waves));
     } else {
-        // many tiles per CU: short rows (256000x2304) take 6 waves at B = 1,
-        // 4 at B = 2 (129.9 us against 132.4 with 3) and 3 at B = 3..4
+        // many tiles per CU: short rows (256000x2304) take 4 waves at B = 1
+        // (heavy-tailed weights 133.5 us against 139.4 with 6, Gaussian 130.9
+        // against 132.9) and 2 (129.9 against 132.4 with 3), 3 at B = 3..4
         // (B = 4: 154 against 209 with 6); rows over 12 K tiles 8 waves
         // (36864x4608 B = 1: 41.1 us against 41.5 with 6; 256000x3584: 200
         // against 210 with 1), 4 at B = 2 (256000x3584: 198.5 against 202
         // with 8), at B = 3..4 on 256+ tiles per CU 2 (256000x3584 B = 4:
         // 231 against 258 with 8)
-        if (bl == 2)
+        if (bl == 2 || (bl == 1 && tc <= 12))
             waves = 4;
         else if (tc <= 12)
-            waves = bl >= 2 ? 3 : 6;
+            waves = 3;
         else
             waves = bl >= 3 && tiles >= 256 * cus ? 2 : 8;
         waves = std::min<int64_t>(waves, tc);

@@ -687,20 +687,14 @@ __attribute__((amdgpu_waves_per_eu(gemv_waves_per_simd(B, RAW, G, PF, GENERIC)))
         __syncthreads();
         if (!*flag) return;
         if (tid < 16 * B) {
-            // the splits' partials in groups of 8 loads issued together, added
-            // in ascending split order (a load per add waits a round trip per
-            // split)
-            const float* pp = &a.partial[(int64_t)b * a.Np + n];
-            const int64_t stride = (int64_t)B * a.Np;
+            // the splits' partials in ascending split order, one load per add:
+            // this path serves only launches with a decode-step tail (split
+            // launches without one meet in the pair tree above), and the
+            // smaller code keeps the cold-cache batch-1 launches short (the 2B
+            // q and k alone, 26 launches after an eviction: 5.11 / 4.92 us
+            // with 8 loads in flight here, 4.71 / 4.52 with one)
             v = 0.0f;
-            for (int s0 = 0; s0 < S; s0 += 8) {
-                float q[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) q[k] = s0 + k < S ? load_dev(pp + (s0 + k) * stride) : 0.0f;
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (s0 + k < S) v += q[k];
-            }
+            for (int ss = 0; ss < S; ++ss) v += load_dev(&a.partial[((int64_t)ss * B + b) * a.Np + n]);
         }
         if (tid == 0) __hip_atomic_store(&a.counters[tr], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

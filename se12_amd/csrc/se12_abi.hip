@@ -505,6 +505,17 @@ static void gemm_default_launch(se12_handle* const* hs, int32_t count, int32_t b
             best_dev = dev;
         }
     }
+    // one tile row per block on few rows of 32-48 K tiles (2304x9216 and
+    // 2048x9216 at 5..8 batch rows): one-wave blocks and splits of ~6 K
+    // tiles, no K groups (2304x9216 B = 5 / 6 / 8: 13.6 / 13.7 / 13.8 us
+    // against 15.2 / 15.2 / 15.3 with 2 K groups x 3 splits; 2048x9216 B = 8
+    // 13.4 against 13.8 with 4 x 2); longer rows keep the rule above
+    // (3584x14336 B = 8: 25.0 us with 4 K groups against 30.5 with 10 splits)
+    if (rows == 1 && m > 1 && h0->TC >= 32 && h0->TC <= 48) {
+        best_kg = 1;
+        best_s = std::max<int64_t>(1, std::min<int64_t>({(int64_t)kGemmMaxSplits, (int64_t)h0->s_cap,
+                                                         ceil_div(h0->TC, 6)}));
+    }
     *waves_out = (int32_t)(rows * best_kg);
     *splits_out = (int32_t)best_s;
 }

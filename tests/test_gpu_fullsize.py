@@ -101,6 +101,31 @@ def test_gate_9b_batch_sweep_default_launch(gpu, gate_9b, batch):
     assert torch.equal(y, yr)
 
 
+@pytest.mark.parametrize("rows,batch", [(2304, 5), (2304, 8), (2048, 8)])
+def test_long_rows_few_tile_rows_mfma_default_launch(gpu, rows, batch):
+    """2304x9216 and 2048x9216 at 5..8 batch rows: the x-slab kernel (x
+    would fit a block's LDS, but one resident-x block per tile row leaves CUs
+    idle) with one-wave blocks and 6 K splits under the default launch:
+    within REL_TOL of the oracle, the raw twin bit-identical."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel, encode_on_device
+    from se12_amd.launch import uses_rx
+
+    cols = 9216
+    assert not uses_rx(rows, cols, batch)
+    bits = o.normal_bf16(rows, cols, seed=700 + rows + batch, std=0.02)
+    w = bf16_tensor(bits, gpu)
+    fused, raw = Se12MatVecKernel(encode_on_device(w)), RawBf16MatVecKernel(w)
+    lc = fused.default_launch(batch)
+    assert (lc.threads_per_block.value, lc.blocks.value) == (64, 6 * rows // 16)
+    xb = o.normal_bf16(batch, cols, seed=800 + rows + batch, std=1.0)
+    x = bf16_tensor(xb, gpu)
+    y, yr = fused.multiply(x), raw.multiply(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y, yr)
+    enc = o.encode(bits.reshape(-1), rows, cols)
+    assert max_rel_error(y, o.gemv_reference(enc, o.bf16_bits_to_f32(xb))) <= REL_TOL
+
+
 @pytest.mark.parametrize("batch", [1, 2, 4])
 def test_9b_gate_up_grouped_default_launch(gpu, gate_9b, batch):
     """The 9B gate/up launch shape (two 14336x3584 matrices, 1,792 tile

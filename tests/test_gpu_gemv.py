@@ -263,12 +263,14 @@ def test_raw_twin_is_bit_identical_under_one_launch(gpu, shape):
             assert torch.equal(fused.multiply(x, launch=cfg), raw.multiply(x, launch=cfg)), (batch, cfg)
 
 
-@pytest.mark.parametrize("batch", [1, 8, 16, 24])
+@pytest.mark.parametrize("batch", [1, 2, 8, 16, 24])
 def test_graph_replay_matches_eager(gpu, batch):
     """Replays of a captured product equal the eager result, with eager work
-    between replays: the dot2 kernel (B = 1), the resident-x kernel (8), the
-    x-slab kernel with K splits (16) and the resident-x kernel with K splits
-    (24), whose arrival counters must be back at zero after every launch."""
+    between replays, at 2304x9216: the dot2 kernel (B = 1), the dot2 kernel
+    with 3 K splits meeting in the pair tree (2), the x-slab kernel with K
+    splits (8: one-wave blocks, 6 splits; 16) and the resident-x kernel with K
+    splits (24), whose pair slots and arrival counters must be back at zero
+    after every launch."""
     from se12_amd.hip import Se12MatVecKernel
 
     bits, enc = normal_case(2304, 9216, seed=0)

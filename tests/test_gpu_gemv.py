@@ -93,6 +93,30 @@ def test_gemv_float32_activations(gpu, batch):
     assert max_rel_error(y, ref) <= REL_TOL
 
 
+@pytest.mark.parametrize("batch", [2, 4])
+def test_float32_activations_through_the_pair_tree(gpu, batch):
+    """FP32 activations (the edge-handling dot2 variants) at 2304x9216 and 2-4
+    batch rows, whose default launch splits K in 3 (4 waves x 432 blocks) and
+    adds the splits in the pair tree: within REL_TOL of the oracle, run to run
+    identical, the raw twin bit-identical."""
+    from se12_amd.hip import RawBf16MatVecKernel, Se12MatVecKernel
+
+    bits, enc = normal_case(2304, 9216, seed=14)
+    k = Se12MatVecKernel(to_device(enc, gpu))
+    r = RawBf16MatVecKernel(bf16_tensor(bits, gpu))
+    lc = k.default_launch(batch)
+    assert (lc.threads_per_block.value, lc.blocks.value) == (256, 432)
+    rng = np.random.default_rng(100 + batch)
+    xf = rng.standard_normal((batch, 9216)).astype(np.float32)
+    x = torch.from_numpy(xf).to(gpu)
+    y1 = k.multiply(x).clone()
+    y2 = k.multiply(x)
+    yr = r.multiply(x, launch=lc)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2) and torch.equal(y1, yr)
+    assert max_rel_error(y1, o.gemv_reference(enc, xf)) <= REL_TOL
+
+
 @pytest.mark.parametrize("rows,cols", [(1, 1), (17, 257), (33, 300), (100, 2304), (2048, 2304), (64, 9216)])
 def test_gemv_ragged_and_escape_heavy(gpu, rows, cols):
     from se12_amd.hip import Se12MatVecKernel

@@ -813,6 +813,28 @@ def main(argv=None) -> int:
     log(f"[bench] down_proj launches: {us_launch:.2f} us each -> {achieved:.0f} GB/s of SE12 streams")
     del g_down
 
+    # the launch that takes the largest share of the step: the grouped gate/up
+    # product (2 x 9216x2304, 63.9 MB of streams per launch), timed the same
+    # way over its 26 layers and reported beside the down_proj roofline
+    gu = [[layer[4], layer[5]] for layer in stack]
+    g_gu = capture(lambda: [multiply_grouped([e["kern"] for e in es], es[0]["x"], outs=[e["y"] for e in es])
+                            for es in gu])
+    ms_gu = time_graph(g_gu, args.steps, args.warmup)
+    del g_gu
+    us_gu = ms_gu * 1e3 / len(gu)
+    bytes_gu = sum(e["enc"].byte_size() + e["n"] * 4 for e in gu[0]) + gu[0][0]["k"] * 2
+    result["roofline_step_dominant"] = {
+        "kernel": "se12::gemv_kernel, grouped gate/up (2 matrices per launch, batch 1)",
+        "shape": [[e["n"], e["k"]] for e in gu[0]],
+        "avg_launch_us": round(us_gu, 3),
+        "algorithmic_bytes_per_launch": bytes_gu,
+        "achieved": round(bytes_gu / (us_gu * 1e-6) / 1e9, 1),
+        "peak": HBM_PEAK_GBPS,
+        "frac": round(bytes_gu / (us_gu * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "share_of_step": round(us_gu * len(gu) / (ms * 1e3), 4),
+    }
+    log(f"[bench] gate/up launches: {us_gu:.2f} us each -> {bytes_gu / (us_gu * 1e-6) / 1e9:.0f} GB/s")
+
     if not args.only_fused:
         # hipBLASLt BF16 with the same grouping: one GEMV over concatenated weights
         cat = []

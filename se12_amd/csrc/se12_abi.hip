@@ -664,10 +664,18 @@ static RxLayout rx_layout(se12_handle* const* hs, int32_t count, int32_t batch) 
            (int64_t)(rx_lds_bytes(ceil_div(tc, sp) * SE12_TILE_COLS, batch) + kLutBytes) > lds)
         ++sp;
     if (sp > std::min<int32_t>(kRxMaxSplits, tc)) return {0, 0};
-    // what measured faster than the x-slab kernel: single matrices, and two
-    // splits only on long launches of two batch groups (the cross-block
-    // sums' round trips end every wave)
-    if (count > 1 || (sp == 2 && (batch <= 16 || rows * tc < 16384))) return {0, 0};
+    // what measured faster than the x-slab kernel: single matrices; two
+    // splits at one batch group only on 8192+ tiles (3584x14336 B = 6 / 8 /
+    // 11: 23.9 / 23.8 / 24.6 us against 24.5 / 24.3 / 26.1; 4096x14336 24.5-
+    // 25.5 / 24.4-24.7 / 24.8-25.0 against 28.5 / 27.8-27.9 / 25.9-26.1;
+    // 4608x9216 B = 9 / 12 / 16 22.1-22.7 / 22.5-22.6 / 22.9-23.1 against
+    // 24.0-24.1 / 24.0 / 23.8; but 2304x9216 B = 9..16 17.6-18.3 against
+    // 15.0-15.3), at two batch groups on every size (14336x3584
+    // B = 24 / 32: 24.4 / 25.0-26.0 against 25.4-26.1 / 25.5-26.3; 8192x4096
+    // 18.9-19.2 / 19.3-19.8 against 25.4-25.9; 6144x4096 17.3 / 17.8 against
+    // 19.8 / 20.0; 4608x4096 16.0 / 16.7 against 17.2 / 17.5), the x-slab
+    // launch leaving CUs idle there (4 tile rows per block)
+    if (count > 1 || (sp == 2 && batch <= 16 && rows * tc < 8192)) return {0, 0};
     return {batch, sp};
 }
 

@@ -37,8 +37,8 @@ MFMA_MAX_WAVES_GENERIC = 4   # the edge-handling MFMA variants (K % 256 != 0 or 
 # 1's x then comes from global memory, at most RX_MAX_WAVES_XG waves per
 # block). A single matrix whose x fits neither way can split K: split s of S
 # takes K tiles [s TC / S, (s + 1) TC / S) of every row and holds only their
-# columns of x (the fewest splits that fit, 3..RX_MAX_SPLITS, or 2 on
-# launches of 16384+ tiles with 17+ batch rows; the library adds the splits'
+# columns of x (the fewest splits that fit, 2..RX_MAX_SPLITS, but 2 at 16 or
+# fewer batch rows only on 8192+ tiles; the library adds the splits'
 # partial sums in split order). Its launch is (waves per block 1..12, blocks
 # per matrix and split 1..tile rows) with blocks = that count x splits x
 # matrices; the launch fixes the K groups (rx_kgroups) and with them the order
@@ -105,7 +105,8 @@ def rx_layout(output_rows: int, k: int, batch: int, float32_activations: bool = 
     on rows of 32+ K tiles with at most 5/8 of the CUs' worth of tile rows;
     (16, 1) for 17..32 rows whose first 16 fit on a matrix of at most one
     tile row per CU; (batch, S) with the fewest K splits S whose share of x's
-    columns fits, where splits pay; else (0, 0), the x-slab kernel."""
+    columns fits, except S = 2 at 16 or fewer rows on fewer than 8192 tiles;
+    else (0, 0), the x-slab kernel."""
     if not (uses_mfma(batch, float32_activations) and aligned_x
             and not runs_generic(output_rows, k, float32_activations)):
         return 0, 0
@@ -118,7 +119,7 @@ def rx_layout(output_rows: int, k: int, batch: int, float32_activations: bool = 
     tc = k_tiles(k)
     for s in range(2, min(RX_MAX_SPLITS, tc) + 1):
         if rx_lds_bytes(-(-tc // s) * 256, batch) + LUT_BYTES <= LDS_PER_BLOCK:
-            if s == 2 and (batch <= 16 or tile_rows(output_rows) * tc < 16384):
+            if s == 2 and batch <= 16 and tile_rows(output_rows) * tc < 8192:
                 return 0, 0
             return batch, s
     return 0, 0

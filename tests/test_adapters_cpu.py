@@ -111,10 +111,14 @@ def test_translation_keeps_the_block_and_refuses_uncovered_launches():
     assert launch.waves_and_splits(cfg, 2304, 1, 9216) == (4, 1)
     cfg = launch.from_reference_configuration(RefLaunch(RefThreads(32), RefBlocks(2304)), 2304, 9216, 1)
     assert launch.waves_and_splits(cfg, 2304, 1, 9216) == (1, 1)
-    # B = 24 on the x-slab MFMA kernel: 4 tile rows per block, 448 threads
-    # (7 waves) -> 8 waves
+    # B = 24 on the x-slab MFMA kernel (4608x36864: x's columns would need 12
+    # resident-x splits): 4 tile rows per block, 448 threads (7 waves) -> 8 waves
+    cfg = launch.from_reference_configuration(RefLaunch(RefThreads(448), RefBlocks(25000)), 4608, 36864, 24)
+    assert launch.waves_and_splits(cfg, 4608, 24, 36864) == (8, 1)
+    # B = 24 at 14336x3584 on the resident-x kernel with 2 K splits: 7 waves,
+    # 896 tile rows over 128 blocks of 7 row slots in each split
     cfg = launch.from_reference_configuration(RefLaunch(RefThreads(448), RefBlocks(25000)), 14336, 3584, 24)
-    assert launch.waves_and_splits(cfg, 14336, 24, 3584) == (8, 1)
+    assert launch.waves_and_splits(cfg, 14336, 24, 3584) == (7, 128 * 2)
     # B = 24 at K = 9216 on the resident-x kernel with 3 K splits: 7 waves,
     # one tile row per slot, in each split
     cfg = launch.from_reference_configuration(RefLaunch(RefThreads(448), RefBlocks(4000)), 2304, 9216, 24)
@@ -156,23 +160,21 @@ def test_translation_follows_the_adapters_compute_units(batch):
     """A matrix of 256 tile rows at K = 3584: x of 24 or 32 rows does not fit
     a block's LDS but its first 16 rows do, and on a GPU of 256+ CUs (one
     tile row per CU) such batches run the resident-x kernel with batch group
-    1's x from global memory; with 132 compute units the library picks the
-    x-slab kernel instead. The translation must follow the count the library
-    was given."""
+    1's x from global memory; with 132 compute units the library splits K
+    in two instead and keeps every row of x. The translation must follow the
+    count the library was given."""
     rows, k = 4096, 3584
     ref = RefLaunch(RefThreads(256), RefBlocks(-(-rows * batch // 8)))
     cfg256 = launch.from_reference_configuration(ref, rows, k, batch, compute_units=256)
-    assert launch.uses_rx(rows, k, batch, compute_units=256)
+    assert launch.rx_layout(rows, k, batch, compute_units=256) == (16, 1)
     assert launch.waves_and_splits(cfg256, rows, batch, k, compute_units=256) == (4, 64)
-    assert launch.rx_staged_rows(rows, k, batch, compute_units=256) == 16
-    assert not launch.uses_rx(rows, k, batch, compute_units=132)
-    # the rows whose x fits whole run the resident-x kernel on either GPU
-    assert launch.uses_rx(rows, k, 20, compute_units=132) and launch.uses_rx(rows, k, 20, compute_units=256)
+    assert launch.rx_layout(rows, k, batch, compute_units=132) == (batch, 2)
+    # the rows whose x fits whole run the resident-x kernel unsplit on either GPU
+    assert launch.rx_layout(rows, k, 20, compute_units=132) == (20, 1) == launch.rx_layout(rows, k, 20, compute_units=256)
     cfg132 = launch.from_reference_configuration(ref, rows, k, batch, compute_units=132)
-    # the x-slab kernel: a multiple of ceil(batch / 8) (4 for 3) tile rows per block, no K split
-    lo = launch.mfma_min_waves(batch)
-    assert launch.waves_and_splits(cfg132, rows, batch, k, compute_units=132) == (4 if lo <= 4 else lo, 1)
-    assert cfg132.blocks.value == -(-launch.tile_rows(rows) // lo)
+    # 4 row slots per block: 64 blocks in each of the 2 K splits
+    assert launch.waves_and_splits(cfg132, rows, batch, k, compute_units=132) == (4, 64 * 2)
+    assert cfg132.blocks.value == 64 * 2
     # and the candidates the tuner would time follow the same rule
     c132 = launch.candidate_configurations(rows, k, batch, compute_units=132)
     for c in c132:

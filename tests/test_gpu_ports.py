@@ -264,7 +264,8 @@ def test_tuner_writes_through_the_cache_port(gpu, tmp_path):
 @pytest.mark.parametrize("batch", [24, 32])
 def test_reference_launch_on_a_smaller_gpu_count(gpu, batch):
     """An adapter told of 132 compute units runs the library's kernel choice
-    for 132 (x-slab at 4096x3584, batch 24 / 32) and translates reference
+    for 132 (at 4096x3584, batch 24 / 32: the resident-x kernel with two K
+    splits, where 256 CUs keep 16 rows of x unsplit) and translates reference
     launches for that choice."""
     from test_adapters_cpu import RefBlocks, RefLaunch, RefThreads
 

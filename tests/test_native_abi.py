@@ -125,11 +125,12 @@ def test_launch_candidates_respect_each_kernels_limits():
         waves_and_splits(configuration(6, 1, 2304, batch=17), 2304, batch=17)
     with pytest.raises(ValueError, match="multiple of 2"):
         waves_and_splits(configuration(3, 1, 2304, batch=9), 2304, batch=9)
-    # (the x-slab kernel serves 14336x3584 at 24 and 32 rows)
-    assert all(waves_and_splits(c, 14336, batch=24, k=3584)[0] % 4 == 0 for c in candidate_configurations(14336, 3584, batch=24))
-    assert min(waves_and_splits(c, 14336, batch=32, k=3584)[0] for c in candidate_configurations(14336, 3584, batch=32)) == 4
+    # (the x-slab kernel serves 4608x36864 at 24 and 32 rows: x's columns
+    # would need 12 and 16 resident-x splits)
+    assert all(waves_and_splits(c, 4608, batch=24, k=36864)[0] % 4 == 0 for c in candidate_configurations(4608, 36864, batch=24))
+    assert min(waves_and_splits(c, 4608, batch=32, k=36864)[0] for c in candidate_configurations(4608, 36864, batch=32)) == 4
     assert max_waves_per_block(1) == 16 and max_waves_per_block(6) == 8
-    for rows, k, batch, f32, max_s in ((2304, 9216, 1, False, 36), (14336, 3584, 32, False, 12), (2304, 9216, 6, True, 36)):
+    for rows, k, batch, f32, max_s in ((2304, 9216, 1, False, 36), (4608, 36864, 32, False, 16), (2304, 9216, 6, True, 36)):
         cfgs = candidate_configurations(rows, k, batch=batch, float32_activations=f32)
         pairs = [waves_and_splits(c, rows, batch=batch, k=k, float32_activations=f32) for c in cfgs]
         assert max(s for _, s in pairs) == max_s
@@ -141,18 +142,20 @@ def test_launch_candidates_respect_each_kernels_limits():
     from se12_amd.launch import rx_lds_bytes, uses_rx
 
     assert uses_rx(2304, 2304, 9) and not uses_rx(2304, 9216, 9) and not uses_rx(2304, 2304, 9, float32_activations=True)
-    assert uses_rx(4608, 9216, 6) and uses_rx(4096, 14336, 5) and not uses_rx(4096, 14336, 6) and uses_rx(256000, 2304, 5)
+    assert uses_rx(4608, 9216, 6) and uses_rx(4096, 14336, 5) and uses_rx(4096, 14336, 6) and uses_rx(256000, 2304, 5)
     assert not uses_rx(2304, 9216, 6) and not uses_rx(2560, 8192, 8) and uses_rx(2576, 8192, 8)
     assert uses_rx(2304, 6144, 8) and uses_rx(2304, 9216, 8, compute_units=128)  # 144 rows > 5/8 of 128 CUs
-    assert uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and not uses_rx(14336, 3584, 24)
+    assert uses_rx(14336, 3584, 8) and uses_rx(14336, 3584, 16) and uses_rx(14336, 3584, 24)
     # 17..32 rows whose first 16 fit, on at most one tile row per CU: 16 rows
     # in LDS, batch group 1 from global memory, at most 8 waves
-    from se12_amd.launch import rx_max_waves, rx_staged_rows
+    from se12_amd.launch import rx_max_waves, rx_splits, rx_staged_rows
 
     assert rx_staged_rows(4096, 3584, 32) == 16 and rx_staged_rows(4096, 3584, 16) == 16
     assert rx_staged_rows(4096, 3584, 24) == 16 and rx_staged_rows(4096, 2304, 32) == 32
-    assert rx_staged_rows(4112, 3584, 32) == 0 and rx_staged_rows(4096, 14336, 17) == 17
-    assert rx_staged_rows(4096, 3584, 32, compute_units=128) == 0
+    # past one tile row per CU, two K splits with all the rows of x
+    assert rx_staged_rows(4112, 3584, 32) == 32 and rx_splits(4112, 3584, 32) == 2
+    assert rx_staged_rows(4096, 14336, 17) == 17
+    assert rx_staged_rows(4096, 3584, 32, compute_units=128) == 32 and rx_splits(4096, 3584, 32, compute_units=128) == 2
     assert rx_max_waves(4096, 3584, 32) == 8 and rx_max_waves(4096, 3584, 16) == 12 and rx_max_waves(14336, 3584, 16) == 12
     assert not uses_rx(2304, 2300, 9) and not uses_rx(2300, 2304, 9) and not uses_rx(256000, 2304, 4)
     assert rx_lds_bytes(9216, 6) == 6 * 1152 * 16 and rx_lds_bytes(2304, 5) == 1472 * 16
@@ -163,7 +166,7 @@ def test_launch_candidates_respect_each_kernels_limits():
 def test_resident_x_k_split_rule():
     """A single matrix whose x fits a block's LDS neither whole nor as its
     first 16 rows splits K into the fewest ranges whose columns of x fit
-    (3..8; 2 only on launches of 16384+ tiles with 17+ rows); the x-slab
+    (2..8; 2 at up to 16 rows only on launches of 8192+ tiles); the x-slab
     kernel serves the rest. Blocks then count K splits too."""
     from se12_amd.launch import (candidate_configurations, rx_configuration, rx_kgroups, rx_layout, rx_splits,
                                  waves_and_splits)
@@ -173,8 +176,11 @@ def test_resident_x_k_split_rule():
     assert rx_layout(2304, 9216, 24) == (24, 3) and rx_layout(2304, 9216, 32) == (32, 4)
     assert rx_layout(4608, 36864, 9) == (9, 5) and rx_layout(4608, 36864, 16) == (16, 8)
     assert rx_layout(36864, 4608, 24) == (24, 2)      # 2304 tile rows x 18 K tiles
-    assert rx_layout(3584, 14336, 9) == (0, 0)        # two splits at one batch group
-    assert rx_layout(2304, 9216, 16) == (0, 0) and rx_layout(14336, 3584, 32) == (0, 0)
+    assert rx_layout(3584, 14336, 9) == (9, 2)        # two splits at one batch group: 12,544 tiles
+    assert rx_layout(2304, 9216, 16) == (0, 0)        # 5,184 tiles: the x-slab kernel
+    assert rx_layout(14336, 3584, 32) == (32, 2) and rx_layout(14336, 3584, 23) == (23, 2)
+    assert rx_layout(14336, 3584, 22) == (22, 1)      # x fits whole
+    assert rx_layout(4608, 4096, 24) == (24, 2)       # two batch groups: two splits on any size
     assert rx_layout(4608, 36864, 24) == (0, 0)       # 12 splits: over the limit
     assert rx_layout(4096, 3584, 32) == (16, 1) and rx_layout(2304, 2304, 32) == (32, 1)
     assert rx_splits(2304, 9216, 4) == 0 and rx_splits(2304, 9216, 24, float32_activations=True) == 0

@@ -40,7 +40,7 @@ def test_noalloc_equals_the_allocating_product_twice_in_a_row(gpu):
     from se12_amd.hip import Se12MatVecKernel
     from se12_amd.launch import configuration, rx_configuration, rx_layout, uses_rx
 
-    assert not uses_rx(4608, 9216, 16) and not uses_rx(1040, 9216, 9) and uses_rx(1040, 2304, 9)
+    assert rx_layout(4608, 9216, 16) == (16, 2) and not uses_rx(1040, 9216, 9) and uses_rx(1040, 2304, 9)
     assert rx_layout(1040, 9216, 24) == (24, 3)
     big_bits, big_enc = normal_case(4608, 9216, seed=41)
     small_bits, small_enc = normal_case(1040, 2304, seed=42)
@@ -51,8 +51,8 @@ def test_noalloc_equals_the_allocating_product_twice_in_a_row(gpu):
     cases = [
         (big, big_enc, 4, configuration(4, 9, 4608, 4)),       # dot2, 9 K splits over 4 batch rows
         (small, small_enc, 2, configuration(3, 3, 1040, 2)),   # a smaller input after it
-        (big, big_enc, 16, configuration(4, 3, 4608, 16)),     # MFMA (x over a block's LDS), 3 K splits
-        (long, long_enc, 9, configuration(2, 3, 1040, 9)),     # smaller again, MFMA, 3 K splits
+        (big, big_enc, 16, rx_configuration(8, 128, splits=2)),  # resident-x (x over a block's LDS), 2 K splits
+        (long, long_enc, 9, configuration(2, 3, 1040, 9)),     # smaller again, x-slab MFMA, 3 K splits
         (long, long_enc, 24, rx_configuration(8, 32, splits=3)),  # resident-x kernel, 3 K splits
         (small, small_enc, 9, rx_configuration(4, 7)),         # resident-x kernel (no split-K scratch)
         (small, small_enc, 1, None),                            # the default launch

@@ -62,9 +62,12 @@ __device__ __forceinline__ void unpack8(const uint4 r, float* v) {
     }
 }
 
-// (value, index) with the larger value, the smaller index on a tie
+// (value, index) with the larger value, the smaller index on a tie; NaN
+// ranks above every number (torch.argmax's order), so a row of NaNs still
+// gives an index in the vocabulary (its first NaN) and never the initial one
 __device__ __forceinline__ void keep_first_max(float& bv, int& bi, float v, int i) {
-    if (v > bv || (v == bv && i < bi)) {
+    const bool vn = v != v, bn = bv != bv;
+    if (vn ? (!bn || i < bi) : (!bn && (v > bv || (v == bv && i < bi)))) {
         bv = v;
         bi = i;
     }

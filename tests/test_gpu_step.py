@@ -251,6 +251,32 @@ def test_logits_argmax_and_token_slot(gpu, dtype, vocab):
     assert bool((ws[: 4 * rows] == 0).all())
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_logits_argmax_with_nan_logits(gpu, dtype):
+    """NaN ranks above every number, as in torch.argmax: a row with NaNs
+    gives its first NaN (across vocabulary slices too), a row of NaNs its
+    first index, so the token id always indexes the vocabulary."""
+    rows, vocab, max_len = 3, 256000, 8
+    g = _gen(gpu, 23)
+    z = torch.randn((rows, vocab), generator=g, device=gpu) * 5
+    z[0, 100] = 1000.0
+    z[0, vocab - 5] = float("nan")
+    z[0, vocab // 2 + 3] = float("nan")
+    z[1].fill_(float("nan"))
+    z[2, 1] = float("nan")
+    logits = z.to(dtype)
+    ids = torch.full((rows,), -1, dtype=torch.int64, device=gpu)
+    tokens = torch.full((rows, max_len), -1, dtype=torch.int64, device=gpu)
+    step = torch.tensor(0, dtype=torch.int64, device=gpu)
+    ws = torch.zeros(nat.lib().se12_step_logits_workspace(rows, vocab), dtype=torch.uint8, device=gpu)
+    _argmax(logits, dtype, vocab, rows, vocab, 30.0, None, ids, tokens, max_len, step, ws)
+    torch.cuda.synchronize()
+    assert ids.tolist() == [vocab // 2 + 3, 0, 1]
+    assert torch.equal(ids, torch.argmax(logits.float(), dim=1))
+    assert torch.equal(tokens[:, 0], ids)
+    assert bool((ws[: 4 * rows] == 0).all())
+
+
 def test_advance(gpu):
     pos = torch.tensor(41, dtype=torch.int64, device=gpu)
     step = torch.tensor(2, dtype=torch.int64, device=gpu)

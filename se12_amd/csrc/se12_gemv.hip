@@ -149,7 +149,7 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
     const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
     auto lo = [](uint32_t u) { return bf16_to_f(u & 0xFFFFu); };
     auto hi = [](uint32_t u) { return bf16_to_f(u >> 16); };
-    auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
+    auto pack = [](float a, float c) { return f_to_bf16x2(a, c); };
     const int trp = (k + 15) / 16;
     const float* row_ss = reinterpret_cast<const float*>(stage + (size_t)B * k * 6 + (size_t)k * 4);
     for (int b = 0; b < B; ++b) {
@@ -178,6 +178,59 @@ __device__ void gemv_prologue_compute(const GemvPrologue& pr, int64_t K, char* s
         // the new residual (BF16-exact) goes to x's place in LDS, where the
         // same thread turns it into x
         uint2* xb = reinterpret_cast<uint2*>(xs + (size_t)b * k);
+        // 4-element groups a thread holds in registers between the passes
+        // (batch 1: at 2..4 rows the registers of the weights in flight
+        // leave no room)
+        constexpr int U = B == 1 ? 4 : 1;
+        if (B == 1 && n4 <= U * nt) {
+            // every LDS read of a pass issued at once (one latency per pass),
+            // the residual kept in registers; the same arithmetic, in the
+            // same order, as the loops below
+            float4 v[U];
+            uint2 c1[U], c2[U], c3[U], rp[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = tid + u * nt;
+                if (g < n4) {
+                    v[u] = yb[g];
+                    c1[u] = w1s[g];
+                    c2[u] = rb[g];
+                    c3[u] = w2s[g];
+                }
+            }
+            float ss2 = 0.0f;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (tid + u * nt < n4) {
+                    float4 r;
+                    r.x = round_bf16(lo(c2[u].x) + round_bf16(rms_scale(round_bf16(v[u].x), inv, lo(c1[u].x))));
+                    r.y = round_bf16(hi(c2[u].x) + round_bf16(rms_scale(round_bf16(v[u].y), inv, hi(c1[u].x))));
+                    r.z = round_bf16(lo(c2[u].y) + round_bf16(rms_scale(round_bf16(v[u].z), inv, lo(c1[u].y))));
+                    r.w = round_bf16(hi(c2[u].y) + round_bf16(rms_scale(round_bf16(v[u].w), inv, hi(c1[u].y))));
+                    rp[u] = make_uint2(pack(r.x, r.y), pack(r.z, r.w));
+                    ss2 += r.x * r.x;
+                    ss2 += r.y * r.y;
+                    ss2 += r.z * r.z;
+                    ss2 += r.w * r.w;
+                }
+            }
+            const float inv2 = rms_inv(block_sum(ss2, sh), k, pr.eps);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int g = tid + u * nt;
+                if (g < n4) {
+                    const float4 r = make_float4(lo(rp[u].x), hi(rp[u].x), lo(rp[u].y), hi(rp[u].y));
+                    const uint2 h = make_uint2(pack(rms_scale(r.x, inv2, lo(c3[u].x)), rms_scale(r.y, inv2, hi(c3[u].x))),
+                                               pack(rms_scale(r.z, inv2, lo(c3[u].y)), rms_scale(r.w, inv2, hi(c3[u].y))));
+                    xb[g] = h;
+                    if (writer) {
+                        reinterpret_cast<uint2*>(pr.res_out + (int64_t)b * K)[g] = rp[u];
+                        reinterpret_cast<uint2*>(pr.h_out + (int64_t)b * K)[g] = h;
+                    }
+                }
+            }
+            continue;
+        }
         float ss2 = 0.0f;
         for (int g = tid; g < n4; g += nt) {
             const float4 v = yb[g];
@@ -314,7 +367,7 @@ __device__ void gemv_epilogue(const GemvGroupArgs& ga, int tr, float* lds) {
         for (int g = tid; g < n4; g += nt) {
             const float4 r = buf[g];
             const uint2 w = w2s[g];
-            auto pack = [](float a, float c) { return (uint32_t)f_to_bf16(a) | ((uint32_t)f_to_bf16(c) << 16); };
+            auto pack = [](float a, float c) { return f_to_bf16x2(a, c); };
             res[g] = make_uint2(pack(r.x, r.y), pack(r.z, r.w));
             out[g] = make_uint2(pack(rms_scale(r.x, inv2, lo(w.x)), rms_scale(r.y, inv2, hi(w.x))),
                                 pack(rms_scale(r.z, inv2, lo(w.y)), rms_scale(r.w, inv2, hi(w.y))));

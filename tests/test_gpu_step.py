@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
@@ -275,6 +276,34 @@ def test_logits_argmax_with_nan_logits(gpu, dtype):
     assert torch.equal(ids, torch.argmax(logits.float(), dim=1))
     assert torch.equal(tokens[:, 0], ids)
     assert bool((ws[: 4 * rows] == 0).all())
+
+
+def test_bf16_rounding_of_fp32_inputs(gpu):
+    """The step kernels round FP32 inputs to BF16 with the hardware
+    conversion; it must give the integer round-to-nearest-even form, a NaN its
+    top 16 bits with the quiet bit set. Through the logits kernel (soft cap
+    off: its BF16 logits are the inputs rounded): ties, subnormals, the
+    overflow to infinity, signalling and quiet NaNs, and 2^20 random bit
+    patterns."""
+    special = np.array([0x00000000, 0x80000000, 0x00000001, 0x007FFFFF, 0x00008000, 0x00018000, 0x3F808000,
+                        0x3F818000, 0x3F80FFFF, 0x7F7FFFFF, 0x7F7F8000, 0x7F7F7FFF, 0x7F800000, 0xFF800000,
+                        0x7F800001, 0x7FBFFFFF, 0x7FC00000, 0xFFC12345, 0xFF800001, 0x7FFFFFFF], dtype=np.uint32)
+    rng = np.random.default_rng(7)
+    u = np.concatenate([special, rng.integers(0, 2 ** 32, size=1 << 20, dtype=np.uint64).astype(np.uint32)])
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    want = np.where(nan, (u >> 16) | 0x40, (u.astype(np.uint64) + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    vocab = int(u.size)
+    logits = torch.from_numpy(u.view(np.float32).copy()).to(gpu).view(1, vocab)
+    out = torch.empty((1, vocab), dtype=torch.bfloat16, device=gpu)
+    ids = torch.full((1,), -1, dtype=torch.int64, device=gpu)
+    tokens = torch.full((1, 4), -1, dtype=torch.int64, device=gpu)
+    step = torch.tensor(0, dtype=torch.int64, device=gpu)
+    ws = torch.zeros(nat.lib().se12_step_logits_workspace(1, vocab), dtype=torch.uint8, device=gpu)
+    _argmax(logits, torch.float32, vocab, 1, vocab, 0.0, out, ids, tokens, 4, step, ws)
+    torch.cuda.synchronize()
+    got = out.view(torch.int16).cpu().numpy().view(np.uint16).reshape(-1)
+    assert np.array_equal(got, want), int((got != want).sum())
+    assert 0 <= int(ids[0]) < vocab
 
 
 def test_advance(gpu):

@@ -597,7 +597,7 @@ __global__ void gelu_mul_kernel(const void* gate, const void* up, int64_t stride
 // ---------------------------------------------------------------------------
 
 constexpr int kArgmaxThreads = 256;
-constexpr int kArgmaxPer = 16;
+constexpr int kArgmaxPer = 8;
 constexpr int kArgmaxSlice = kArgmaxThreads * kArgmaxPer;
 
 struct ArgmaxArgs {

@@ -254,7 +254,7 @@ def test_step_kernels_reject_invalid_arguments():
     with pytest.raises(nat.Se12Error, match="NULL"):
         nat.step_check(attention(8, 4, 256, 640, None, need))
     ws = lib.se12_step_logits_workspace(2, 256000)
-    assert ws == 256 + 512 + 512            # counters; 2 rows x 63 slices of 4,096 logits: values, indices
+    assert ws == 256 + 1024 + 1024          # counters; 2 rows x 125 slices of 2,048 logits: values, indices
     assert lib.se12_step_logits_workspace(0, 10) < 0
 
     def argmax(rows, vocab, stride, wsp, ws_bytes):

@@ -76,11 +76,11 @@ int se12_step_gelu_mul(const void* gate, const void* up, int32_t dtype, int64_t 
  * and to tokens[row * token_stride + *step] (skipped when *step is outside
  * [0, token_stride)). rows <= 65535.
  *
- * Blocks over slices of 4,096 logits per row; `workspace` (device, 256-byte
+ * Blocks over slices of 2,048 logits per row; `workspace` (device, 256-byte
  * aligned, se12_step_logits_workspace() bytes) holds their partial results
- * and per-row arrival counters: zero-fill it once before its first use; each
- * call leaves the counters at zero again. Calls sharing a workspace must not
- * run concurrently. */
+ * and arrival counters: zero-fill it once before its first use; each call
+ * leaves the counters at zero again. Calls sharing a workspace must not run
+ * concurrently. */
 int64_t se12_step_logits_workspace(int32_t rows, int32_t vocab);
 
 int se12_step_logits_argmax(const void* logits, int32_t dtype, int64_t stride, int32_t rows, int32_t vocab, float softcap,
@@ -89,6 +89,16 @@ int se12_step_logits_argmax(const void* logits, int32_t dtype, int64_t stride, i
 
 /* *pos += 1, *step += 1 (device counters of a captured decode loop). */
 int se12_step_advance(int64_t* pos, int64_t* step, void* stream);
+
+/* se12_step_logits_argmax followed by se12_step_advance, in one launch: once
+ * every row's pick is stored (the rows read *step first), the last row's
+ * final block sets *pos += 1 and *step += 1. Same workspace. Saves the
+ * decode loop the advance launch; no counterpart in the reference, whose
+ * sampling is the framework's. */
+int se12_step_logits_argmax_advance(const void* logits, int32_t dtype, int64_t stride, int32_t rows, int32_t vocab,
+                                    float softcap, uint16_t* logits_out, int64_t* ids, int64_t* tokens,
+                                    int64_t token_stride, int64_t* step, int64_t* pos, void* workspace,
+                                    int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -167,6 +167,11 @@ SIGNATURES = {
          c_i64, c_void_p],
     ),
     "se12_step_advance": (c_i32, [c_void_p, c_void_p, c_void_p]),
+    "se12_step_logits_argmax_advance": (
+        c_i32,
+        [c_void_p, c_i32, c_i64, c_i32, c_i32, ctypes.c_float, c_void_p, c_void_p, c_void_p, c_i64, c_void_p, c_void_p,
+         c_void_p, c_i64, c_void_p],
+    ),
 }
 
 STEP_BF16 = 0

@@ -609,10 +609,11 @@ struct ArgmaxArgs {
     int64_t* ids;
     int64_t* tokens;
     int64_t token_stride;
-    const int64_t* step;
+    int64_t* step;          // read only unless pos is set
+    int64_t* pos;           // NULL, or advance pos and step once every row's pick is stored
     float* part_v;          // [rows, blocks]
     int* part_i;            // [rows, blocks]
-    int* counters;          // [rows], zero between launches
+    int* counters;          // [rows + 1]: per-row block arrivals, then row arrivals; zero between launches
 };
 
 template <int DT>
@@ -683,6 +684,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void logits_argmax_kernel(ArgmaxArg
         const int64_t st = *a.step;
         if (st >= 0 && st < a.token_stride) a.tokens[(int64_t)r * a.token_stride + st] = bi;
         if (nblk > 1) __hip_atomic_store(&a.counters[r], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.pos) {
+            // every row has read the step before the last row's block moves
+            // it: a row arrives only once its step load has returned (the
+            // wait is also a compiler barrier)
+            bool last = true;
+            const int rows = (int)gridDim.y;
+            if (rows > 1) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                last = __hip_atomic_fetch_add(&a.counters[rows], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == rows - 1;
+            }
+            if (last) {
+                if (rows > 1) __hip_atomic_store(&a.counters[rows], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *a.pos += 1;
+                *a.step = st + 1;
+            }
+        }
     }
 }
 
@@ -703,6 +720,11 @@ thread_local char g_step_err[256] = "";
 
 int step_fail(const char* msg) {
     snprintf(g_step_err, sizeof g_step_err, "%s", msg);
+    return SE12_STEP_E_INVALID;
+}
+
+int step_fail(const char* who, const char* msg) {
+    snprintf(g_step_err, sizeof g_step_err, "%s: %s", who, msg);
     return SE12_STEP_E_INVALID;
 }
 
@@ -767,7 +789,7 @@ ArgmaxLayout argmax_layout(int32_t rows, int32_t vocab) {
     ArgmaxLayout l;
     l.blocks = (vocab + kArgmaxSlice - 1) / kArgmaxSlice;
     l.counters = 0;
-    l.part_v = up256((int64_t)rows * sizeof(int));
+    l.part_v = up256((int64_t)(rows + 1) * sizeof(int));
     l.part_i = l.part_v + up256((int64_t)rows * l.blocks * sizeof(float));
     l.total = l.part_i + up256((int64_t)rows * l.blocks * sizeof(int));
     return l;
@@ -884,17 +906,21 @@ int64_t se12_step_logits_workspace(int32_t rows, int32_t vocab) {
     return argmax_layout(rows, vocab).total;
 }
 
-int se12_step_logits_argmax(const void* logits, int32_t dtype, int64_t stride, int32_t rows, int32_t vocab, float softcap,
-                            uint16_t* logits_out, int64_t* ids, int64_t* tokens, int64_t token_stride,
-                            const int64_t* step, void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int launch_argmax(const char* who, const void* logits, int32_t dtype, int64_t stride, int32_t rows, int32_t vocab,
+                  float softcap, uint16_t* logits_out, int64_t* ids, int64_t* tokens, int64_t token_stride,
+                  int64_t* step, int64_t* pos, void* workspace, int64_t workspace_bytes, void* stream) {
     if (!logits || !ids || !tokens || !step || !workspace || rows <= 0 || rows > 65535 || vocab <= 0 || stride < vocab ||
         !dtype_ok(dtype))
-        return step_fail("se12_step_logits_argmax: bad argument");
+        return step_fail(who, "bad argument");
     const ArgmaxLayout l = argmax_layout(rows, vocab);
-    if (workspace_bytes < l.total) return step_fail("se12_step_logits_argmax: workspace too small");
-    if (reinterpret_cast<uintptr_t>(workspace) % 256) return step_fail("se12_step_logits_argmax: workspace not 256-byte aligned");
+    if (workspace_bytes < l.total) return step_fail(who, "workspace too small");
+    if (reinterpret_cast<uintptr_t>(workspace) % 256) return step_fail(who, "workspace not 256-byte aligned");
     char* ws = static_cast<char*>(workspace);
-    ArgmaxArgs a{logits, stride, vocab, softcap, logits_out, ids, tokens, token_stride, step,
+    ArgmaxArgs a{logits, stride, vocab, softcap, logits_out, ids, tokens, token_stride, step, pos,
                  reinterpret_cast<float*>(ws + l.part_v), reinterpret_cast<int*>(ws + l.part_i),
                  reinterpret_cast<int*>(ws + l.counters)};
     const dim3 grid((unsigned)l.blocks, rows);
@@ -904,6 +930,27 @@ int se12_step_logits_argmax(const void* logits, int32_t dtype, int64_t stride, i
     else
         hipLaunchKernelGGL(logits_argmax_kernel<SE12_STEP_BF16>, grid, dim3(kArgmaxThreads), 0, st, a);
     return step_launched();
+}
+
+}  // namespace
+
+extern "C" {
+
+int se12_step_logits_argmax(const void* logits, int32_t dtype, int64_t stride, int32_t rows, int32_t vocab, float softcap,
+                            uint16_t* logits_out, int64_t* ids, int64_t* tokens, int64_t token_stride,
+                            const int64_t* step, void* workspace, int64_t workspace_bytes, void* stream) {
+    // the kernel writes the step only when it is given pos
+    return launch_argmax("se12_step_logits_argmax", logits, dtype, stride, rows, vocab, softcap, logits_out, ids, tokens,
+                         token_stride, const_cast<int64_t*>(step), nullptr, workspace, workspace_bytes, stream);
+}
+
+int se12_step_logits_argmax_advance(const void* logits, int32_t dtype, int64_t stride, int32_t rows, int32_t vocab,
+                                    float softcap, uint16_t* logits_out, int64_t* ids, int64_t* tokens,
+                                    int64_t token_stride, int64_t* step, int64_t* pos, void* workspace,
+                                    int64_t workspace_bytes, void* stream) {
+    if (!pos) return step_fail("se12_step_logits_argmax_advance: NULL pos");
+    return launch_argmax("se12_step_logits_argmax_advance", logits, dtype, stride, rows, vocab, softcap, logits_out, ids,
+                         tokens, token_stride, step, pos, workspace, workspace_bytes, stream);
 }
 
 int se12_step_advance(int64_t* pos, int64_t* step, void* stream) {

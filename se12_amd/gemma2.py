@@ -411,10 +411,10 @@ class Gemma2Decoder:
                 ck(lib.se12_step_rmsnorm(nat.ptr(dn), dt(dn), dn.shape[1], nat.ptr(lw["post_ffw_norm"]),
                                          nat.ptr(self.x), nat.ptr(nxt), nat.ptr(self.h), B, s.hidden, s.eps, 0.0, 1, st))
         lg = self.be.logits_raw(self.h, self.logits_out)
-        ck(lib.se12_step_logits_argmax(nat.ptr(lg), dt(lg), lg.shape[1], B, s.vocab, s.final_softcap,
-                                       nat.ptr(self.last_logits), nat.ptr(self.ids), nat.ptr(self.tokens), self.max_len,
-                                       nat.ptr(self.step_index), nat.ptr(self.logits_ws), self.logits_ws.numel(), st))
-        ck(lib.se12_step_advance(nat.ptr(self.pos), nat.ptr(self.step_index), st))
+        ck(lib.se12_step_logits_argmax_advance(nat.ptr(lg), dt(lg), lg.shape[1], B, s.vocab, s.final_softcap,
+                                               nat.ptr(self.last_logits), nat.ptr(self.ids), nat.ptr(self.tokens),
+                                               self.max_len, nat.ptr(self.step_index), nat.ptr(self.pos),
+                                               nat.ptr(self.logits_ws), self.logits_ws.numel(), st))
 
     def _attention(self, li: int, q_ptr: int, k_ptr: int, v_ptr: int, dtype: int, q_stride: int, kv_stride: int) -> None:
         s = self.s

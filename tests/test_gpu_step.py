@@ -306,6 +306,40 @@ def test_bf16_rounding_of_fp32_inputs(gpu):
     assert 0 <= int(ids[0]) < vocab
 
 
+@pytest.mark.parametrize("rows,vocab", [(1, 256000), (3, 256000), (2, 1000)])
+def test_logits_argmax_advance_equals_argmax_then_advance(gpu, rows, vocab):
+    """The one-launch pick-and-advance gives the ids, tokens, logits, pos
+    and step of argmax followed by advance, on consecutive calls (its
+    counters return to zero), across rows and with a single block per row."""
+    max_len = 16
+    g = _gen(gpu, 31)
+    want, got = {}, {}
+    for name, res in (("two", want), ("one", got)):
+        ids = torch.full((rows,), -1, dtype=torch.int64, device=gpu)
+        tokens = torch.full((rows, max_len), -1, dtype=torch.int64, device=gpu)
+        out = torch.empty((rows, vocab), dtype=torch.bfloat16, device=gpu)
+        step = torch.tensor(3, dtype=torch.int64, device=gpu)
+        pos = torch.tensor(100, dtype=torch.int64, device=gpu)
+        ws = torch.zeros(nat.lib().se12_step_logits_workspace(rows, vocab), dtype=torch.uint8, device=gpu)
+        g.manual_seed(31)
+        for _ in range(4):
+            z = torch.randn((rows, vocab), generator=g, device=gpu) * 5
+            if name == "two":
+                _argmax(z, torch.float32, vocab, rows, vocab, 30.0, out, ids, tokens, max_len, step, ws)
+                nat.step_check(nat.lib().se12_step_advance(nat.ptr(pos), nat.ptr(step), nat.stream_ptr()))
+            else:
+                nat.step_check(nat.lib().se12_step_logits_argmax_advance(
+                    nat.ptr(z), nat.STEP_F32, vocab, rows, vocab, 30.0, nat.ptr(out), nat.ptr(ids), nat.ptr(tokens),
+                    max_len, nat.ptr(step), nat.ptr(pos), nat.ptr(ws), ws.numel(), nat.stream_ptr()))
+        torch.cuda.synchronize()
+        res.update(ids=ids.cpu(), tokens=tokens.cpu(), out=out.view(torch.int16).cpu(), step=int(step), pos=int(pos))
+        assert bool((ws[: 4 * (rows + 1)] == 0).all())
+    assert got["step"] == want["step"] == 7 and got["pos"] == want["pos"] == 104
+    assert torch.equal(got["ids"], want["ids"]) and torch.equal(got["tokens"], want["tokens"])
+    assert torch.equal(got["out"], want["out"])
+    assert int((got["tokens"] != -1).sum()) == 4 * rows and bool((got["tokens"][:, 3:7] != -1).all())
+
+
 def test_advance(gpu):
     pos = torch.tensor(41, dtype=torch.int64, device=gpu)
     step = torch.tensor(2, dtype=torch.int64, device=gpu)

@@ -272,3 +272,12 @@ def test_step_kernels_reject_invalid_arguments():
                                              2, 9000, 1e-6, 0.0, 0, s))
     with pytest.raises(nat.Se12Error, match="NULL"):
         nat.step_check(lib.se12_step_advance(None, nat.ptr(x), s))
+    with pytest.raises(nat.Se12Error, match="NULL pos"):
+        nat.step_check(lib.se12_step_logits_argmax_advance(nat.ptr(x), nat.STEP_BF16, 256000, 2, 256000, 0.0, None,
+                                                           nat.ptr(x), nat.ptr(x), 4, nat.ptr(x), None, aligned, ws, s))
+    with pytest.raises(nat.Se12Error, match="se12_step_logits_argmax_advance: workspace too small"):
+        nat.step_check(lib.se12_step_logits_argmax_advance(nat.ptr(x), nat.STEP_BF16, 256000, 2, 256000, 0.0, None,
+                                                           nat.ptr(x), nat.ptr(x), 4, nat.ptr(x), nat.ptr(x), aligned,
+                                                           ws - 1, s))
+    # the row-arrival counter after the per-row ones: 64 rows need a second 256-byte line
+    assert lib.se12_step_logits_workspace(64, 2048) == 512 + 256 + 256

@@ -340,6 +340,50 @@ def test_logits_argmax_advance_equals_argmax_then_advance(gpu, rows, vocab):
     assert int((got["tokens"] != -1).sum()) == 4 * rows and bool((got["tokens"][:, 3:7] != -1).all())
 
 
+def test_logits_argmax_advance_graph_replays(gpu):
+    """Captured in a HIP graph and replayed with new logits copied in
+    between (eager work and synchronisations between replays), every
+    replay picks the eager argmax, stores it at the current step and
+    advances pos and step by one."""
+    rows, vocab, max_len = 2, 256000, 8
+    g = _gen(gpu, 37)
+    z = torch.zeros((rows, vocab), device=gpu)
+    ids = torch.full((rows,), -1, dtype=torch.int64, device=gpu)
+    tokens = torch.full((rows, max_len), -1, dtype=torch.int64, device=gpu)
+    step = torch.tensor(1, dtype=torch.int64, device=gpu)
+    pos = torch.tensor(50, dtype=torch.int64, device=gpu)
+    ws = torch.zeros(nat.lib().se12_step_logits_workspace(rows, vocab), dtype=torch.uint8, device=gpu)
+
+    def pick():
+        nat.step_check(nat.lib().se12_step_logits_argmax_advance(
+            nat.ptr(z), nat.STEP_F32, vocab, rows, vocab, 0.0, None, nat.ptr(ids), nat.ptr(tokens), max_len,
+            nat.ptr(step), nat.ptr(pos), nat.ptr(ws), ws.numel(), nat.stream_ptr()))
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            pick()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert int(step) == 1 and int(pos) == 50      # capture launches nothing
+    want_tokens = []
+    for rep in range(4):
+        z.copy_(torch.randn((rows, vocab), generator=g, device=gpu) * 5)
+        zb = z.to(torch.bfloat16).float()
+        first = torch.arange(vocab, device=gpu).expand(rows, -1)
+        want = torch.where(zb == zb.max(dim=1, keepdim=True).values, first, vocab).min(dim=1).values
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ids, want), rep
+        assert int(step) == 2 + rep and int(pos) == 51 + rep
+        want_tokens.append(want)
+        assert torch.equal(tokens[:, 1:2 + rep], torch.stack(want_tokens, dim=1))
+        assert bool((ws[: 4 * (rows + 1)] == 0).all())
+
+
 def test_advance(gpu):
     pos = torch.tensor(41, dtype=torch.int64, device=gpu)
     step = torch.tensor(2, dtype=torch.int64, device=gpu)
